@@ -1,0 +1,165 @@
+/* include/knj_capi.h -- C ABI of the MI355X (gfx950) MoE decode library.
+ *
+ * Plain C: pointers, sizes, ints.  Device pointers are addresses in the GPU's
+ * memory (from knj_malloc, or any HIP allocation); `stream` is a hipStream_t
+ * passed as void* (NULL = the default stream).  Every function returns 0 on
+ * success or one of the KNJ_E_* codes below, with a message in knj_last_error().
+ *
+ * The status codes keep the reference's driver exit codes
+ * (/root/reference/tools/bench/q4k_moe_ffn.hip:63, tests/test_gemm_w4.hip:11-19):
+ * 5 correctness, 6 arch mismatch, 7 environment, 9 HIP error.
+ */
+#ifndef KNJ_CAPI_H
+#define KNJ_CAPI_H
+
+#include <stdint.h>
+
+#include "knj_model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KNJ_OK 0
+#define KNJ_E_CORRECTNESS 5
+#define KNJ_E_ARCH 6
+#define KNJ_E_ENV 7
+#define KNJ_E_HIP 9
+#define KNJ_E_ARG 22
+#define KNJ_E_STATE 23
+
+/* ------------------------------------------------------------ device gate
+ * Replaces the reference's C2 gate: Backend::create's arch guard and
+ * DeviceCaps probe (/root/reference/src/device/backend.cpp:54-62,
+ * src/device/device_caps.h:69-157).  The guard compares the device's
+ * gcnArchName up to the first ':' with the arch this library was compiled for
+ * ("gfx950"); if KNJ_BUILD_ARCH is set in the environment it must name the same
+ * arch.  Refusals return KNJ_E_ARCH (mismatch) and leave the device untouched. */
+typedef struct knj_device_caps {
+  char gcn_arch[32];      /* e.g. "gfx950" (the part before ':') */
+  char name[64];
+  int32_t wave_size;      /* 64 on CDNA */
+  int32_t cu_count;
+  int32_t clock_khz;
+  int32_t lds_per_block;  /* bytes */
+  int32_t l2_bytes;
+  int32_t arch_ok;
+  int32_t has_mfma_bf16;
+  int32_t has_mfma_i8;
+  int32_t has_fp8;
+  uint64_t vram_total;
+  uint64_t vram_free;
+} knj_device_caps;
+
+int knj_device_open(int device);
+int knj_device_close(void);
+int knj_device_caps_get(knj_device_caps* out);
+/* Arch guard alone, on strings (host-testable without a GPU): 0 when
+ * `device_arch` (full gcnArchName) matches `built_arch` and `env_arch` (may be
+ * NULL) agrees, else KNJ_E_ARCH. */
+int knj_check_arch(const char* device_arch, const char* built_arch, const char* env_arch);
+const char* knj_built_arch(void);
+const char* knj_last_error(void);
+
+/* ------------------------------------------------------------ memory */
+int knj_malloc(void** dptr, uint64_t bytes);
+int knj_free(void* dptr);
+int knj_memcpy_h2d(void* dst, const void* src, uint64_t bytes);
+int knj_memcpy_d2h(void* dst, const void* src, uint64_t bytes);
+int knj_memset_zero(void* dst, uint64_t bytes);
+int knj_synchronize(void);
+
+/* ------------------------------------------------------------ format / GEMV
+ * knj_dequant: n_weights of `type` at w -> f32, bit-exact with
+ *   dequant_row_f32 (/root/reference/src/loader/dequant.cpp:1114-1256).
+ * knj_gemv: y[j] = sum_i W[j][i] x[i] for the n_out rows of W, the device
+ *   counterpart of Model::matmul at m == 1 (/root/reference/src/model/model.cpp:
+ *   326-380) and dequant_dot_f32 (dequant.cpp:1075-1112).  `norm_w` (optional)
+ *   applies RMSNorm(x, norm_w, eps) to x first (model.cpp:240-271); `resid`
+ *   (optional) makes y = resid + W x (the residual adds at model.cpp:624, 652).
+ *   Types: Q4_K, Q6_K (rows of n_in/256 blocks), BF16, F32. */
+int knj_dequant(int type, const void* w, uint64_t n_weights, float* out, void* stream);
+int knj_gemv(int type, const void* w, int n_in, int n_out, const float* x, const float* norm_w,
+             float eps, const float* resid, float* y, void* stream);
+int knj_rmsnorm(const float* x, const float* w, int n, float eps, float* out, void* stream);
+
+/* ------------------------------------------------------------ MoE (config 1)
+ * knj_moe_router: logits = router_w . RMSNorm(x) (norm skipped when norm_w is
+ *   NULL), softmax over all experts, top-k by repeated argmax with ties to the
+ *   lower index, weights renormalised over the kept k (model.cpp:420-460).
+ *   hx receives the normalised input.  topk in selection order.
+ * knj_moe_decode_layer: the whole batch-1 MoE FFN: router as above, then for the
+ *   k chosen experts gate/up GEMV, silu(gate)*up, down GEMV, and
+ *   out = resid + sum_e w_e * down_e, summed in ascending expert index
+ *   (model.cpp:462-509, the moe-router/gate/up/act/down/scatter stages).
+ *   `resid` may be NULL (out is then the expert branch alone). */
+int knj_moe_router(const float* x, const float* norm_w, float eps, const float* router_w,
+                   int n_embd, int n_expert, int k, float* hx, float* logits, int32_t* topk_idx,
+                   float* topk_w, void* stream);
+int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const float* router_w,
+                         const void* gate, const void* up, const void* down, int type_gate_up,
+                         int type_down, int n_embd, int n_ff, int n_expert, int k,
+                         const float* resid, float* out, float* logits, int32_t* topk_idx,
+                         float* topk_w, void* stream);
+
+/* ------------------------------------------------------------ attention
+ * knj_qk_norm_rope_append: per-head RMSNorm of q and k with q_norm/k_norm,
+ *   NEOX RoPE at position `pos` (pairs (i, i+D/2), theta = pos*base^(-2i/D)),
+ *   q rewritten in place, k and v rounded to f16 and stored at slot `pos` of a
+ *   [n_head_kv][n_ctx][D] cache (model.cpp:567-584 with an f16 cache).
+ * knj_attention_decode: GQA decode attention of one query position over cache
+ *   slots [0, n_kv): scores q.k*scale, softmax, sum a*v (model.cpp:591-616). */
+int knj_qk_norm_rope_append(float* q, const float* k, const float* v, const float* q_norm,
+                            const float* k_norm, float eps, float rope_base, int pos, int n_head,
+                            int n_head_kv, int head_dim, int n_ctx, uint16_t* k_cache,
+                            uint16_t* v_cache, void* stream);
+int knj_attention_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
+                         int n_head, int n_head_kv, int head_dim, int n_ctx, int n_kv, float scale,
+                         float* out, void* stream);
+
+/* ------------------------------------------------------------ model step
+ * The device counterpart of knj::Model (/root/reference/src/model/model.h:55-80):
+ * open -> forward(tokens, n) -> logits of the last token, reset(), pos().
+ * Weights live in one device image laid out per include/knj_model.h.
+ * knj_model_create_synthetic generates the seeded synthetic weights on the GPU
+ * (include/knj_synth.h, bit-identical to the host generator);
+ * knj_model_create_from_image uploads a host image. */
+typedef struct knj_model knj_model;
+int knj_model_create_synthetic(const knj_model_config* cfg, uint64_t seed, knj_model** out);
+int knj_model_create_from_image(const knj_model_config* cfg, const void* image, uint64_t bytes,
+                                knj_model** out);
+int knj_model_free(knj_model* m);
+uint64_t knj_model_image_bytes(const knj_model* m);
+const void* knj_model_image_device(const knj_model* m);
+int knj_model_download_image(const knj_model* m, void* host, uint64_t bytes);
+int knj_model_reset(knj_model* m);
+int knj_model_pos(const knj_model* m);
+int knj_model_set_pos(knj_model* m, int pos);
+/* Runs n tokens one decode step each; logits_host (n_vocab floats, may be NULL)
+ * receives the last token's logits.  Errors: KNJ_E_ARG for token ids out of
+ * range or a full context (model.cpp:514-517, 533). */
+int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_host);
+/* Greedy decode entirely on the device: feeds `first`, then `steps` argmax
+ * tokens (first maximum wins, /root/reference/src/cli/main.cpp:126-132) into
+ * out_tokens.  Replays one captured HIP graph per step. */
+int knj_model_decode_greedy(knj_model* m, int32_t first, int steps, int32_t* out_tokens);
+/* Diagnostics of the most recent step: residual stream after layer il
+ * (model.cpp:654-658), router choice of layer il, last logits, KV caches. */
+int knj_model_hidden(const knj_model* m, int il, float* host_out);
+int knj_model_topk(const knj_model* m, int il, int32_t* idx_out, float* w_out);
+int knj_model_logits(const knj_model* m, float* host_out);
+int knj_model_kv_download(const knj_model* m, uint16_t* k_host, uint16_t* v_host);
+int knj_model_kv_upload(knj_model* m, const uint16_t* k_host, const uint16_t* v_host);
+/* Times `iters` greedy steps with HIP events on the model's stream (graph
+ * replays), returns total milliseconds. */
+int knj_model_time_decode(knj_model* m, int iters, float* ms_out);
+/* Times the expert GEMV pass (gate/up + down kernels of one layer) over
+ * `iters` launches, rotating through all layers so repeats come from HBM, not
+ * the last-level cache; returns the average microseconds per launch pair. */
+int knj_model_time_experts(knj_model* m, int iters, float* us_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KNJ_CAPI_H */

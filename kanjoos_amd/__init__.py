@@ -1,0 +1,378 @@
+"""kanjoos_amd -- MI355X (gfx950) batch-1 MoE decode path of Kanjoos.
+
+Python view of the C ABI in ``include/knj_capi.h`` (``libkanjoos_amd.so``,
+built in-tree by ``kanjoos_amd/build.py``).  The classes mirror the reference's
+host interfaces:
+
+* :class:`Model` -- ``knj::Model`` (/root/reference/src/model/model.h:55-80):
+  ``forward(tokens) -> logits`` of the last token, ``reset()``, ``pos``.
+* :func:`open_device` -- the C2 gate (``Backend::create``,
+  /root/reference/src/device/backend.cpp:54-62): refuses a non-gfx950 device.
+
+There is no CPU fallback: every call goes to the HIP library, and importing a
+missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkanjoos_amd.so")
+
+TYPE_F32, TYPE_F16, TYPE_Q4_K, TYPE_Q6_K, TYPE_BF16 = 0, 1, 12, 14, 30
+KNJ_OK, KNJ_E_CORRECTNESS, KNJ_E_ARCH, KNJ_E_ENV, KNJ_E_HIP, KNJ_E_ARG, KNJ_E_STATE = 0, 5, 6, 7, 9, 22, 23
+
+# every entry point include/knj_capi.h declares
+EXPORTS = (
+    "knj_device_open", "knj_device_close", "knj_device_caps_get", "knj_check_arch",
+    "knj_built_arch", "knj_last_error", "knj_malloc", "knj_free", "knj_memcpy_h2d",
+    "knj_memcpy_d2h", "knj_memset_zero", "knj_synchronize", "knj_dequant", "knj_gemv",
+    "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_qk_norm_rope_append",
+    "knj_attention_decode", "knj_model_create_synthetic", "knj_model_create_from_image",
+    "knj_model_free", "knj_model_image_bytes", "knj_model_image_device",
+    "knj_model_download_image", "knj_model_reset", "knj_model_pos", "knj_model_set_pos",
+    "knj_model_forward", "knj_model_decode_greedy", "knj_model_hidden", "knj_model_topk",
+    "knj_model_logits", "knj_model_kv_download", "knj_model_kv_upload",
+    "knj_model_time_decode", "knj_model_time_experts",
+)
+
+
+class KnjError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[knj {code}] {msg}")
+        self.code = code
+
+
+class ModelConfig(C.Structure):
+    """``knj_model_config`` (include/knj_model.h)."""
+
+    _fields_ = [
+        ("n_layer", C.c_int32), ("n_embd", C.c_int32), ("n_head", C.c_int32),
+        ("n_head_kv", C.c_int32), ("head_dim", C.c_int32), ("n_ff", C.c_int32),
+        ("n_expert", C.c_int32), ("n_expert_used", C.c_int32), ("n_vocab", C.c_int32),
+        ("n_ctx", C.c_int32), ("rms_eps", C.c_float), ("rope_base", C.c_float),
+        ("type_embd", C.c_int32), ("type_attn", C.c_int32), ("type_gate_up", C.c_int32),
+        ("type_down", C.c_int32), ("type_head", C.c_int32), ("init_std", C.c_float),
+    ]
+
+    def as_dict(self):
+        return {f: getattr(self, f) for f, _ in self._fields_}
+
+
+def qwen3_30b_a3b(**kw) -> ModelConfig:
+    """Qwen3-30B-A3B geometry: 48 layers, hidden 2048, 32/4 heads x 128, 128 experts
+    top-8 of width 768, vocab 151936, Q4_K attention and experts, bf16 embeddings
+    and LM head.  Any field can be overridden."""
+    base = dict(n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, head_dim=128, n_ff=768,
+                n_expert=128, n_expert_used=8, n_vocab=151936, n_ctx=4352, rms_eps=1e-6,
+                rope_base=1e6, type_embd=TYPE_BF16, type_attn=TYPE_Q4_K,
+                type_gate_up=TYPE_Q4_K, type_down=TYPE_Q4_K, type_head=TYPE_BF16,
+                init_std=0.02)
+    base.update(kw)
+    return ModelConfig(**base)
+
+
+class DeviceCaps(C.Structure):
+    _fields_ = [
+        ("gcn_arch", C.c_char * 32), ("name", C.c_char * 64), ("wave_size", C.c_int32),
+        ("cu_count", C.c_int32), ("clock_khz", C.c_int32), ("lds_per_block", C.c_int32),
+        ("l2_bytes", C.c_int32), ("arch_ok", C.c_int32), ("has_mfma_bf16", C.c_int32),
+        ("has_mfma_i8", C.c_int32), ("has_fp8", C.c_int32), ("vram_total", C.c_uint64),
+        ("vram_free", C.c_uint64),
+    ]
+
+
+_P = C.c_void_p
+_i = C.c_int
+_f = C.c_float
+_u64 = C.c_uint64
+_SIGS = {
+    "knj_device_open": (_i, [_i]),
+    "knj_device_close": (_i, []),
+    "knj_device_caps_get": (_i, [C.POINTER(DeviceCaps)]),
+    "knj_check_arch": (_i, [C.c_char_p, C.c_char_p, C.c_char_p]),
+    "knj_built_arch": (C.c_char_p, []),
+    "knj_last_error": (C.c_char_p, []),
+    "knj_malloc": (_i, [C.POINTER(_P), _u64]),
+    "knj_free": (_i, [_P]),
+    "knj_memcpy_h2d": (_i, [_P, _P, _u64]),
+    "knj_memcpy_d2h": (_i, [_P, _P, _u64]),
+    "knj_memset_zero": (_i, [_P, _u64]),
+    "knj_synchronize": (_i, []),
+    "knj_dequant": (_i, [_i, _P, _u64, _P, _P]),
+    "knj_gemv": (_i, [_i, _P, _i, _i, _P, _P, _f, _P, _P, _P]),
+    "knj_rmsnorm": (_i, [_P, _P, _i, _f, _P, _P]),
+    "knj_moe_router": (_i, [_P, _P, _f, _P, _i, _i, _i, _P, _P, _P, _P, _P]),
+    "knj_moe_decode_layer": (_i, [_P, _P, _f, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _P, _P,
+                                  _P, _P, _P, _P]),
+    "knj_qk_norm_rope_append": (_i, [_P, _P, _P, _P, _P, _f, _f, _i, _i, _i, _i, _i, _P, _P, _P]),
+    "knj_attention_decode": (_i, [_P, _P, _P, _i, _i, _i, _i, _i, _f, _P, _P]),
+    "knj_model_create_synthetic": (_i, [C.POINTER(ModelConfig), _u64, C.POINTER(_P)]),
+    "knj_model_create_from_image": (_i, [C.POINTER(ModelConfig), _P, _u64, C.POINTER(_P)]),
+    "knj_model_free": (_i, [_P]),
+    "knj_model_image_bytes": (_u64, [_P]),
+    "knj_model_image_device": (_P, [_P]),
+    "knj_model_download_image": (_i, [_P, _P, _u64]),
+    "knj_model_reset": (_i, [_P]),
+    "knj_model_pos": (_i, [_P]),
+    "knj_model_set_pos": (_i, [_P, _i]),
+    "knj_model_forward": (_i, [_P, _P, _i, _P]),
+    "knj_model_decode_greedy": (_i, [_P, C.c_int32, _i, _P]),
+    "knj_model_hidden": (_i, [_P, _i, _P]),
+    "knj_model_topk": (_i, [_P, _i, _P, _P]),
+    "knj_model_logits": (_i, [_P, _P]),
+    "knj_model_kv_download": (_i, [_P, _P, _P]),
+    "knj_model_kv_upload": (_i, [_P, _P, _P]),
+    "knj_model_time_decode": (_i, [_P, _i, C.POINTER(_f)]),
+    "knj_model_time_experts": (_i, [_P, _i, C.POINTER(_f)]),
+}
+
+_lib = None
+
+
+def lib():
+    """The HIP library.  Raises if it has not been built -- there is no fallback."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(f"{LIB_PATH} is missing: run `python -m kanjoos_amd.build` first")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != KNJ_OK:
+        raise KnjError(rc, lib().knj_last_error().decode())
+
+
+def _ptr(a: np.ndarray):
+    return a.ctypes.data_as(C.c_void_p)
+
+
+def row_bytes(type_id: int, n: int) -> int:
+    if type_id == TYPE_F32:
+        return 4 * n
+    if type_id in (TYPE_F16, TYPE_BF16):
+        return 2 * n
+    if type_id == TYPE_Q4_K:
+        return n // 256 * 144
+    if type_id == TYPE_Q6_K:
+        return n // 256 * 210
+    raise ValueError(type_id)
+
+
+# ------------------------------------------------------------------ device
+
+def open_device(device: int = 0) -> DeviceCaps:
+    """Arch-guarded open of `device`; returns its probed capabilities."""
+    check(lib().knj_device_open(device))
+    caps = DeviceCaps()
+    check(lib().knj_device_caps_get(C.byref(caps)))
+    return caps
+
+
+def close_device() -> None:
+    check(lib().knj_device_close())
+
+
+def synchronize() -> None:
+    check(lib().knj_synchronize())
+
+
+class DeviceBuffer:
+    """A device allocation of `nbytes` (HIP memory owned by this object)."""
+
+    def __init__(self, nbytes: int):
+        self.nbytes = int(nbytes)
+        p = _P()
+        check(lib().knj_malloc(C.byref(p), self.nbytes))
+        self.ptr = p.value
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        check(lib().knj_memcpy_h2d(self.ptr, _ptr(a), a.nbytes))
+
+    def download(self, dtype, count: int | None = None) -> np.ndarray:
+        dt = np.dtype(dtype)
+        n = self.nbytes // dt.itemsize if count is None else count
+        out = np.empty(n, dtype=dt)
+        check(lib().knj_memcpy_d2h(_ptr(out), self.ptr, out.nbytes))
+        return out
+
+    def zero(self) -> None:
+        check(lib().knj_memset_zero(self.ptr, self.nbytes))
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().knj_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _p(b):
+    return None if b is None else (b.ptr if isinstance(b, DeviceBuffer) else b)
+
+
+# ------------------------------------------------------------------ primitives
+
+def dequant(type_id: int, w: DeviceBuffer, n: int, out: DeviceBuffer) -> None:
+    check(lib().knj_dequant(type_id, _p(w), n, _p(out), None))
+
+
+def gemv(type_id: int, w, n_in: int, n_out: int, x, y, norm_w=None, eps: float = 1e-6,
+         resid=None) -> None:
+    check(lib().knj_gemv(type_id, _p(w), n_in, n_out, _p(x), _p(norm_w), eps, _p(resid), _p(y), None))
+
+
+def moe_router(x, router_w, n_embd, n_expert, k, hx, logits, topk_idx, topk_w, norm_w=None,
+               eps: float = 1e-6) -> None:
+    check(lib().knj_moe_router(_p(x), _p(norm_w), eps, _p(router_w), n_embd, n_expert, k, _p(hx),
+                               _p(logits), _p(topk_idx), _p(topk_w), None))
+
+
+def moe_decode_layer(x, router_w, gate, up, down, n_embd, n_ff, n_expert, k, out, logits,
+                     topk_idx, topk_w, norm_w=None, eps: float = 1e-6, resid=None,
+                     type_gate_up: int = TYPE_Q4_K, type_down: int = TYPE_Q4_K) -> None:
+    check(lib().knj_moe_decode_layer(_p(x), _p(norm_w), eps, _p(router_w), _p(gate), _p(up),
+                                     _p(down), type_gate_up, type_down, n_embd, n_ff, n_expert, k,
+                                     _p(resid), _p(out), _p(logits), _p(topk_idx), _p(topk_w), None))
+
+
+def qk_norm_rope_append(q, k, v, q_norm, k_norm, eps, rope_base, pos, n_head, n_head_kv,
+                        head_dim, n_ctx, k_cache, v_cache) -> None:
+    check(lib().knj_qk_norm_rope_append(_p(q), _p(k), _p(v), _p(q_norm), _p(k_norm), eps,
+                                        rope_base, pos, n_head, n_head_kv, head_dim, n_ctx,
+                                        _p(k_cache), _p(v_cache), None))
+
+
+def attention_decode(q, k_cache, v_cache, n_head, n_head_kv, head_dim, n_ctx, n_kv, scale, out) -> None:
+    check(lib().knj_attention_decode(_p(q), _p(k_cache), _p(v_cache), n_head, n_head_kv, head_dim,
+                                     n_ctx, n_kv, scale, _p(out), None))
+
+
+# ------------------------------------------------------------------ model
+
+class Model:
+    """The device decode step, shaped like the reference's ``knj::Model``."""
+
+    def __init__(self, handle, cfg: ModelConfig):
+        self.h = handle
+        self.cfg = cfg
+
+    @classmethod
+    def synthetic(cls, cfg: ModelConfig, seed: int = 0) -> "Model":
+        h = _P()
+        check(lib().knj_model_create_synthetic(C.byref(cfg), seed, C.byref(h)))
+        return cls(h.value, cfg)
+
+    @classmethod
+    def from_image(cls, cfg: ModelConfig, image: np.ndarray) -> "Model":
+        image = np.ascontiguousarray(image, dtype=np.uint8)
+        h = _P()
+        check(lib().knj_model_create_from_image(C.byref(cfg), _ptr(image), image.nbytes, C.byref(h)))
+        return cls(h.value, cfg)
+
+    def close(self) -> None:
+        if self.h:
+            lib().knj_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def pos(self) -> int:
+        return lib().knj_model_pos(self.h)
+
+    def set_pos(self, pos: int) -> None:
+        check(lib().knj_model_set_pos(self.h, pos))
+
+    def reset(self) -> None:
+        check(lib().knj_model_reset(self.h))
+
+    def image_bytes(self) -> int:
+        return lib().knj_model_image_bytes(self.h)
+
+    def download_image(self) -> np.ndarray:
+        n = self.image_bytes()
+        out = np.empty(n, dtype=np.uint8)
+        check(lib().knj_model_download_image(self.h, _ptr(out), n))
+        return out
+
+    def forward(self, tokens, want_logits: bool = True):
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+        logits = np.empty(self.cfg.n_vocab, dtype=np.float32) if want_logits else None
+        check(lib().knj_model_forward(self.h, _ptr(t), t.size,
+                                      _ptr(logits) if logits is not None else None))
+        return logits
+
+    def decode_greedy(self, first: int, steps: int) -> np.ndarray:
+        out = np.empty(steps, dtype=np.int32)
+        check(lib().knj_model_decode_greedy(self.h, int(first), steps, _ptr(out)))
+        return out
+
+    def hidden(self, il: int) -> np.ndarray:
+        out = np.empty(self.cfg.n_embd, dtype=np.float32)
+        check(lib().knj_model_hidden(self.h, il, _ptr(out)))
+        return out
+
+    def topk(self, il: int):
+        k = self.cfg.n_expert_used
+        i = np.empty(k, dtype=np.int32)
+        w = np.empty(k, dtype=np.float32)
+        check(lib().knj_model_topk(self.h, il, _ptr(i), _ptr(w)))
+        return i, w
+
+    def logits(self) -> np.ndarray:
+        out = np.empty(self.cfg.n_vocab, dtype=np.float32)
+        check(lib().knj_model_logits(self.h, _ptr(out)))
+        return out
+
+    def kv_shape(self):
+        c = self.cfg
+        return (c.n_layer, c.n_head_kv, c.n_ctx, c.head_dim)
+
+    def kv_download(self):
+        k = np.empty(self.kv_shape(), dtype=np.uint16)
+        v = np.empty(self.kv_shape(), dtype=np.uint16)
+        check(lib().knj_model_kv_download(self.h, _ptr(k), _ptr(v)))
+        return k, v
+
+    def kv_upload(self, k: np.ndarray, v: np.ndarray) -> None:
+        k = np.ascontiguousarray(k, dtype=np.uint16)
+        v = np.ascontiguousarray(v, dtype=np.uint16)
+        check(lib().knj_model_kv_upload(self.h, _ptr(k), _ptr(v)))
+
+    def time_decode(self, iters: int) -> float:
+        ms = C.c_float()
+        check(lib().knj_model_time_decode(self.h, iters, C.byref(ms)))
+        return ms.value
+
+    def time_experts(self, iters: int) -> float:
+        us = C.c_float()
+        check(lib().knj_model_time_experts(self.h, iters, C.byref(us)))
+        return us.value

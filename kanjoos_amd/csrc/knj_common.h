@@ -1,0 +1,129 @@
+// kanjoos_amd/csrc/knj_common.h -- internal helpers shared by the HIP sources.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../../include/knj_capi.h"
+#include "../../include/knj_format.h"
+
+namespace knj {
+
+// Last error text for knj_last_error(); thread-local so callers on different
+// threads do not see each other's messages.
+void set_error(const std::string& msg);
+
+// Returns KNJ_E_HIP and records the HIP error text when `e` is not hipSuccess.
+int hip_fail(hipError_t e, const char* what);
+
+#define KNJ_HIP(call)                                   \
+  do {                                                  \
+    hipError_t e_ = (call);                             \
+    if (e_ != hipSuccess) return knj::hip_fail(e_, #call); \
+  } while (0)
+
+#define KNJ_CHECK_ARG(cond, msg)        \
+  do {                                  \
+    if (!(cond)) {                      \
+      knj::set_error(msg);              \
+      return KNJ_E_ARG;                 \
+    }                                   \
+  } while (0)
+
+// Refuses launches before knj_device_open() has passed the arch guard.
+int require_open();
+
+// Per-device scratch owned by the library (partials, counters); grown on
+// demand, never shrunk, released at knj_device_close().
+void* device_scratch(uint64_t bytes, hipStream_t stream);
+
+// 1024 zero-initialised device counters (tickets of last-workgroup-done
+// reductions); every kernel that takes one returns it to zero before exiting.
+unsigned int* device_counters();
+
+// ---------------------------------------------------------------- kernels
+// Launchers return hipError_t of the launch; shapes are validated by callers.
+struct GemvArgs {
+  int type;                 // KNJ_TYPE_Q4_K / Q6_K / BF16 / F32
+  const uint8_t* w;         // n_out rows of n_in weights
+  int n_in, n_out;
+  const float* x;           // input vector (n_in)
+  const float* norm_w;      // optional: RMSNorm weight applied to x first
+  float eps;
+  const float* resid;       // optional: y = resid + W x
+  float* y;                 // output (n_out)
+  unsigned long long* argmax_key;  // optional: packed (value, index) maximum of y
+};
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
+
+hipError_t launch_dequant(int type, const uint8_t* w, uint64_t n, float* out, hipStream_t s);
+
+hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* out, hipStream_t s);
+
+struct RouterArgs {
+  const float* x;         // residual stream (n_embd)
+  const float* norm_w;    // optional RMSNorm weight (ffn_norm)
+  float eps;
+  const float* router_w;  // [n_expert][n_embd] f32
+  int n_embd, n_expert, k;
+  float* hx;              // normalised x written for the expert kernels
+  float* logits;          // [n_expert]
+  int32_t* topk_idx;      // [k], selection order
+  float* topk_w;          // [k]
+  unsigned int* counter;  // zero-initialised ticket, left at zero on exit
+};
+hipError_t launch_router(const RouterArgs& a, hipStream_t s);
+
+struct ExpertArgs {
+  const float* hx;        // [n_embd] normalised input
+  const int32_t* topk_idx;
+  const float* topk_w;
+  const uint8_t* gate;    // [n_expert] slabs
+  const uint8_t* up;
+  const uint8_t* down;
+  int type_gate_up, type_down;
+  int n_embd, n_ff, n_expert, k;
+  float* act;             // [k][n_ff] scratch
+  const float* resid;     // optional residual added to the output
+  float* out;             // [n_embd]
+  float* hidden_copy;     // optional second destination of out
+};
+hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
+
+struct QkRopeArgs {
+  float* q;               // [n_head][D] in place
+  const float* k;         // [n_head_kv][D]
+  const float* v;         // [n_head_kv][D]
+  const float* q_norm;    // [D]
+  const float* k_norm;    // [D]
+  float eps;
+  const float* rope_cos;  // [n_ctx][D/2]
+  const float* rope_sin;
+  const int* pos;         // device position (write slot)
+  uint16_t* k_cache;      // [n_head_kv][n_ctx][D] of this layer
+  uint16_t* v_cache;
+  int n_head, n_head_kv, head_dim, n_ctx;
+};
+hipError_t launch_qk_rope_append(const QkRopeArgs& a, hipStream_t s);
+
+struct AttnArgs {
+  const float* q;            // [n_head][D]
+  const uint16_t* k_cache;   // [n_head_kv][n_ctx][D]
+  const uint16_t* v_cache;
+  const int* n_kv_dev;       // device count of valid positions = *n_kv_dev + n_kv_add
+  int n_kv_add;
+  int n_kv_host;             // used when n_kv_dev is null
+  int n_head, n_head_kv, head_dim, n_ctx;
+  float scale;
+  float* partial;            // [n_head][n_split][D + 2] scratch
+  float* out;                // [n_head][D]
+};
+int attn_splits(int n_ctx);
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
+
+hipError_t launch_embed(int type, const uint8_t* table, int n_embd, const int32_t* tok, float* x,
+                        hipStream_t s);
+
+}  // namespace knj

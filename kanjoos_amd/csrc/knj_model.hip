@@ -1,0 +1,552 @@
+// kanjoos_amd/csrc/knj_model.hip -- the device decode step behind knj_model_*.
+//
+// One model = one weight image in HBM (layout of include/knj_model.h), an f16
+// KV cache, and a fixed set of activation buffers.  A decode step reads the
+// token and the position from device memory, so the whole step is captured
+// once as a HIP graph and replayed: greedy decode never returns to the host
+// between tokens.
+//
+// Step (per token):  embed -> 48 x [ qkv GEMV (attn RMSNorm fused) ->
+//   q/k norm + RoPE + f16 KV append -> split-KV attention -> merge ->
+//   o GEMV + residual -> router (ffn RMSNorm fused, softmax, top-k) ->
+//   gate/up GEMV + SwiGLU -> down GEMV + weighted sum + residual ]
+//   -> LM head GEMV (final RMSNorm fused) with argmax -> step end.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <memory>
+#include <vector>
+
+#include "../../include/knj_synth.h"
+#include "knj_common.h"
+
+namespace knj {
+namespace {
+
+// ----------------------------------------------------------- synthetic weights
+
+// One thread per quantised block: 256 draws, then the block quantiser.
+__global__ void k_synth_quant(uint64_t seed, int layer, int kind, int type, uint64_t n_in,
+                              uint64_t rows_per_expert, int n_expert, int expert_base,
+                              float stddev, uint8_t* __restrict__ out) {
+  const uint64_t nb_row = n_in / KNJ_QK;
+  const uint64_t per_expert = rows_per_expert * nb_row;
+  const uint64_t total = per_expert * (uint64_t)n_expert;
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const uint64_t e = i / per_expert, b = i % per_expert;
+  const int expert = expert_base < 0 ? -1 : expert_base + (int)e;
+  const uint64_t key = knj_tensor_key(seed, layer, kind, expert);
+  float tmp[KNJ_QK];
+  const uint64_t bb = knj_row_bytes(type, KNJ_QK);
+  knj_synth_quant_block(key, type, n_in, b, stddev, tmp, out + i * bb);
+}
+
+__global__ void k_synth_plain(uint64_t key, int type, uint64_t n, float stddev,
+                              uint8_t* __restrict__ out) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float v = knj_synth_value(key, i, stddev);
+  if (type == KNJ_TYPE_F32) reinterpret_cast<float*>(out)[i] = v;
+  else if (type == KNJ_TYPE_BF16) reinterpret_cast<uint16_t*>(out)[i] = knj_f32_to_bf16(v);
+  else reinterpret_cast<uint16_t*>(out)[i] = knj_f32_to_f16(v);
+}
+
+__global__ void k_fill_ones(float* p, uint64_t n) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 1.0f;
+}
+
+// ----------------------------------------------------------- step bookkeeping
+
+struct StepState {
+  int32_t token;              // token fed to the next step
+  int32_t pos;                // position of the next step
+  int32_t step;               // index into out_tokens
+  int32_t pad;
+  unsigned long long key;     // packed argmax of the LM head
+};
+
+__global__ void k_step_begin(StepState* st) { st->key = 0ull; }
+
+__global__ void k_step_end(StepState* st, int32_t* out_tokens, int max_steps) {
+  const int32_t tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(st->key & 0xFFFFFFFFull));
+  if (st->step < max_steps) out_tokens[st->step] = tok;
+  st->step += 1;
+  st->token = tok;
+  st->pos += 1;
+}
+
+}  // namespace
+}  // namespace knj
+
+using namespace knj;
+
+struct knj_model {
+  knj_model_config c{};
+  uint8_t* image = nullptr;
+  uint64_t image_bytes = 0;
+  std::vector<knj_layer_offsets> lo;
+  uint64_t off_embd = 0, off_onorm = 0, off_head = 0;
+  hipStream_t stream = nullptr;
+  // activations
+  float *x = nullptr, *qkv = nullptr, *ctx = nullptr, *hx = nullptr, *act = nullptr;
+  float *logits = nullptr, *router_logits = nullptr, *hidden = nullptr, *topk_w = nullptr;
+  int32_t* topk_idx = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr, *attn_part = nullptr;
+  uint16_t *kv_k = nullptr, *kv_v = nullptr;
+  StepState* st = nullptr;
+  int32_t* out_tokens = nullptr;
+  int max_steps = 0;
+  unsigned int* counter = nullptr;
+  int pos = 0;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  std::vector<void*> owned;
+};
+
+namespace {
+
+int alloc(knj_model* m, void** p, uint64_t bytes) {
+  KNJ_HIP(hipMalloc(p, std::max<uint64_t>(bytes, 256)));
+  m->owned.push_back(*p);
+  return KNJ_OK;
+}
+
+int validate(const knj_model_config* c) {
+  KNJ_CHECK_ARG(c, "null config");
+  KNJ_CHECK_ARG(c->n_layer > 0 && c->n_embd > 0 && c->n_vocab > 0, "empty model");
+  KNJ_CHECK_ARG(c->n_embd % 256 == 0 && c->n_embd <= 16384, "n_embd must be a multiple of 256, <= 16384");
+  KNJ_CHECK_ARG(c->head_dim > 0 && c->head_dim <= 128 && c->head_dim % 8 == 0,
+                "head_dim must be a multiple of 8, <= 128");
+  KNJ_CHECK_ARG(c->n_head_kv > 0 && c->n_head % c->n_head_kv == 0 && c->n_head / c->n_head_kv <= 8,
+                "n_head must be a multiple of n_head_kv with a group of at most 8");
+  KNJ_CHECK_ARG(((int64_t)c->n_head * c->head_dim) % 256 == 0, "q_dim must be a multiple of 256");
+  KNJ_CHECK_ARG(c->n_ff > 0 && c->n_ff % 256 == 0, "n_ff must be a multiple of 256");
+  KNJ_CHECK_ARG(c->n_expert > 0 && c->n_expert <= 256, "n_expert must be in [1, 256]");
+  KNJ_CHECK_ARG(c->n_expert_used > 0 && c->n_expert_used <= 16 && c->n_expert_used <= c->n_expert,
+                "n_expert_used must be in [1, min(16, n_expert)]");
+  KNJ_CHECK_ARG(c->n_ctx > 0, "n_ctx must be positive");
+  KNJ_CHECK_ARG(c->type_embd == KNJ_TYPE_BF16 || c->type_embd == KNJ_TYPE_F32, "embeddings must be BF16 or F32");
+  KNJ_CHECK_ARG(c->type_attn == KNJ_TYPE_Q4_K || c->type_attn == KNJ_TYPE_Q6_K, "attention weights must be Q4_K or Q6_K");
+  KNJ_CHECK_ARG(c->type_gate_up == KNJ_TYPE_Q4_K, "expert gate/up must be Q4_K");
+  KNJ_CHECK_ARG(c->type_down == KNJ_TYPE_Q4_K || c->type_down == KNJ_TYPE_Q6_K, "expert down must be Q4_K or Q6_K");
+  KNJ_CHECK_ARG(c->type_head == KNJ_TYPE_BF16 || c->type_head == KNJ_TYPE_Q6_K || c->type_head == KNJ_TYPE_Q4_K,
+                "LM head must be BF16, Q4_K or Q6_K");
+  const uint64_t lds_down = ((uint64_t)c->n_expert_used * c->n_ff * 4) + (uint64_t)c->n_expert_used * (c->n_ff / 32) * 4 +
+                            (uint64_t)c->n_expert_used * 8 * 4;
+  KNJ_CHECK_ARG(lds_down <= 160 * 1024, "n_expert_used * n_ff too large for LDS staging");
+  return KNJ_OK;
+}
+
+int setup(knj_model* m) {
+  const knj_model_config& c = m->c;
+  m->image_bytes = knj_model_layout(&c, 0, nullptr, &m->off_embd, &m->off_onorm, &m->off_head);
+  m->lo.resize((size_t)c.n_layer);
+  for (int il = 0; il < c.n_layer; ++il) knj_model_layout(&c, il, &m->lo[il], nullptr, nullptr, nullptr);
+  KNJ_HIP(hipStreamCreateWithFlags(&m->stream, hipStreamNonBlocking));
+  int rc;
+  const uint64_t H = c.n_embd, QD = (uint64_t)c.n_head * c.head_dim, KVD = (uint64_t)c.n_head_kv * c.head_dim;
+  if ((rc = alloc(m, (void**)&m->image, m->image_bytes))) return rc;
+  if ((rc = alloc(m, (void**)&m->x, H * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->qkv, (QD + 2 * KVD) * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->ctx, QD * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->hx, H * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->act, (uint64_t)c.n_expert_used * c.n_ff * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->logits, (uint64_t)c.n_vocab * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->router_logits, (uint64_t)c.n_layer * c.n_expert * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->hidden, (uint64_t)c.n_layer * H * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->topk_idx, (uint64_t)c.n_layer * c.n_expert_used * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->topk_w, (uint64_t)c.n_layer * c.n_expert_used * 4))) return rc;
+  const int half = c.head_dim / 2;
+  if ((rc = alloc(m, (void**)&m->rope_cos, (uint64_t)c.n_ctx * half * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->rope_sin, (uint64_t)c.n_ctx * half * 4))) return rc;
+  const int n_split = attn_splits(c.n_ctx);
+  if ((rc = alloc(m, (void**)&m->attn_part, (uint64_t)c.n_head * n_split * (c.head_dim + 2) * 4))) return rc;
+  const uint64_t kv = knj_kv_elems(&c);
+  if ((rc = alloc(m, (void**)&m->kv_k, kv * 2))) return rc;
+  if ((rc = alloc(m, (void**)&m->kv_v, kv * 2))) return rc;
+  if ((rc = alloc(m, (void**)&m->st, sizeof(StepState)))) return rc;
+  m->max_steps = std::max(c.n_ctx, 1);
+  if ((rc = alloc(m, (void**)&m->out_tokens, (uint64_t)m->max_steps * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->counter, 256))) return rc;
+  KNJ_HIP(hipMemset(m->counter, 0, 256));
+  KNJ_HIP(hipMemset(m->kv_k, 0, kv * 2));
+  KNJ_HIP(hipMemset(m->kv_v, 0, kv * 2));
+  KNJ_HIP(hipMemset(m->st, 0, sizeof(StepState)));
+  // RoPE table: theta = pos * base^(-2i/D) in f32, cos/sin in f32 on the host,
+  // the expressions of model.cpp:227-230 and :278-279
+  std::vector<float> inv(half), tc((size_t)c.n_ctx * half), ts((size_t)c.n_ctx * half);
+  for (int i = 0; i < half; ++i) inv[i] = std::pow(c.rope_base, -2.0f * (float)i / (float)c.head_dim);
+  for (int p = 0; p < c.n_ctx; ++p)
+    for (int i = 0; i < half; ++i) {
+      const float th = (float)p * inv[i];
+      tc[(size_t)p * half + i] = std::cos(th);
+      ts[(size_t)p * half + i] = std::sin(th);
+    }
+  KNJ_HIP(hipMemcpy(m->rope_cos, tc.data(), tc.size() * 4, hipMemcpyHostToDevice));
+  KNJ_HIP(hipMemcpy(m->rope_sin, ts.data(), ts.size() * 4, hipMemcpyHostToDevice));
+  return KNJ_OK;
+}
+
+int synth_quant(knj_model* m, uint64_t seed, int layer, int kind, int type, uint64_t n_in,
+                uint64_t rows, int n_expert, int expert_base, uint8_t* dst) {
+  const uint64_t total = rows * (n_in / KNJ_QK) * (uint64_t)n_expert;
+  const unsigned grid = (unsigned)((total + 127) / 128);
+  hipLaunchKernelGGL(k_synth_quant, dim3(grid), dim3(128), 0, m->stream, seed, layer, kind, type,
+                     n_in, rows, n_expert, expert_base, m->c.init_std, dst);
+  KNJ_HIP(hipGetLastError());
+  return KNJ_OK;
+}
+
+int synth_plain(knj_model* m, uint64_t key, int type, uint64_t n, uint8_t* dst) {
+  const unsigned grid = (unsigned)((n + 255) / 256);
+  hipLaunchKernelGGL(k_synth_plain, dim3(grid), dim3(256), 0, m->stream, key, type, n,
+                     m->c.init_std, dst);
+  KNJ_HIP(hipGetLastError());
+  return KNJ_OK;
+}
+
+int ones(knj_model* m, uint64_t off, uint64_t n) {
+  hipLaunchKernelGGL(k_fill_ones, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, m->stream,
+                     reinterpret_cast<float*>(m->image + off), n);
+  KNJ_HIP(hipGetLastError());
+  return KNJ_OK;
+}
+
+// Same tensor keys and element order as the host generator (oracle synth_model).
+int synth_all(knj_model* m, uint64_t seed) {
+  const knj_model_config& c = m->c;
+  const uint64_t H = c.n_embd, QD = (uint64_t)c.n_head * c.head_dim, KVD = (uint64_t)c.n_head_kv * c.head_dim;
+  const uint64_t F = c.n_ff, V = c.n_vocab;
+  int rc;
+  auto tensor = [&](int layer, int kind, int type, uint64_t n_in, uint64_t rows, uint8_t* dst) {
+    if (type == KNJ_TYPE_Q4_K || type == KNJ_TYPE_Q6_K)
+      return synth_quant(m, seed, layer, kind, type, n_in, rows, 1, -1, dst);
+    return synth_plain(m, knj_tensor_key(seed, layer, kind, -1), type, n_in * rows, dst);
+  };
+  if ((rc = tensor(-1, KNJ_T_EMBD, c.type_embd, H, V, m->image + m->off_embd))) return rc;
+  for (int il = 0; il < c.n_layer; ++il) {
+    const knj_layer_offsets& lo = m->lo[il];
+    if ((rc = ones(m, lo.attn_norm, H))) return rc;
+    if ((rc = ones(m, lo.ffn_norm, H))) return rc;
+    if ((rc = ones(m, lo.q_norm, (uint64_t)c.head_dim))) return rc;
+    if ((rc = ones(m, lo.k_norm, (uint64_t)c.head_dim))) return rc;
+    const uint64_t rb = knj_row_bytes(c.type_attn, H);
+    uint8_t* wqkv = m->image + lo.wqkv;
+    if ((rc = tensor(il, KNJ_T_Q, c.type_attn, H, QD, wqkv))) return rc;
+    if ((rc = tensor(il, KNJ_T_K, c.type_attn, H, KVD, wqkv + rb * QD))) return rc;
+    if ((rc = tensor(il, KNJ_T_V, c.type_attn, H, KVD, wqkv + rb * (QD + KVD)))) return rc;
+    if ((rc = tensor(il, KNJ_T_O, c.type_attn, QD, H, m->image + lo.wo))) return rc;
+    if ((rc = tensor(il, KNJ_T_ROUTER, KNJ_TYPE_F32, H, (uint64_t)c.n_expert, m->image + lo.router))) return rc;
+    if ((rc = synth_quant(m, seed, il, KNJ_T_GATE, c.type_gate_up, H, F, c.n_expert, 0, m->image + lo.gate))) return rc;
+    if ((rc = synth_quant(m, seed, il, KNJ_T_UP, c.type_gate_up, H, F, c.n_expert, 0, m->image + lo.up))) return rc;
+    if ((rc = synth_quant(m, seed, il, KNJ_T_DOWN, c.type_down, F, H, c.n_expert, 0, m->image + lo.down))) return rc;
+  }
+  if ((rc = ones(m, m->off_onorm, H))) return rc;
+  if ((rc = tensor(-1, KNJ_T_HEAD, c.type_head, H, V, m->image + m->off_head))) return rc;
+  KNJ_HIP(hipStreamSynchronize(m->stream));
+  return KNJ_OK;
+}
+
+// The per-layer launches.  `layer_out` receives the residual after the layer.
+int enqueue_layer(knj_model* m, int il, hipStream_t s) {
+  const knj_model_config& c = m->c;
+  const knj_layer_offsets& lo = m->lo[il];
+  const int H = c.n_embd, D = c.head_dim, QD = c.n_head * D, KVD = c.n_head_kv * D;
+  const uint8_t* img = m->image;
+  GemvArgs qkv{c.type_attn, img + lo.wqkv, H, QD + 2 * KVD, m->x,
+               reinterpret_cast<const float*>(img + lo.attn_norm), c.rms_eps, nullptr, m->qkv, nullptr};
+  KNJ_HIP(launch_gemv(qkv, s));
+  const uint64_t kv_layer = (uint64_t)il * c.n_head_kv * c.n_ctx * D;
+  QkRopeArgs qr{m->qkv, m->qkv + QD, m->qkv + QD + KVD,
+                reinterpret_cast<const float*>(img + lo.q_norm),
+                reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos, m->rope_sin,
+                &m->st->pos, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head, c.n_head_kv, D, c.n_ctx};
+  KNJ_HIP(launch_qk_rope_append(qr, s));
+  AttnArgs at{m->qkv, m->kv_k + kv_layer, m->kv_v + kv_layer, &m->st->pos, 1, 0, c.n_head, c.n_head_kv,
+              D, c.n_ctx, 1.0f / std::sqrt((float)D), m->attn_part, m->ctx};
+  KNJ_HIP(launch_attention(at, s));
+  GemvArgs o{c.type_attn, img + lo.wo, QD, H, m->ctx, nullptr, 0.0f, m->x, m->x, nullptr};
+  KNJ_HIP(launch_gemv(o, s));
+  RouterArgs ra{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
+                reinterpret_cast<const float*>(img + lo.router), H, c.n_expert, c.n_expert_used,
+                m->hx, m->router_logits + (uint64_t)il * c.n_expert,
+                m->topk_idx + (uint64_t)il * c.n_expert_used, m->topk_w + (uint64_t)il * c.n_expert_used,
+                m->counter};
+  KNJ_HIP(launch_router(ra, s));
+  ExpertArgs ea{m->hx, m->topk_idx + (uint64_t)il * c.n_expert_used,
+                m->topk_w + (uint64_t)il * c.n_expert_used, img + lo.gate, img + lo.up, img + lo.down,
+                c.type_gate_up, c.type_down, H, c.n_ff, c.n_expert, c.n_expert_used, m->act, m->x,
+                m->x, m->hidden + (uint64_t)il * H};
+  KNJ_HIP(launch_experts(ea, s));
+  return KNJ_OK;
+}
+
+int enqueue_step(knj_model* m, hipStream_t s) {
+  const knj_model_config& c = m->c;
+  hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(1), 0, s, m->st);
+  KNJ_HIP(hipGetLastError());
+  KNJ_HIP(launch_embed(c.type_embd, m->image + m->off_embd, c.n_embd, &m->st->token, m->x, s));
+  for (int il = 0; il < c.n_layer; ++il) {
+    int rc = enqueue_layer(m, il, s);
+    if (rc) return rc;
+  }
+  GemvArgs head{c.type_head, m->image + m->off_head, c.n_embd, c.n_vocab, m->x,
+                reinterpret_cast<const float*>(m->image + m->off_onorm), c.rms_eps, nullptr,
+                m->logits, &m->st->key};
+  if (c.type_head == KNJ_TYPE_Q4_K) {
+    set_error("a Q4_K LM head has no fused argmax; use BF16 or Q6_K");
+    return KNJ_E_ARG;
+  }
+  KNJ_HIP(launch_gemv(head, s));
+  hipLaunchKernelGGL(k_step_end, dim3(1), dim3(1), 0, s, m->st, m->out_tokens, m->max_steps);
+  KNJ_HIP(hipGetLastError());
+  return KNJ_OK;
+}
+
+int ensure_graph(knj_model* m) {
+  if (m->exec) return KNJ_OK;
+  KNJ_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
+  const int rc = enqueue_step(m, m->stream);
+  hipGraph_t g = nullptr;
+  const hipError_t e = hipStreamEndCapture(m->stream, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
+  m->graph = g;
+  KNJ_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+  return KNJ_OK;
+}
+
+int set_state(knj_model* m, int32_t token, int step) {
+  StepState h{};
+  h.token = token;
+  h.pos = m->pos;
+  h.step = step;
+  KNJ_HIP(hipMemcpyAsync(m->st, &h, sizeof(h), hipMemcpyHostToDevice, m->stream));
+  KNJ_HIP(hipStreamSynchronize(m->stream));
+  return KNJ_OK;
+}
+
+int finish_create(knj_model* m, knj_model** out) {
+  int rc = ensure_graph(m);
+  if (rc) {
+    knj_model_free(m);
+    return rc;
+  }
+  *out = m;
+  return KNJ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int knj_model_create_synthetic(const knj_model_config* cfg, uint64_t seed, knj_model** out) {
+  int rc = require_open();
+  if (rc) return rc;
+  KNJ_CHECK_ARG(out, "null output pointer");
+  if ((rc = validate(cfg))) return rc;
+  knj_model* m = new knj_model();
+  m->c = *cfg;
+  if ((rc = setup(m)) || (rc = synth_all(m, seed))) {
+    knj_model_free(m);
+    return rc;
+  }
+  return finish_create(m, out);
+}
+
+int knj_model_create_from_image(const knj_model_config* cfg, const void* image, uint64_t bytes,
+                                knj_model** out) {
+  int rc = require_open();
+  if (rc) return rc;
+  KNJ_CHECK_ARG(out && image, "null pointer");
+  if ((rc = validate(cfg))) return rc;
+  knj_model* m = new knj_model();
+  m->c = *cfg;
+  if ((rc = setup(m))) {
+    knj_model_free(m);
+    return rc;
+  }
+  if (bytes != m->image_bytes) {
+    knj_model_free(m);
+    set_error("image size does not match the configuration's layout");
+    return KNJ_E_ARG;
+  }
+  if (hipMemcpy(m->image, image, bytes, hipMemcpyHostToDevice) != hipSuccess) {
+    knj_model_free(m);
+    return hip_fail(hipErrorUnknown, "image upload");
+  }
+  return finish_create(m, out);
+}
+
+int knj_model_free(knj_model* m) {
+  if (!m) return KNJ_OK;
+  if (m->stream) (void)hipStreamSynchronize(m->stream);
+  if (m->exec) (void)hipGraphExecDestroy(m->exec);
+  if (m->graph) (void)hipGraphDestroy(m->graph);
+  for (void* p : m->owned) (void)hipFree(p);
+  if (m->stream) (void)hipStreamDestroy(m->stream);
+  delete m;
+  return KNJ_OK;
+}
+
+uint64_t knj_model_image_bytes(const knj_model* m) { return m ? m->image_bytes : 0; }
+const void* knj_model_image_device(const knj_model* m) { return m ? m->image : nullptr; }
+
+int knj_model_download_image(const knj_model* m, void* host, uint64_t bytes) {
+  KNJ_CHECK_ARG(m && host && bytes == m->image_bytes, "bad image download arguments");
+  KNJ_HIP(hipMemcpy(host, m->image, bytes, hipMemcpyDeviceToHost));
+  return KNJ_OK;
+}
+
+int knj_model_reset(knj_model* m) {
+  KNJ_CHECK_ARG(m, "null model");
+  const uint64_t kv = knj_kv_elems(&m->c);
+  KNJ_HIP(hipMemsetAsync(m->kv_k, 0, kv * 2, m->stream));
+  KNJ_HIP(hipMemsetAsync(m->kv_v, 0, kv * 2, m->stream));
+  KNJ_HIP(hipStreamSynchronize(m->stream));
+  m->pos = 0;
+  return KNJ_OK;
+}
+
+int knj_model_pos(const knj_model* m) { return m ? m->pos : -1; }
+
+int knj_model_set_pos(knj_model* m, int pos) {
+  KNJ_CHECK_ARG(m && pos >= 0 && pos <= m->c.n_ctx, "position outside the context");
+  m->pos = pos;
+  return KNJ_OK;
+}
+
+int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_host) {
+  KNJ_CHECK_ARG(m && tokens, "null pointer");
+  KNJ_CHECK_ARG(n > 0, "forward needs at least one token");
+  if (m->pos + n > m->c.n_ctx) {
+    set_error("context exhausted");
+    return KNJ_E_ARG;
+  }
+  for (int t = 0; t < n; ++t) {
+    KNJ_CHECK_ARG(tokens[t] >= 0 && tokens[t] < m->c.n_vocab, "token id out of range");
+  }
+  for (int t = 0; t < n; ++t) {
+    int rc = set_state(m, tokens[t], 0);
+    if (rc) return rc;
+    KNJ_HIP(hipGraphLaunch(m->exec, m->stream));
+    m->pos += 1;
+  }
+  if (logits_host) {
+    KNJ_HIP(hipMemcpyAsync(logits_host, m->logits, (uint64_t)m->c.n_vocab * 4, hipMemcpyDeviceToHost,
+                           m->stream));
+  }
+  KNJ_HIP(hipStreamSynchronize(m->stream));
+  return KNJ_OK;
+}
+
+int knj_model_decode_greedy(knj_model* m, int32_t first, int steps, int32_t* out_tokens) {
+  KNJ_CHECK_ARG(m && out_tokens, "null pointer");
+  KNJ_CHECK_ARG(steps > 0 && steps <= m->max_steps, "steps out of range");
+  KNJ_CHECK_ARG(first >= 0 && first < m->c.n_vocab, "token id out of range");
+  if (m->pos + steps > m->c.n_ctx) {
+    set_error("context exhausted");
+    return KNJ_E_ARG;
+  }
+  int rc = set_state(m, first, 0);
+  if (rc) return rc;
+  for (int i = 0; i < steps; ++i) KNJ_HIP(hipGraphLaunch(m->exec, m->stream));
+  m->pos += steps;
+  KNJ_HIP(hipMemcpyAsync(out_tokens, m->out_tokens, (uint64_t)steps * 4, hipMemcpyDeviceToHost, m->stream));
+  KNJ_HIP(hipStreamSynchronize(m->stream));
+  return KNJ_OK;
+}
+
+int knj_model_hidden(const knj_model* m, int il, float* host_out) {
+  KNJ_CHECK_ARG(m && host_out && il >= 0 && il < m->c.n_layer, "bad arguments");
+  KNJ_HIP(hipMemcpy(host_out, m->hidden + (uint64_t)il * m->c.n_embd, (uint64_t)m->c.n_embd * 4,
+                    hipMemcpyDeviceToHost));
+  return KNJ_OK;
+}
+
+int knj_model_topk(const knj_model* m, int il, int32_t* idx_out, float* w_out) {
+  KNJ_CHECK_ARG(m && idx_out && w_out && il >= 0 && il < m->c.n_layer, "bad arguments");
+  const uint64_t k = m->c.n_expert_used;
+  KNJ_HIP(hipMemcpy(idx_out, m->topk_idx + il * k, k * 4, hipMemcpyDeviceToHost));
+  KNJ_HIP(hipMemcpy(w_out, m->topk_w + il * k, k * 4, hipMemcpyDeviceToHost));
+  return KNJ_OK;
+}
+
+int knj_model_logits(const knj_model* m, float* host_out) {
+  KNJ_CHECK_ARG(m && host_out, "bad arguments");
+  KNJ_HIP(hipMemcpy(host_out, m->logits, (uint64_t)m->c.n_vocab * 4, hipMemcpyDeviceToHost));
+  return KNJ_OK;
+}
+
+int knj_model_kv_download(const knj_model* m, uint16_t* k_host, uint16_t* v_host) {
+  KNJ_CHECK_ARG(m && k_host && v_host, "bad arguments");
+  const uint64_t kv = knj_kv_elems(&m->c) * 2;
+  KNJ_HIP(hipMemcpy(k_host, m->kv_k, kv, hipMemcpyDeviceToHost));
+  KNJ_HIP(hipMemcpy(v_host, m->kv_v, kv, hipMemcpyDeviceToHost));
+  return KNJ_OK;
+}
+
+int knj_model_kv_upload(knj_model* m, const uint16_t* k_host, const uint16_t* v_host) {
+  KNJ_CHECK_ARG(m && k_host && v_host, "bad arguments");
+  const uint64_t kv = knj_kv_elems(&m->c) * 2;
+  KNJ_HIP(hipMemcpy(m->kv_k, k_host, kv, hipMemcpyHostToDevice));
+  KNJ_HIP(hipMemcpy(m->kv_v, v_host, kv, hipMemcpyHostToDevice));
+  return KNJ_OK;
+}
+
+int knj_model_time_decode(knj_model* m, int iters, float* ms_out) {
+  KNJ_CHECK_ARG(m && ms_out && iters > 0, "bad arguments");
+  if (m->pos + iters > m->c.n_ctx) {
+    set_error("context exhausted");
+    return KNJ_E_ARG;
+  }
+  int rc = set_state(m, 0, 0);
+  if (rc) return rc;
+  hipEvent_t a, b;
+  KNJ_HIP(hipEventCreate(&a));
+  KNJ_HIP(hipEventCreate(&b));
+  KNJ_HIP(hipEventRecord(a, m->stream));
+  for (int i = 0; i < iters; ++i) KNJ_HIP(hipGraphLaunch(m->exec, m->stream));
+  KNJ_HIP(hipEventRecord(b, m->stream));
+  KNJ_HIP(hipEventSynchronize(b));
+  KNJ_HIP(hipEventElapsedTime(ms_out, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  m->pos += iters;
+  return KNJ_OK;
+}
+
+int knj_model_time_experts(knj_model* m, int iters, float* us_out) {
+  KNJ_CHECK_ARG(m && us_out && iters > 0, "bad arguments");
+  const knj_model_config& c = m->c;
+  hipEvent_t a, b;
+  KNJ_HIP(hipEventCreate(&a));
+  KNJ_HIP(hipEventCreate(&b));
+  KNJ_HIP(hipEventRecord(a, m->stream));
+  for (int i = 0; i < iters; ++i) {
+    const int il = i % c.n_layer;
+    const knj_layer_offsets& lo = m->lo[il];
+    ExpertArgs ea{m->hx, m->topk_idx + (uint64_t)il * c.n_expert_used,
+                  m->topk_w + (uint64_t)il * c.n_expert_used, m->image + lo.gate, m->image + lo.up,
+                  m->image + lo.down, c.type_gate_up, c.type_down, c.n_embd, c.n_ff, c.n_expert,
+                  c.n_expert_used, m->act, nullptr, m->ctx, nullptr};
+    KNJ_HIP(launch_experts(ea, m->stream));
+  }
+  KNJ_HIP(hipEventRecord(b, m->stream));
+  KNJ_HIP(hipEventSynchronize(b));
+  float ms = 0.0f;
+  KNJ_HIP(hipEventElapsedTime(&ms, a, b));
+  (void)hipEventDestroy(a);
+  (void)hipEventDestroy(b);
+  *us_out = ms * 1000.0f / (float)iters;
+  return KNJ_OK;
+}
+
+}  // extern "C"

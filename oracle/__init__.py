@@ -131,6 +131,9 @@ def lib():
         L.knjo_model_kv_v.argtypes = [_P]
         L.knjo_model_set_pos.restype = C.c_int
         L.knjo_model_set_pos.argtypes = [_P, C.c_int]
+        L.knjo_model_set_kv_source.argtypes = [_P, _P, _P]
+        L.knjo_model_kv_stats.argtypes = [_P, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
+                                          C.POINTER(C.c_int), C.POINTER(C.c_float)]
         L.knjo_last_error.restype = C.c_char_p
         _lib = L
     return _lib
@@ -244,6 +247,7 @@ class OracleModel:
         return lib().knjo_model_threads(self.h)
 
     def image(self) -> np.ndarray:
+        """The weight image as a view (no copy): valid while this model is alive."""
         L = lib()
         n = L.knjo_model_image_bytes(self.h)
         p = L.knjo_model_image(self.h)
@@ -276,6 +280,17 @@ class OracleModel:
         k = np.ctypeslib.as_array(lib().knjo_model_kv_k(self.h), shape=shape)
         v = np.ctypeslib.as_array(lib().knjo_model_kv_v(self.h), shape=shape)
         return k, v
+
+    def set_kv_source(self, k: np.ndarray | None, v: np.ndarray | None):
+        """Adopt these f16 caches' values for newly written slots (see the C header)."""
+        self._kv_src = (k, v)
+        lib().knjo_model_set_kv_source(self.h, _ptr(k) if k is not None else None,
+                                       _ptr(v) if v is not None else None)
+
+    def kv_stats(self):
+        a, d, u, mid = C.c_int64(), C.c_int64(), C.c_int(), C.c_float()
+        lib().knjo_model_kv_stats(self.h, C.byref(a), C.byref(d), C.byref(u), C.byref(mid))
+        return dict(adopted=a.value, differing=d.value, max_ulp=u.value, max_mid_dist=mid.value)
 
     def set_pos(self, pos: int):
         if lib().knjo_model_set_pos(self.h, pos) != 0:

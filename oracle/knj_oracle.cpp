@@ -461,6 +461,8 @@ void synth_model(Pool& pool, const knj_model_config* c, uint64_t seed, uint8_t* 
 }  // namespace
 
 // ======================================================================= model
+struct knjo_model;
+static uint16_t adopt_kv(knjo_model* m, float v, const uint16_t* src, size_t idx);
 
 struct knjo_model {
   knj_model_config c;
@@ -473,6 +475,13 @@ struct knjo_model {
   int pos = 0;
   std::vector<float> x, xn, q, k, v, ctx, ao, hx, ffn_out, rlog, scores, logits, inv_freq, head_tmp;
   std::vector<uint16_t> kv_k, kv_v;
+  // optional f16 values to adopt for each newly written slot (see
+  // knjo_model_set_kv_source) and the statistics of that adoption
+  const uint16_t* src_k = nullptr;
+  const uint16_t* src_v = nullptr;
+  int64_t kv_adopted = 0, kv_diff = 0;
+  int kv_max_ulp = 0;
+  float kv_max_mid = 0.0f;
   std::vector<float> hidden;     // [n_layer][H], last token
   std::vector<int32_t> topk_idx; // [n_layer][K]
   std::vector<float> topk_w;     // [n_layer][K]
@@ -482,7 +491,56 @@ struct knjo_model {
   std::vector<float> col;
 };
 
+// f16 of one new cache element.  Without a source this is the oracle's own
+// round-to-nearest-even.  With a source (the GPU's cache), the source's value
+// is adopted; when it differs from the oracle's own rounding, the distance from
+// `v` to the set of f32 values that round to the source's value is recorded
+// (zero would mean the source rounded `v` itself differently, which RNE never
+// does; a tiny distance means an f32 value a few ulps from `v` was rounded).  This separates the
+// single rounding decision an f32 difference in the last bits can flip from
+// every other operation of the step.
+static uint16_t adopt_kv(knjo_model* m, float v, const uint16_t* src, size_t idx) {
+  const uint16_t own = knj_f32_to_f16(v);
+  if (!src) return own;
+  const uint16_t got = src[idx];
+  m->kv_adopted += 1;
+  if (got == own) return own;
+  m->kv_diff += 1;
+  const int ulp = std::abs((int)(own & 0x7FFF) - (int)(got & 0x7FFF)) +
+                  (((own ^ got) & 0x8000) ? 1 : 0);
+  m->kv_max_ulp = std::max(m->kv_max_ulp, ulp);
+  // the interval of f32 values that round to `got` lies between the midpoints
+  // to its two f16 neighbours; record how far `v` is from that interval
+  auto ord = [](uint16_t h) { return (h & 0x8000) ? 0x8000 - (int)(h & 0x7FFF) : 0x8000 + (int)h; };
+  auto unord = [](int k) {
+    return (uint16_t)(k >= 0x8000 ? (k - 0x8000) : (0x8000 | (0x8000 - k)));
+  };
+  const float g = knj_f16_to_f32(got);
+  const float below = knj_f16_to_f32(unord(ord(got) - 1));
+  const float above = knj_f16_to_f32(unord(ord(got) + 1));
+  const double lo = 0.5 * ((double)g + (double)below), hi = 0.5 * ((double)g + (double)above);
+  const double dist = v < lo ? lo - v : (v > hi ? v - hi : 0.0);
+  m->kv_max_mid = std::max(m->kv_max_mid, (float)dist);
+  return got;
+}
+
 extern "C" {
+
+void knjo_model_set_kv_source(knjo_model* m, const uint16_t* k, const uint16_t* v) {
+  m->src_k = k;
+  m->src_v = v;
+  m->kv_adopted = m->kv_diff = 0;
+  m->kv_max_ulp = 0;
+  m->kv_max_mid = 0.0f;
+}
+
+void knjo_model_kv_stats(knjo_model* m, int64_t* adopted, int64_t* differing, int* max_ulp,
+                         float* max_mid_dist) {
+  *adopted = m->kv_adopted;
+  *differing = m->kv_diff;
+  *max_ulp = m->kv_max_ulp;
+  *max_mid_dist = m->kv_max_mid;
+}
 
 float knjo_f16_to_f32(uint16_t h) { return knj_f16_to_f32(h); }
 uint16_t knjo_f32_to_f16(float f) { return knj_f32_to_f16(f); }
@@ -672,8 +730,8 @@ int knjo_model_forward(knjo_model* m, const int32_t* tokens, int n, float* logit
         for (int h = 0; h < c.n_head_kv; ++h) {
           const size_t off = (((size_t)il * c.n_head_kv + h) * c.n_ctx + p) * D;
           for (int d = 0; d < D; ++d) {
-            m->kv_k[off + d] = knj_f32_to_f16(m->k[(size_t)h * D + d]);
-            m->kv_v[off + d] = knj_f32_to_f16(m->v[(size_t)h * D + d]);
+            m->kv_k[off + d] = adopt_kv(m, m->k[(size_t)h * D + d], m->src_k, off + d);
+            m->kv_v[off + d] = adopt_kv(m, m->v[(size_t)h * D + d], m->src_v, off + d);
           }
         }
         // attention (model.cpp:591-616), K/V read back from the f16 cache

@@ -80,6 +80,17 @@ const float* knjo_model_topk_w(knjo_model* m, int il);
 uint16_t* knjo_model_kv_k(knjo_model* m);
 uint16_t* knjo_model_kv_v(knjo_model* m);
 int knjo_model_set_pos(knjo_model* m, int pos);
+/* Cache-source mode: when k/v are non-NULL (same layout as the model's cache),
+ * each newly written cache element takes the source's f16 value.  Statistics
+ * since the last call: elements adopted, elements that differed from the
+ * oracle's own rounding, the largest difference in f16 ulps, and the largest
+ * absolute distance from the oracle's f32 value to the set of f32 values that
+ * round to the source's f16 value (K and V elements are O(1) here, so a bound
+ * like 1e-5 says the source rounded an f32 value that agrees with the oracle's
+ * to ~1e-5 relative). */
+void knjo_model_set_kv_source(knjo_model* m, const uint16_t* k, const uint16_t* v);
+void knjo_model_kv_stats(knjo_model* m, int64_t* adopted, int64_t* differing, int* max_ulp,
+                         float* max_mid_dist);
 const char* knjo_last_error(void);
 
 #ifdef __cplusplus
