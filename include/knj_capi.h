@@ -153,10 +153,12 @@ int knj_model_kv_upload(knj_model* m, const uint16_t* k_host, const uint16_t* v_
 /* Times `iters` greedy steps with HIP events on the model's stream (graph
  * replays), returns total milliseconds. */
 int knj_model_time_decode(knj_model* m, int iters, float* ms_out);
-/* Times the expert GEMV pass (gate/up + down kernels of one layer) over
- * `iters` launches, rotating through all layers so repeats come from HBM, not
- * the last-level cache; returns the average microseconds per launch pair. */
-int knj_model_time_experts(knj_model* m, int iters, float* us_out);
+/* Times the expert GEMV kernels of the decode step with HIP events on the
+ * model's stream: `iters` launches of the gate/up kernel, then `iters` of the
+ * down kernel, each launch on the next layer's weights (rotating through all
+ * layers so repeats come from HBM, not the 256 MB last-level cache).  Returns
+ * the average microseconds per launch of each. */
+int knj_model_time_experts(knj_model* m, int iters, float* us_gateup, float* us_down);
 
 #ifdef __cplusplus
 }

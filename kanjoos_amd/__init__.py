@@ -127,7 +127,7 @@ _SIGS = {
     "knj_model_kv_download": (_i, [_P, _P, _P]),
     "knj_model_kv_upload": (_i, [_P, _P, _P]),
     "knj_model_time_decode": (_i, [_P, _i, C.POINTER(_f)]),
-    "knj_model_time_experts": (_i, [_P, _i, C.POINTER(_f)]),
+    "knj_model_time_experts": (_i, [_P, _i, C.POINTER(_f), C.POINTER(_f)]),
 }
 
 _lib = None
@@ -372,7 +372,8 @@ class Model:
         check(lib().knj_model_time_decode(self.h, iters, C.byref(ms)))
         return ms.value
 
-    def time_experts(self, iters: int) -> float:
-        us = C.c_float()
-        check(lib().knj_model_time_experts(self.h, iters, C.byref(us)))
-        return us.value
+    def time_experts(self, iters: int):
+        """(gate/up, down) average microseconds per launch, rotating over layers."""
+        a, b = C.c_float(), C.c_float()
+        check(lib().knj_model_time_experts(self.h, iters, C.byref(a), C.byref(b)))
+        return a.value, b.value

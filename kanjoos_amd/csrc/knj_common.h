@@ -91,6 +91,8 @@ struct ExpertArgs {
   float* hidden_copy;     // optional second destination of out
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s);
+hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s);
 
 struct QkRopeArgs {
   float* q;               // [n_head][D] in place

@@ -783,14 +783,20 @@ hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
 }
 
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s) {
-  {
-    const size_t lds = (size_t)a.n_embd * 4 + (size_t)(a.n_embd / 32) * 4 + 64;
-    const int rows_per_block = 16;  // 4 waves x 4 row pairs
-    dim3 grid((a.n_ff + rows_per_block - 1) / rows_per_block, a.k);
-    hipLaunchKernelGGL(k_expert_gateup, grid, dim3(kBlock), lds, s, a);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  const hipError_t e = launch_expert_gateup(a, s);
+  if (e != hipSuccess) return e;
+  return launch_expert_down(a, s);
+}
+
+hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s) {
+  const size_t lds = (size_t)a.n_embd * 4 + (size_t)(a.n_embd / 32) * 4 + 64;
+  const int rows_per_block = 16;  // 4 waves x 4 row pairs
+  dim3 grid((a.n_ff + rows_per_block - 1) / rows_per_block, a.k);
+  hipLaunchKernelGGL(k_expert_gateup, grid, dim3(kBlock), lds, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s) {
   const bool q6 = a.type_down == KNJ_TYPE_Q6_K;
   const int nb = a.n_ff / KNJ_QK;
   const int lpr = std::min(64, pow2_at_least((q6 ? 8 : 4) * nb));

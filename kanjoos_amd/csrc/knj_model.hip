@@ -523,29 +523,31 @@ int knj_model_time_decode(knj_model* m, int iters, float* ms_out) {
   return KNJ_OK;
 }
 
-int knj_model_time_experts(knj_model* m, int iters, float* us_out) {
-  KNJ_CHECK_ARG(m && us_out && iters > 0, "bad arguments");
+int knj_model_time_experts(knj_model* m, int iters, float* us_gateup, float* us_down) {
+  KNJ_CHECK_ARG(m && us_gateup && us_down && iters > 0, "bad arguments");
   const knj_model_config& c = m->c;
-  hipEvent_t a, b;
-  KNJ_HIP(hipEventCreate(&a));
-  KNJ_HIP(hipEventCreate(&b));
-  KNJ_HIP(hipEventRecord(a, m->stream));
-  for (int i = 0; i < iters; ++i) {
-    const int il = i % c.n_layer;
-    const knj_layer_offsets& lo = m->lo[il];
-    ExpertArgs ea{m->hx, m->topk_idx + (uint64_t)il * c.n_expert_used,
-                  m->topk_w + (uint64_t)il * c.n_expert_used, m->image + lo.gate, m->image + lo.up,
-                  m->image + lo.down, c.type_gate_up, c.type_down, c.n_embd, c.n_ff, c.n_expert,
-                  c.n_expert_used, m->act, nullptr, m->ctx, nullptr};
-    KNJ_HIP(launch_experts(ea, m->stream));
+  hipEvent_t ev[3];
+  for (auto& e : ev) KNJ_HIP(hipEventCreate(&e));
+  for (int phase = 0; phase < 2; ++phase) {
+    KNJ_HIP(hipEventRecord(ev[phase], m->stream));
+    for (int i = 0; i < iters; ++i) {
+      const int il = i % c.n_layer;  // rotate so repeats come from HBM
+      const knj_layer_offsets& lo = m->lo[il];
+      ExpertArgs ea{m->hx, m->topk_idx + (uint64_t)il * c.n_expert_used,
+                    m->topk_w + (uint64_t)il * c.n_expert_used, m->image + lo.gate, m->image + lo.up,
+                    m->image + lo.down, c.type_gate_up, c.type_down, c.n_embd, c.n_ff, c.n_expert,
+                    c.n_expert_used, m->act, nullptr, m->ctx, nullptr};
+      KNJ_HIP(phase == 0 ? launch_expert_gateup(ea, m->stream) : launch_expert_down(ea, m->stream));
+    }
   }
-  KNJ_HIP(hipEventRecord(b, m->stream));
-  KNJ_HIP(hipEventSynchronize(b));
-  float ms = 0.0f;
-  KNJ_HIP(hipEventElapsedTime(&ms, a, b));
-  (void)hipEventDestroy(a);
-  (void)hipEventDestroy(b);
-  *us_out = ms * 1000.0f / (float)iters;
+  KNJ_HIP(hipEventRecord(ev[2], m->stream));
+  KNJ_HIP(hipEventSynchronize(ev[2]));
+  float a = 0.0f, b = 0.0f;
+  KNJ_HIP(hipEventElapsedTime(&a, ev[0], ev[1]));
+  KNJ_HIP(hipEventElapsedTime(&b, ev[1], ev[2]));
+  for (auto& e : ev) (void)hipEventDestroy(e);
+  *us_gateup = a * 1000.0f / (float)iters;
+  *us_down = b * 1000.0f / (float)iters;
   return KNJ_OK;
 }
 
