@@ -103,19 +103,18 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
                          float* topk_w, void* stream);
 
 /* ------------------------------------------------------------ attention
- * knj_qk_norm_rope_append: per-head RMSNorm of q and k with q_norm/k_norm,
- *   NEOX RoPE at position `pos` (pairs (i, i+D/2), theta = pos*base^(-2i/D)),
- *   q rewritten in place, k and v rounded to f16 and stored at slot `pos` of a
- *   [n_head_kv][n_ctx][D] cache (model.cpp:567-584 with an f16 cache).
- * knj_attention_decode: GQA decode attention of one query position over cache
- *   slots [0, n_kv): scores q.k*scale, softmax, sum a*v (model.cpp:591-616). */
-int knj_qk_norm_rope_append(float* q, const float* k, const float* v, const float* q_norm,
-                            const float* k_norm, float eps, float rope_base, int pos, int n_head,
-                            int n_head_kv, int head_dim, int n_ctx, uint16_t* k_cache,
-                            uint16_t* v_cache, void* stream);
-int knj_attention_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                         int n_head, int n_head_kv, int head_dim, int n_ctx, int n_kv, float scale,
-                         float* out, void* stream);
+ * knj_attention_step: the attention block of one decode token
+ *   (/root/reference/src/model/model.cpp:567-616 with an f16 cache): per-head
+ *   RMSNorm of the raw projections q [n_head][D] and k [n_head_kv][D] with
+ *   q_norm / k_norm, NEOX RoPE at `pos` (pairs (i, i+D/2),
+ *   theta = pos*base^(-2i/D)), k and v rounded to f16 and stored at slot `pos`
+ *   of the [n_head_kv][n_ctx][D] caches, then GQA attention of every query head
+ *   over slots [0, pos]: scores q.k/sqrt(D), softmax, out = sum a*v.
+ *   q, k, v are not modified.  D is 64 or 128; the GQA group is at most 8. */
+int knj_attention_step(const float* q, const float* k, const float* v, const float* q_norm,
+                       const float* k_norm, float eps, float rope_base, int pos, int n_head,
+                       int n_head_kv, int head_dim, int n_ctx, uint16_t* k_cache, uint16_t* v_cache,
+                       float* out, void* stream);
 
 /* ------------------------------------------------------------ model step
  * The device counterpart of knj::Model (/root/reference/src/model/model.h:55-80):

@@ -30,8 +30,7 @@ EXPORTS = (
     "knj_device_open", "knj_device_close", "knj_device_caps_get", "knj_check_arch",
     "knj_built_arch", "knj_last_error", "knj_malloc", "knj_free", "knj_memcpy_h2d",
     "knj_memcpy_d2h", "knj_memset_zero", "knj_synchronize", "knj_dequant", "knj_gemv",
-    "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_qk_norm_rope_append",
-    "knj_attention_decode", "knj_model_create_synthetic", "knj_model_create_from_image",
+    "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_attention_step", "knj_model_create_synthetic", "knj_model_create_from_image",
     "knj_model_free", "knj_model_image_bytes", "knj_model_image_device",
     "knj_model_download_image", "knj_model_reset", "knj_model_pos", "knj_model_set_pos",
     "knj_model_forward", "knj_model_decode_greedy", "knj_model_hidden", "knj_model_topk",
@@ -108,8 +107,7 @@ _SIGS = {
     "knj_moe_router": (_i, [_P, _P, _f, _P, _i, _i, _i, _P, _P, _P, _P, _P]),
     "knj_moe_decode_layer": (_i, [_P, _P, _f, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _P, _P,
                                   _P, _P, _P, _P]),
-    "knj_qk_norm_rope_append": (_i, [_P, _P, _P, _P, _P, _f, _f, _i, _i, _i, _i, _i, _P, _P, _P]),
-    "knj_attention_decode": (_i, [_P, _P, _P, _i, _i, _i, _i, _i, _f, _P, _P]),
+    "knj_attention_step": (_i, [_P, _P, _P, _P, _P, _f, _f, _i, _i, _i, _i, _i, _P, _P, _P, _P]),
     "knj_model_create_synthetic": (_i, [C.POINTER(ModelConfig), _u64, C.POINTER(_P)]),
     "knj_model_create_from_image": (_i, [C.POINTER(ModelConfig), _P, _u64, C.POINTER(_P)]),
     "knj_model_free": (_i, [_P]),
@@ -259,16 +257,11 @@ def moe_decode_layer(x, router_w, gate, up, down, n_embd, n_ff, n_expert, k, out
                                      _p(resid), _p(out), _p(logits), _p(topk_idx), _p(topk_w), None))
 
 
-def qk_norm_rope_append(q, k, v, q_norm, k_norm, eps, rope_base, pos, n_head, n_head_kv,
-                        head_dim, n_ctx, k_cache, v_cache) -> None:
-    check(lib().knj_qk_norm_rope_append(_p(q), _p(k), _p(v), _p(q_norm), _p(k_norm), eps,
-                                        rope_base, pos, n_head, n_head_kv, head_dim, n_ctx,
-                                        _p(k_cache), _p(v_cache), None))
-
-
-def attention_decode(q, k_cache, v_cache, n_head, n_head_kv, head_dim, n_ctx, n_kv, scale, out) -> None:
-    check(lib().knj_attention_decode(_p(q), _p(k_cache), _p(v_cache), n_head, n_head_kv, head_dim,
-                                     n_ctx, n_kv, scale, _p(out), None))
+def attention_step(q, k, v, q_norm, k_norm, eps, rope_base, pos, n_head, n_head_kv, head_dim,
+                   n_ctx, k_cache, v_cache, out) -> None:
+    check(lib().knj_attention_step(_p(q), _p(k), _p(v), _p(q_norm), _p(k_norm), eps, rope_base, pos,
+                                   n_head, n_head_kv, head_dim, n_ctx, _p(k_cache), _p(v_cache),
+                                   _p(out), None))
 
 
 # ------------------------------------------------------------------ model

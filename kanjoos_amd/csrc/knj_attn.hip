@@ -1,0 +1,258 @@
+// kanjoos_amd/csrc/knj_attn.hip -- decode attention of one token over the f16 KV cache.
+//
+// Device side of the attention block of Model::forward
+// (/root/reference/src/model/model.cpp:560-617): per-head RMSNorm of q and k
+// (q_norm / k_norm), NEOX RoPE, append of k and v to the cache, then for every
+// query head h (kv head h / group) scores q.k * 1/sqrt(D) over positions
+// 0..pos, softmax, and sum a*v.
+//
+// One fused launch, split-KV: workgroup (kv head, split) owns 64 cache slots.
+// It normalises and rotates the `group` query heads itself, stages its K and V
+// slots in LDS (the slot being written this step comes from registers, and
+// only the workgroup that owns it writes it to the cache), and emits a partial
+// record {max, sum, sum a*v} per query head.  The last workgroup of each kv
+// head merges that head's partials in ascending split order.
+#include "knj_common.h"
+#include "knj_dev.h"
+
+namespace knj {
+namespace {
+
+using namespace dev;
+
+constexpr int kChunk = 64;
+
+// q/k normalisation + rotation of one head held as 4 floats per thread in a
+// group of D/4 threads: returns the thread's 4 outputs (elements 4c..4c+3).
+template <int D>
+__device__ __forceinline__ float4 norm_rope4(float4 v, int c, const float* __restrict__ nw,
+                                             float eps, const float* __restrict__ cs,
+                                             const float* __restrict__ sn) {
+  constexpr int T = D / 4;  // threads per head
+  float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  ss = group_sum<T>(ss);
+  const float scale = 1.0f / sqrtf(ss / (float)D + eps);
+  const float4 w = *reinterpret_cast<const float4*>(nw + 4 * c);
+  float4 n;
+  n.x = v.x * scale * w.x;
+  n.y = v.y * scale * w.y;
+  n.z = v.z * scale * w.z;
+  n.w = v.w * scale * w.w;
+  // partner: elements 4c +- D/2 live in thread c +- T/2
+  float4 p;
+  p.x = __shfl_xor(n.x, T / 2, 64);
+  p.y = __shfl_xor(n.y, T / 2, 64);
+  p.z = __shfl_xor(n.z, T / 2, 64);
+  p.w = __shfl_xor(n.w, T / 2, 64);
+  const bool lo = c < T / 2;
+  const int i0 = lo ? 4 * c : 4 * c - D / 2;  // rotation index of element x
+  float4 out;
+  const float e[4] = {n.x, n.y, n.z, n.w};
+  const float q[4] = {p.x, p.y, p.z, p.w};
+  float r[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float cc = cs[i0 + k], s = sn[i0 + k];
+    // (x0, x1) -> (x0*c - x1*s, x0*s + x1*c) with x0 the low-half element
+    r[k] = lo ? (e[k] * cc - q[k] * s) : (q[k] * s + e[k] * cc);
+  }
+  out.x = r[0];
+  out.y = r[1];
+  out.z = r[2];
+  out.w = r[3];
+  return out;
+}
+
+template <int D>
+__global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
+  constexpr int ROWH = D + 8;            // f16 elements per LDS row (16-byte pad)
+  constexpr int T = D / 4;               // threads per head for the q pass
+  __shared__ float qs[8 * D];            // normalised, rotated queries
+  __shared__ uint16_t ks[kChunk * ROWH];
+  __shared__ uint16_t vs[kChunk * ROWH];
+  __shared__ float es[8 * kChunk];       // exp(score - max) per head
+  __shared__ unsigned int flag;
+  const int kvh = blockIdx.x, split = blockIdx.y, n_split = gridDim.y;
+  const int G = a.n_head / a.n_head_kv;
+  const int pos = *a.pos;
+  const int n_kv = pos + 1;
+  const int p0 = split * kChunk;
+  const int cnt = min(kChunk, n_kv - p0);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
+  uint16_t* vc = a.v_cache + (uint64_t)kvh * a.n_ctx * D;
+  float* part = a.partial + ((uint64_t)(kvh * G) * n_split + split) * (D + 2);
+  const uint64_t hstride = (uint64_t)n_split * (D + 2);
+
+  if (cnt > 0) {
+    // 1) cache loads for this chunk (16 bytes per load, 64*D*2 bytes each of K, V)
+    constexpr int PER = (kChunk * D * 2) / (16 * kBlock);  // loads per thread per matrix
+    static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
+    // (named registers rather than an array: an array live across the query
+    // pass below was placed in scratch memory)
+    uint4 k0, k1, k2, k3, v0, v1, v2, v3;
+    auto ld = [&](int j, uint4& kk, uint4& vv) {
+      const int c16 = tid + kBlock * j;
+      const int p = min((c16 * 8) / D, cnt - 1), off = (c16 * 8) % D;
+      kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)(p0 + p) * D + off);
+      vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)(p0 + p) * D + off);
+    };
+    ld(0, k0, v0);
+    ld(1, k1, v1);
+    if constexpr (PER > 2) {
+      ld(2, k2, v2);
+      ld(3, k3, v3);
+    }
+    // 2) queries of this kv head: 4 floats per thread, T threads per head
+    const float* cs = a.rope_cos + (uint64_t)pos * (D / 2);
+    const float* sn = a.rope_sin + (uint64_t)pos * (D / 2);
+    if (tid < G * T) {
+      const int h = tid / T, c = tid % T;
+      const float4 v = *reinterpret_cast<const float4*>(a.q + (uint64_t)(kvh * G + h) * D + 4 * c);
+      const float4 r = norm_rope4<D>(v, c, a.q_norm, a.eps, cs, sn);
+      *reinterpret_cast<float4*>(qs + h * D + 4 * c) = r;
+    }
+    // 3) the slot written this step, if it is in this chunk
+    if (pos >= p0 && pos < p0 + cnt && tid < T) {
+      const int c = tid;
+      const float4 v = *reinterpret_cast<const float4*>(a.k + (uint64_t)kvh * D + 4 * c);
+      const float4 r = norm_rope4<D>(v, c, a.k_norm, a.eps, cs, sn);
+      const float4 vv = *reinterpret_cast<const float4*>(a.v + (uint64_t)kvh * D + 4 * c);
+      const uint16_t kh[4] = {f2h(r.x), f2h(r.y), f2h(r.z), f2h(r.w)};
+      const uint16_t vh[4] = {f2h(vv.x), f2h(vv.y), f2h(vv.z), f2h(vv.w)};
+      const int lp = pos - p0;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        kc[(uint64_t)pos * D + 4 * c + k] = kh[k];
+        vc[(uint64_t)pos * D + 4 * c + k] = vh[k];
+        ks[lp * ROWH + 4 * c + k] = kh[k];
+        vs[lp * ROWH + 4 * c + k] = vh[k];
+      }
+    }
+    auto st = [&](int j, const uint4& kk, const uint4& vv) {
+      const int c16 = tid + kBlock * j;
+      const int p = (c16 * 8) / D, off = (c16 * 8) % D;
+      if (p < cnt && p0 + p != pos) {
+        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = kk;
+        *reinterpret_cast<uint4*>(vs + p * ROWH + off) = vv;
+      }
+    };
+    st(0, k0, v0);
+    st(1, k1, v1);
+    if constexpr (PER > 2) {
+      st(2, k2, v2);
+      st(3, k3, v3);
+    }
+    __syncthreads();
+    // 4) scores: wave w owns heads 2w, 2w+1; lane = position
+    const int h0 = 2 * wave, h1 = 2 * wave + 1;
+    if (h0 < G) {
+      float s0 = 0.0f, s1 = 0.0f;
+      if (lane < cnt) {
+        const uint16_t* kr16 = ks + lane * ROWH;
+#pragma unroll 2
+        for (int d8 = 0; d8 < D; d8 += 8) {
+          const uint4 kk = *reinterpret_cast<const uint4*>(kr16 + d8);
+          const float kf[8] = {h2f(kk.x), h2f(kk.x >> 16), h2f(kk.y), h2f(kk.y >> 16),
+                               h2f(kk.z), h2f(kk.z >> 16), h2f(kk.w), h2f(kk.w >> 16)};
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            s0 += qs[h0 * D + d8 + i] * kf[i];
+            if (h1 < G) s1 += qs[h1 * D + d8 + i] * kf[i];
+          }
+        }
+      }
+      s0 = lane < cnt ? s0 * a.scale : -INFINITY;
+      s1 = (lane < cnt && h1 < G) ? s1 * a.scale : -INFINITY;
+      const float m0 = group_max<64>(s0), m1 = group_max<64>(s1);
+      const float e0 = lane < cnt ? expf(s0 - m0) : 0.0f;
+      const float e1 = (lane < cnt && h1 < G) ? expf(s1 - m1) : 0.0f;
+      const float l0 = group_sum<64>(e0), l1 = group_sum<64>(e1);
+      es[h0 * kChunk + lane] = e0;
+      if (h1 < G) es[h1 * kChunk + lane] = e1;
+      if (lane == 0) {
+        part[h0 * hstride + 0] = m0;
+        part[h0 * hstride + 1] = l0;
+        if (h1 < G) {
+          part[h1 * hstride + 0] = m1;
+          part[h1 * hstride + 1] = l1;
+        }
+      }
+      // 5) sum a*v for the wave's two heads; lane owns dims (2*lane, 2*lane+1)
+      if (2 * lane < D) {
+        float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
+        for (int p = 0; p < cnt; ++p) {
+          const uint32_t vv = *reinterpret_cast<const uint32_t*>(vs + p * ROWH + 2 * lane);
+          const float v0 = h2f(vv), v1 = h2f(vv >> 16);
+          const float ea = es[h0 * kChunk + p];
+          a00 += ea * v0;
+          a01 += ea * v1;
+          if (h1 < G) {
+            const float eb = es[h1 * kChunk + p];
+            a10 += eb * v0;
+            a11 += eb * v1;
+          }
+        }
+        part[h0 * hstride + 2 + 2 * lane] = a00;
+        part[h0 * hstride + 3 + 2 * lane] = a01;
+        if (h1 < G) {
+          part[h1 * hstride + 2 + 2 * lane] = a10;
+          part[h1 * hstride + 3 + 2 * lane] = a11;
+        }
+      }
+    }
+  } else {
+    for (int i = tid; i < G * (D + 2); i += kBlock) {
+      const int g = i / (D + 2), j = i % (D + 2);
+      part[g * hstride + j] = (j == 0) ? -INFINITY : 0.0f;
+    }
+  }
+
+  // 6) merge: the last workgroup of this kv head combines all splits
+  if (!last_block_done(a.counter + kvh, n_split, &flag)) return;
+  // thread -> (head h = tid / 32, dims 4*(tid%32) ..) for D = 128; D = 64 uses 16 threads/head
+  constexpr int TPH = D / 4;
+  const int h = tid / TPH, c = tid % TPH;
+  if (h >= G) return;
+  const float* ph = a.partial + (uint64_t)(kvh * G + h) * n_split * (D + 2);
+  float M = -INFINITY;
+  for (int s = c; s < n_split; s += TPH) M = fmaxf(M, ld_acquire_f(ph + (uint64_t)s * (D + 2)));
+  M = group_max<TPH>(M);
+  float L = 0.0f;
+  float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s = 0; s < n_split; ++s) {
+    const float m = ld_acquire_f(ph + (uint64_t)s * (D + 2));
+    if (m == -INFINITY) continue;
+    const float f = expf(m - M);
+    L += ld_acquire_f(ph + (uint64_t)s * (D + 2) + 1) * f;
+    const float* pa = ph + (uint64_t)s * (D + 2) + 2 + 4 * c;
+    acc.x += ld_acquire_f(pa + 0) * f;
+    acc.y += ld_acquire_f(pa + 1) * f;
+    acc.z += ld_acquire_f(pa + 2) * f;
+    acc.w += ld_acquire_f(pa + 3) * f;
+  }
+  float4 o;
+  o.x = acc.x / L;
+  o.y = acc.y / L;
+  o.z = acc.z / L;
+  o.w = acc.w / L;
+  *reinterpret_cast<float4*>(a.out + (uint64_t)(kvh * G + h) * D + 4 * c) = o;
+}
+
+}  // namespace
+
+int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
+
+hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
+  const int n_split = attn_splits(a.n_ctx);
+  if (a.head_dim == 128) {
+    hipLaunchKernelGGL(k_attention<128>, dim3(a.n_head_kv, n_split), dim3(kBlock), 0, s, a);
+  } else if (a.head_dim == 64) {
+    hipLaunchKernelGGL(k_attention<64>, dim3(a.n_head_kv, n_split), dim3(kBlock), 0, s, a);
+  } else {
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace knj

@@ -94,38 +94,43 @@ hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s);
 hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s);
 
-struct QkRopeArgs {
-  float* q;               // [n_head][D] in place
-  const float* k;         // [n_head_kv][D]
-  const float* v;         // [n_head_kv][D]
-  const float* q_norm;    // [D]
-  const float* k_norm;    // [D]
-  float eps;
-  const float* rope_cos;  // [n_ctx][D/2]
-  const float* rope_sin;
-  const int* pos;         // device position (write slot)
-  uint16_t* k_cache;      // [n_head_kv][n_ctx][D] of this layer
-  uint16_t* v_cache;
-  int n_head, n_head_kv, head_dim, n_ctx;
-};
-hipError_t launch_qk_rope_append(const QkRopeArgs& a, hipStream_t s);
-
+// Fused decode attention of one token (QK-norm, RoPE, f16 append, split-KV
+// attention, merge).  q/k/v are the raw projections of this token.
 struct AttnArgs {
   const float* q;            // [n_head][D]
-  const uint16_t* k_cache;   // [n_head_kv][n_ctx][D]
-  const uint16_t* v_cache;
-  const int* n_kv_dev;       // device count of valid positions = *n_kv_dev + n_kv_add
-  int n_kv_add;
-  int n_kv_host;             // used when n_kv_dev is null
+  const float* k;            // [n_head_kv][D]
+  const float* v;            // [n_head_kv][D]
+  const float* q_norm;       // [D]
+  const float* k_norm;       // [D]
+  float eps;
+  const float* rope_cos;     // [n_ctx][D/2], row `pos` (row 0 when rope_row0)
+  const float* rope_sin;
+  const int* pos;            // device position of this token (its cache slot)
+  uint16_t* k_cache;         // [n_head_kv][n_ctx][D] of this layer
+  uint16_t* v_cache;
   int n_head, n_head_kv, head_dim, n_ctx;
   float scale;
   float* partial;            // [n_head][n_split][D + 2] scratch
+  unsigned int* counter;     // n_head_kv zero-initialised tickets
   float* out;                // [n_head][D]
 };
 int attn_splits(int n_ctx);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
-hipError_t launch_embed(int type, const uint8_t* table, int n_embd, const int32_t* tok, float* x,
+// Decode-step control block in device memory: the token fed to the step, its
+// position, the index into the output token ring, and the packed argmax of the
+// LM head.
+struct StepState {
+  int32_t token;
+  int32_t pos;
+  int32_t step;
+  int32_t pad;
+  unsigned long long key;
+};
+hipError_t launch_step_close(StepState* st, int32_t* out_tokens, int max_steps, hipStream_t s);
+
+// Embedding row of st->token into x; also clears st->key for the LM head.
+hipError_t launch_embed(int type, const uint8_t* table, int n_embd, StepState* st, float* x,
                         hipStream_t s);
 
 }  // namespace knj

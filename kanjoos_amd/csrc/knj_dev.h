@@ -1,0 +1,249 @@
+// kanjoos_amd/csrc/knj_dev.h -- device-side helpers shared by the gfx950 kernels.
+//
+// Conventions: workgroups of 256 threads (4 wave64s); weights are read with
+// 16-byte loads issued before anything that waits on activations, so their HBM
+// latency overlaps the activation staging; activations that every lane of a
+// row needs are kept in registers ("x slice") and reused across the rows a
+// wave processes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../../include/knj_format.h"
+
+namespace knj {
+namespace dev {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float h2f(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits16 & 0xFFFFu));
+}
+
+__device__ __forceinline__ uint16_t f2h(float v) {
+  // v_cvt_f16_f32, round-to-nearest-even (knj_f32_to_f16 semantics)
+  return __builtin_bit_cast(unsigned short, (_Float16)v);
+}
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Sum over the workgroup: wave trees, then the waves in order.  Every thread
+// returns the same value.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  v = group_sum<64>(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.0f;
+  const int nw = (blockDim.x + 63) >> 6;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  __syncthreads();
+  return t;
+}
+
+__device__ __forceinline__ float ld_acquire_f(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_acquire_i(const int* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Last-workgroup-done ticket: every workgroup calls this once after its global
+// writes; exactly one (the last) gets true.  That workgroup then sees every
+// other workgroup's writes.  The counter is returned to zero by the last one.
+__device__ __forceinline__ bool last_block_done(unsigned int* counter, unsigned int nblocks,
+                                                unsigned int* flag_lds) {
+  __threadfence();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const unsigned int t = atomicAdd(counter, 1u);
+    const bool last = (t == nblocks - 1);
+    if (last) atomicExch(counter, 0u);
+    *flag_lds = last ? 1u : 0u;
+  }
+  __syncthreads();
+  const bool last = *flag_lds != 0u;
+  if (last) __threadfence();
+  return last;
+}
+
+// Padded LDS layout of an activation vector: 16 bytes of padding after every 64
+// floats, so the 64-float slices that consecutive lanes read with ds_read_b128
+// start on different banks.
+__device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
+constexpr int xpad_size(int n) { return n + (n >> 6) * 4; }
+
+// Stage x (n <= 4096 floats) into padded LDS, optionally RMS-normalised:
+// xs = x * (1/sqrt(sum(x^2)/n + eps)) * w.  All threads take part.
+__device__ __forceinline__ void stage_x(const float* __restrict__ x,
+                                        const float* __restrict__ nw, float eps, int n, float* xs,
+                                        float* red) {
+  float4 v[4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * threadIdx.x + 1024 * j;
+    if (i < n) {
+      v[j] = *reinterpret_cast<const float4*>(x + i);
+      ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+    }
+  }
+  float scale = 1.0f;
+  if (nw) {
+    ss = block_sum(ss, red);
+    scale = 1.0f / sqrtf(ss / (float)n + eps);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * threadIdx.x + 1024 * j;
+    if (i < n) {
+      float4 o = v[j];
+      if (nw) {
+        const float4 w = *reinterpret_cast<const float4*>(nw + i);
+        o.x = v[j].x * scale * w.x;
+        o.y = v[j].y * scale * w.y;
+        o.z = v[j].z * scale * w.z;
+        o.w = v[j].w * scale * w.w;
+      }
+      *reinterpret_cast<float4*>(xs + xpad(i)) = o;
+    }
+  }
+  __syncthreads();
+}
+
+// ---------------------------------------------------------------- Q4_K slices
+// A slice is one 32-byte code group g of a super-block: sub-blocks 2g (low
+// nibbles) and 2g+1 (high nibbles), 64 weights, plus the block header.
+struct Q4Slice {
+  uint4 h, a, b;
+};
+
+__device__ __forceinline__ Q4Slice q4k_load(const uint8_t* __restrict__ blk, int g) {
+  Q4Slice s;
+  s.h = *reinterpret_cast<const uint4*>(blk);
+  s.a = *reinterpret_cast<const uint4*>(blk + KNJ_Q4K_QS + 32 * g);
+  s.b = *reinterpret_cast<const uint4*>(blk + KNJ_Q4K_QS + 32 * g + 16);
+  return s;
+}
+
+__device__ __forceinline__ void q4k_scale_min(uint32_t w1, uint32_t w2, uint32_t w3, int s,
+                                              uint32_t& sc, uint32_t& mn) {
+  if (s < 4) {
+    sc = (w1 >> (8 * s)) & 63u;
+    mn = (w2 >> (8 * s)) & 63u;
+  } else {
+    const int t = s - 4;
+    const uint32_t lo = (w3 >> (8 * t)) & 0xFFu;
+    sc = (lo & 15u) | (((w1 >> (8 * t + 6)) & 3u) << 4);
+    mn = (lo >> 4) | (((w2 >> (8 * t + 6)) & 3u) << 4);
+  }
+}
+
+// The 64 activations of a slice, in registers, with the two sub-block sums.
+struct XSlice {
+  float v[64];
+  float s0, s1;
+};
+
+__device__ __forceinline__ void xslice_load(const float* xs_pad, int slice, XSlice& x) {
+  const float* p = xs_pad + 68 * slice;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(p + 4 * k);
+    x.v[4 * k] = t.x;
+    x.v[4 * k + 1] = t.y;
+    x.v[4 * k + 2] = t.z;
+    x.v[4 * k + 3] = t.w;
+  }
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int l = 0; l < 32; ++l) {
+    a += x.v[l];
+    b += x.v[32 + l];
+  }
+  x.s0 = a;
+  x.s1 = b;
+}
+
+__device__ __forceinline__ void q4k_codes16(uint4 q, const float* xlo, const float* xhi, float& slo,
+                                            float& shi) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t lo = w[k] & 0x0F0F0F0Fu;
+    const uint32_t hi = (w[k] >> 4) & 0x0F0F0F0Fu;
+    slo += (float)(lo & 0xFFu) * xlo[4 * k];
+    slo += (float)((lo >> 8) & 0xFFu) * xlo[4 * k + 1];
+    slo += (float)((lo >> 16) & 0xFFu) * xlo[4 * k + 2];
+    slo += (float)(lo >> 24) * xlo[4 * k + 3];
+    shi += (float)(hi & 0xFFu) * xhi[4 * k];
+    shi += (float)((hi >> 8) & 0xFFu) * xhi[4 * k + 1];
+    shi += (float)((hi >> 16) & 0xFFu) * xhi[4 * k + 2];
+    shi += (float)(hi >> 24) * xhi[4 * k + 3];
+  }
+}
+
+// sum over the slice's 64 weights of w*x, in the factored form
+// d1*sum(q*x) - m1*sum(x) per sub-block (dot_q4_k, dequant.cpp:954-984)
+__device__ __forceinline__ float q4k_dot(const Q4Slice& w, int g, const XSlice& x) {
+  float s0 = 0.0f, s1 = 0.0f;
+  q4k_codes16(w.a, x.v, x.v + 32, s0, s1);
+  q4k_codes16(w.b, x.v + 16, x.v + 48, s0, s1);
+  const float d = h2f(w.h.x), dmin = h2f(w.h.x >> 16);
+  uint32_t sc0, m0, sc1, m1;
+  q4k_scale_min(w.h.y, w.h.z, w.h.w, 2 * g, sc0, m0);
+  q4k_scale_min(w.h.y, w.h.z, w.h.w, 2 * g + 1, sc1, m1);
+  const float d0 = d * (float)sc0, dm0 = dmin * (float)m0;
+  const float d1 = d * (float)sc1, dm1 = dmin * (float)m1;
+  return (d0 * s0 - dm0 * x.s0) + (d1 * s1 - dm1 * x.s1);
+}
+
+// ---------------------------------------------------------------- Q6_K slices
+// Quarter t (0..3) of half hf (0..1) of one Q6_K block: 32 weights, two
+// 16-weight scale groups.  Q6_K blocks are 210 bytes (2-byte aligned only), so
+// the codes are read as bytes.
+__device__ __forceinline__ float q6k_quarter(const uint8_t* __restrict__ blk, int hf, int t,
+                                             const float* xq) {
+  const float d = h2f((uint32_t)blk[KNJ_Q6K_D] | ((uint32_t)blk[KNJ_Q6K_D + 1] << 8));
+  const uint8_t* ql = blk + KNJ_Q6K_QL + 64 * hf + 32 * (t & 1);
+  const uint8_t* qh = blk + KNJ_Q6K_QH + 32 * hf;
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll 8
+  for (int l = 0; l < 32; ++l) {
+    const uint32_t lb = ql[l];
+    const uint32_t lo4 = (t < 2) ? (lb & 15u) : (lb >> 4);
+    const uint32_t hi2 = ((uint32_t)qh[l] >> (2 * t)) & 3u;
+    const float v = (float)((int)(lo4 | (hi2 << 4)) - 32) * xq[l];
+    if (l < 16) s0 += v;
+    else s1 += v;
+  }
+  const int8_t* sc = reinterpret_cast<const int8_t*>(blk + KNJ_Q6K_SC) + 8 * hf + 2 * t;
+  return d * ((float)sc[0] * s0 + (float)sc[1] * s1);
+}
+
+__device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
+  uint32_t u = __float_as_uint(v);
+  u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((unsigned long long)u << 32) | (unsigned long long)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ int argmax_index(unsigned long long key) {
+  return (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
+}
+
+}  // namespace dev
+}  // namespace knj

@@ -252,6 +252,8 @@ int knj_moe_router(const float* x, const float* norm_w, float eps, const float* 
   if (rc) return rc;
   rc = check_moe_shape(n_embd, 256, n_expert, k);
   if (rc) return rc;
+  KNJ_CHECK_ARG(n_embd <= 4096, "router: n_embd must be at most 4096");
+  if (rc) return rc;
   KNJ_CHECK_ARG(x && router_w && hx && logits && topk_idx && topk_w, "null pointer");
   RouterArgs a{x, norm_w, eps, router_w, n_embd, n_expert, k, hx, logits, topk_idx, topk_w,
                device_counters()};
@@ -268,6 +270,7 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
   if (rc) return rc;
   rc = check_moe_shape(n_embd, n_ff, n_expert, k);
   if (rc) return rc;
+  KNJ_CHECK_ARG(n_embd <= 4096, "router: n_embd must be at most 4096");
   KNJ_CHECK_ARG(type_gate_up == KNJ_TYPE_Q4_K, "gate/up experts must be Q4_K");
   KNJ_CHECK_ARG(type_down == KNJ_TYPE_Q4_K || type_down == KNJ_TYPE_Q6_K,
                 "down experts must be Q4_K or Q6_K");
@@ -289,61 +292,44 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
   return KNJ_OK;
 }
 
-int knj_qk_norm_rope_append(float* q, const float* k, const float* v, const float* q_norm,
-                            const float* k_norm, float eps, float rope_base, int pos, int n_head,
-                            int n_head_kv, int head_dim, int n_ctx, uint16_t* k_cache,
-                            uint16_t* v_cache, void* stream) {
+int knj_attention_step(const float* q, const float* k, const float* v, const float* q_norm,
+                       const float* k_norm, float eps, float rope_base, int pos, int n_head,
+                       int n_head_kv, int head_dim, int n_ctx, uint16_t* k_cache, uint16_t* v_cache,
+                       float* out, void* stream) {
   int rc = require_open();
   if (rc) return rc;
-  KNJ_CHECK_ARG(q && k && v && q_norm && k_norm && k_cache && v_cache, "null pointer");
-  KNJ_CHECK_ARG(head_dim > 0 && head_dim <= 512 && head_dim % 2 == 0, "head_dim must be even, <= 512");
-  KNJ_CHECK_ARG(n_head > 0 && n_head_kv > 0 && n_head % n_head_kv == 0, "bad head counts");
+  KNJ_CHECK_ARG(q && k && v && q_norm && k_norm && k_cache && v_cache && out, "null pointer");
+  KNJ_CHECK_ARG(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128");
+  KNJ_CHECK_ARG(n_head_kv > 0 && n_head_kv <= 64 && n_head % n_head_kv == 0 &&
+                    n_head / n_head_kv <= 8,
+                "n_head must be a multiple of n_head_kv (<= 64) with a group of at most 8");
   KNJ_CHECK_ARG(pos >= 0 && pos < n_ctx, "position outside the cache");
   hipStream_t s = (hipStream_t)stream;
-  // a one-row cos/sin table for this position, computed like the model's table
+  // cos/sin of this position, computed like the model's table (model.cpp:227-230, 278-279)
   const int half = head_dim / 2;
-  std::vector<float> tab(2 * (size_t)half);
+  std::vector<float> tab(2 * (size_t)half + 64);
   for (int i = 0; i < half; ++i) {
     const float inv = std::pow(rope_base, -2.0f * (float)i / (float)head_dim);
     const float th = (float)pos * inv;
     tab[i] = std::cos(th);
     tab[half + i] = std::sin(th);
   }
-  uint8_t* scr = (uint8_t*)device_scratch(256 + 2 * (uint64_t)half * 4, s);
-  if (!scr) return hip_fail(hipErrorOutOfMemory, "scratch");
-  int* dpos = (int*)scr;
-  float* dtab = (float*)(scr + 256);
-  const int zero = 0;
-  KNJ_HIP(hipMemcpyAsync(dtab, tab.data(), tab.size() * 4, hipMemcpyHostToDevice, s));
-  KNJ_HIP(hipMemcpyAsync(dpos, &zero, 4, hipMemcpyHostToDevice, s));
-  // the kernel indexes the table by the device position (0 here) and writes the
-  // cache slot at that position, so shift the cache base to slot `pos`
-  QkRopeArgs a{q, k, v, q_norm, k_norm, eps, dtab, dtab + half, dpos,
-               k_cache + (uint64_t)pos * head_dim, v_cache + (uint64_t)pos * head_dim,
-               n_head, n_head_kv, head_dim, n_ctx};
-  KNJ_HIP(launch_qk_rope_append(a, s));
-  KNJ_HIP(hipStreamSynchronize(s));  // the host table must stay alive until the copy ran
-  return KNJ_OK;
-}
-
-int knj_attention_decode(const float* q, const uint16_t* k_cache, const uint16_t* v_cache,
-                         int n_head, int n_head_kv, int head_dim, int n_ctx, int n_kv, float scale,
-                         float* out, void* stream) {
-  int rc = require_open();
-  if (rc) return rc;
-  KNJ_CHECK_ARG(q && k_cache && v_cache && out, "null pointer");
-  KNJ_CHECK_ARG(head_dim > 0 && head_dim <= 128 && head_dim % 8 == 0, "head_dim must be <= 128, multiple of 8");
-  KNJ_CHECK_ARG(n_head_kv > 0 && n_head % n_head_kv == 0 && n_head / n_head_kv <= 8,
-                "GQA group must be <= 8");
-  KNJ_CHECK_ARG(n_kv > 0 && n_kv <= n_ctx, "n_kv must be in [1, n_ctx]");
-  hipStream_t s = (hipStream_t)stream;
+  std::memcpy(&tab[2 * half], &pos, sizeof(int));
   const int n_split = attn_splits(n_ctx);
-  const uint64_t bytes = (uint64_t)n_head * n_split * (head_dim + 2) * 4;
-  float* part = (float*)device_scratch(bytes, s);
-  if (!part) return hip_fail(hipErrorOutOfMemory, "scratch");
-  AttnArgs a{q, k_cache, v_cache, nullptr, 0, n_kv, n_head, n_head_kv, head_dim, n_ctx, scale,
-             part, out};
+  const uint64_t part_bytes = (uint64_t)n_head * n_split * (head_dim + 2) * 4;
+  uint8_t* scr = (uint8_t*)device_scratch(1024 + part_bytes, s);
+  if (!scr) return hip_fail(hipErrorOutOfMemory, "scratch");
+  float* dtab = (float*)scr;
+  int* dpos = (int*)(scr + 2 * half * 4);
+  KNJ_HIP(hipMemcpyAsync(scr, tab.data(), 2 * half * 4 + 4, hipMemcpyHostToDevice, s));
+  // the kernel reads row `pos` of the table: point the table base `pos` rows back
+  const float* cs = (const float*)((uintptr_t)dtab - (uintptr_t)pos * half * 4);
+  const float* sn = (const float*)((uintptr_t)(dtab + half) - (uintptr_t)pos * half * 4);
+  AttnArgs a{q, k, v, q_norm, k_norm, eps, cs, sn, dpos, k_cache, v_cache, n_head, n_head_kv,
+             head_dim, n_ctx, 1.0f / std::sqrt((float)head_dim), (float*)(scr + 1024),
+             device_counters() + 64, out};
   KNJ_HIP(launch_attention(a, s));
+  KNJ_HIP(hipStreamSynchronize(s));  // the host table must outlive the copy
   return KNJ_OK;
 }
 

@@ -1,0 +1,409 @@
+// kanjoos_amd/csrc/knj_gemv.hip -- batch-1 GEMV kernels (Q4_K, Q6_K, BF16, F32).
+//
+// y[j] = sum_i W[j][i] * x[i] over rows j of a ggml 2-D weight (one row per
+// output, n_in weights each), the device side of Model::matmul at m == 1
+// (/root/reference/src/model/model.cpp:326-380).  Optional fused RMSNorm of x
+// and residual add.
+//
+// Q4_K rows: LPR lanes per row, one 64-weight slice per lane (n_in <= 64*LPR),
+// RS row-steps per wave.  Every lane issues the 16-byte loads of all its rows
+// before the activation staging starts, keeps its 64 activations in registers
+// and reuses them for each row.
+#include "knj_common.h"
+#include "knj_dev.h"
+
+namespace knj {
+namespace {
+
+using namespace dev;
+
+template <int LPR, int RS>
+__global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__ w, int n_in,
+                                                     int n_out, const float* __restrict__ x,
+                                                     const float* __restrict__ nw, float eps,
+                                                     const float* __restrict__ resid,
+                                                     float* __restrict__ y) {
+  __shared__ float xs[xpad_size(4096)];
+  __shared__ float red[8];
+  constexpr int RPW = 64 / LPR;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % LPR, rsub = lane / LPR;
+  const int nslices = n_in >> 6;
+  const uint64_t rb = (uint64_t)(n_in >> 8) * KNJ_Q4K_BLOCK;
+  const int row0 = (blockIdx.x * (kBlock / 64) + wave) * (RS * RPW);
+  const bool active = sub < nslices;
+  const int b = sub >> 2, g = sub & 3;
+  Q4Slice q[RS];
+#pragma unroll
+  for (int st = 0; st < RS; ++st) {
+    const int row = row0 + st * RPW + rsub;
+    if (active && row < n_out) q[st] = q4k_load(w + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+  }
+  stage_x(x, nw, eps, n_in, xs, red);
+  XSlice xv;
+  if (active) xslice_load(xs, sub, xv);
+#pragma unroll
+  for (int st = 0; st < RS; ++st) {
+    const int row = row0 + st * RPW + rsub;
+    float acc = (active && row < n_out) ? q4k_dot(q[st], g, xv) : 0.0f;
+    acc = group_sum<LPR>(acc);
+    if (sub == 0 && row < n_out) y[row] = resid ? resid[row] + acc : acc;
+  }
+}
+
+// Q4_K rows wider than 64 slices (n_in > 4096, up to 16384): the activations
+// stay in LDS and each lane walks several slices per row.
+__global__ __launch_bounds__(kBlock) void k_gemv_q4k_wide(const uint8_t* __restrict__ w, int n_in,
+                                                          int n_out, const float* __restrict__ x,
+                                                          const float* __restrict__ nw, float eps,
+                                                          const float* __restrict__ resid,
+                                                          float* __restrict__ y) {
+  extern __shared__ float xsw[];
+  __shared__ float red[8];
+  float* xs = xsw;
+  // stage (up to 16384 floats, padded), optional RMSNorm
+  float ss = 0.0f;
+  for (int i = 4 * threadIdx.x; i < n_in; i += 4 * kBlock) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    *reinterpret_cast<float4*>(xs + xpad(i)) = v;
+  }
+  if (nw) {
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)n_in + eps);
+    for (int i = 4 * threadIdx.x; i < n_in; i += 4 * kBlock) {
+      float4 v = *reinterpret_cast<float4*>(xs + xpad(i));
+      const float4 wv = *reinterpret_cast<const float4*>(nw + i);
+      v.x = v.x * scale * wv.x;
+      v.y = v.y * scale * wv.y;
+      v.z = v.z * scale * wv.z;
+      v.w = v.w * scale * wv.w;
+      *reinterpret_cast<float4*>(xs + xpad(i)) = v;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nslices = n_in >> 6;
+  const uint64_t rb = (uint64_t)(n_in >> 8) * KNJ_Q4K_BLOCK;
+  for (int row = blockIdx.x * (kBlock / 64) + wave; row < n_out; row += gridDim.x * (kBlock / 64)) {
+    float acc = 0.0f;
+    for (int s = lane; s < nslices; s += 64) {
+      XSlice xv;
+      xslice_load(xs, s, xv);
+      const Q4Slice q = q4k_load(w + (uint64_t)row * rb + (uint64_t)(s >> 2) * KNJ_Q4K_BLOCK, s & 3);
+      acc += q4k_dot(q, s & 3, xv);
+    }
+    acc = group_sum<64>(acc);
+    if (lane == 0) y[row] = resid ? resid[row] + acc : acc;
+  }
+}
+
+// Q6_K rows: 8 quarters per block, LPR lanes per row, activations in LDS.
+template <int LPR>
+__global__ __launch_bounds__(kBlock) void k_gemv_q6k(const uint8_t* __restrict__ w, int n_in,
+                                                     int n_out, const float* __restrict__ x,
+                                                     const float* __restrict__ nw, float eps,
+                                                     const float* __restrict__ resid,
+                                                     float* __restrict__ y,
+                                                     unsigned long long* argmax) {
+  extern __shared__ float xsq[];
+  __shared__ float red[8];
+  float ss = 0.0f;
+  for (int i = 4 * threadIdx.x; i < n_in; i += 4 * kBlock) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    *reinterpret_cast<float4*>(xsq + i) = v;
+  }
+  if (nw) {
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)n_in + eps);
+    for (int i = 4 * threadIdx.x; i < n_in; i += 4 * kBlock) {
+      float4 v = *reinterpret_cast<float4*>(xsq + i);
+      const float4 wv = *reinterpret_cast<const float4*>(nw + i);
+      v.x = v.x * scale * wv.x;
+      v.y = v.y * scale * wv.y;
+      v.z = v.z * scale * wv.z;
+      v.w = v.w * scale * wv.w;
+      *reinterpret_cast<float4*>(xsq + i) = v;
+    }
+  }
+  __syncthreads();
+  const int nb = n_in / KNJ_QK, nq = 8 * nb;
+  const uint64_t rb = (uint64_t)nb * KNJ_Q6K_BLOCK;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % LPR, rsub = lane / LPR;
+  constexpr int RPW = 64 / LPR;
+  const int stride = gridDim.x * (kBlock / 64) * RPW;
+  unsigned long long best = 0;
+  for (int row0 = (blockIdx.x * (kBlock / 64) + wave) * RPW; row0 < n_out; row0 += stride) {
+    const int row = row0 + rsub;
+    float acc = 0.0f;
+    if (row < n_out) {
+      const uint8_t* rp = w + (uint64_t)row * rb;
+      for (int s = sub; s < nq; s += LPR) {
+        const int bb = s >> 3;
+        acc += q6k_quarter(rp + (uint64_t)bb * KNJ_Q6K_BLOCK, (s >> 2) & 1, s & 3,
+                           xsq + bb * KNJ_QK + 128 * ((s >> 2) & 1) + 32 * (s & 3));
+      }
+    }
+    acc = group_sum<LPR>(acc);
+    if (sub == 0 && row < n_out) {
+      const float v = resid ? resid[row] + acc : acc;
+      y[row] = v;
+      if (argmax) {
+        const unsigned long long k = argmax_key(v, row);
+        best = k > best ? k : best;
+      }
+    }
+  }
+  if (argmax) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const unsigned long long t = __shfl_xor(best, o, 64);
+      best = t > best ? t : best;
+    }
+    if (lane == 0 && best) atomicMax(argmax, best);
+  }
+}
+
+// BF16 rows (the LM head): 8 weights per lane per 16-byte load, NJ loads per
+// row (n_in = 512*NJ); the lane's 8*NJ activations live in registers; RS rows
+// per step with the next step's loads issued before the current rows are
+// reduced.  Optional packed argmax of y.
+template <int NJ, int RS>
+__global__ __launch_bounds__(kBlock) void k_gemv_bf16(const uint8_t* __restrict__ w, int n_in,
+                                                      int n_out, const float* __restrict__ x,
+                                                      const float* __restrict__ nw, float eps,
+                                                      const float* __restrict__ resid,
+                                                      float* __restrict__ y,
+                                                      unsigned long long* argmax) {
+  __shared__ float xs[xpad_size(4096)];
+  __shared__ float red[8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nwaves = gridDim.x * (kBlock / 64);
+  const int wave_g = blockIdx.x * (kBlock / 64) + wave;
+  const uint64_t rb = (uint64_t)n_in * 2;
+  uint4 cur[RS][NJ];
+  int base = wave_g * RS;
+#pragma unroll
+  for (int r = 0; r < RS; ++r)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+      if (base + r < n_out)
+        cur[r][j] = *reinterpret_cast<const uint4*>(w + (uint64_t)(base + r) * rb + 16 * (lane + 64 * j));
+  stage_x(x, nw, eps, n_in, xs, red);
+  float xv[NJ][8];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int i = 8 * lane + 512 * j;
+    const float4 a = *reinterpret_cast<const float4*>(xs + xpad(i));
+    const float4 c = *reinterpret_cast<const float4*>(xs + xpad(i + 4));
+    xv[j][0] = a.x; xv[j][1] = a.y; xv[j][2] = a.z; xv[j][3] = a.w;
+    xv[j][4] = c.x; xv[j][5] = c.y; xv[j][6] = c.z; xv[j][7] = c.w;
+  }
+  unsigned long long best = 0;
+  for (; base < n_out; base += nwaves * RS) {
+    const int nbase = base + nwaves * RS;
+    uint4 nxt[RS][NJ];
+#pragma unroll
+    for (int r = 0; r < RS; ++r)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j)
+        if (nbase + r < n_out)
+          nxt[r][j] = *reinterpret_cast<const uint4*>(w + (uint64_t)(nbase + r) * rb + 16 * (lane + 64 * j));
+#pragma unroll
+    for (int r = 0; r < RS; ++r) {
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const uint4 v = cur[r][j];
+        acc += __uint_as_float(v.x << 16) * xv[j][0];
+        acc += __uint_as_float(v.x & 0xFFFF0000u) * xv[j][1];
+        acc += __uint_as_float(v.y << 16) * xv[j][2];
+        acc += __uint_as_float(v.y & 0xFFFF0000u) * xv[j][3];
+        acc += __uint_as_float(v.z << 16) * xv[j][4];
+        acc += __uint_as_float(v.z & 0xFFFF0000u) * xv[j][5];
+        acc += __uint_as_float(v.w << 16) * xv[j][6];
+        acc += __uint_as_float(v.w & 0xFFFF0000u) * xv[j][7];
+      }
+      acc = group_sum<64>(acc);
+      const int row = base + r;
+      if (row < n_out) {
+        const float o = resid ? resid[row] + acc : acc;
+        if (lane == 0) y[row] = o;
+        if (argmax) {
+          const unsigned long long k = argmax_key(o, row);
+          best = k > best ? k : best;
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RS; ++r)
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) cur[r][j] = nxt[r][j];
+  }
+  if (argmax && lane == 0 && best) atomicMax(argmax, best);
+}
+
+// BF16 / F32 rows of any width (multiple of 8 / 4): one wave per row.
+template <bool BF16>
+__global__ __launch_bounds__(kBlock) void k_gemv_plain(const uint8_t* __restrict__ w, int n_in,
+                                                       int n_out, const float* __restrict__ x,
+                                                       const float* __restrict__ nw, float eps,
+                                                       const float* __restrict__ resid,
+                                                       float* __restrict__ y,
+                                                       unsigned long long* argmax) {
+  extern __shared__ float xsp[];
+  __shared__ float red[8];
+  float ss = 0.0f;
+  for (int i = 4 * threadIdx.x; i < n_in; i += 4 * kBlock) {
+    const float4 v = *reinterpret_cast<const float4*>(x + i);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    *reinterpret_cast<float4*>(xsp + i) = v;
+  }
+  if (nw) {
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)n_in + eps);
+    for (int i = 4 * threadIdx.x; i < n_in; i += 4 * kBlock) {
+      float4 v = *reinterpret_cast<float4*>(xsp + i);
+      const float4 wv = *reinterpret_cast<const float4*>(nw + i);
+      v.x = v.x * scale * wv.x;
+      v.y = v.y * scale * wv.y;
+      v.z = v.z * scale * wv.z;
+      v.w = v.w * scale * wv.w;
+      *reinterpret_cast<float4*>(xsp + i) = v;
+    }
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  constexpr int PER = BF16 ? 8 : 4;
+  const uint64_t rb = (uint64_t)n_in * (BF16 ? 2 : 4);
+  unsigned long long best = 0;
+  for (int row = blockIdx.x * (kBlock / 64) + wave; row < n_out; row += gridDim.x * (kBlock / 64)) {
+    const uint8_t* rp = w + (uint64_t)row * rb;
+    float acc = 0.0f;
+    for (int i0 = lane * PER; i0 < n_in; i0 += 64 * PER) {
+      const uint4 v = *reinterpret_cast<const uint4*>(rp + (uint64_t)i0 * (BF16 ? 2 : 4));
+      const float4 xa = *reinterpret_cast<const float4*>(xsp + i0);
+      if (BF16) {
+        const float4 xb = *reinterpret_cast<const float4*>(xsp + i0 + 4);
+        acc += __uint_as_float(v.x << 16) * xa.x;
+        acc += __uint_as_float(v.x & 0xFFFF0000u) * xa.y;
+        acc += __uint_as_float(v.y << 16) * xa.z;
+        acc += __uint_as_float(v.y & 0xFFFF0000u) * xa.w;
+        acc += __uint_as_float(v.z << 16) * xb.x;
+        acc += __uint_as_float(v.z & 0xFFFF0000u) * xb.y;
+        acc += __uint_as_float(v.w << 16) * xb.z;
+        acc += __uint_as_float(v.w & 0xFFFF0000u) * xb.w;
+      } else {
+        acc += __uint_as_float(v.x) * xa.x;
+        acc += __uint_as_float(v.y) * xa.y;
+        acc += __uint_as_float(v.z) * xa.z;
+        acc += __uint_as_float(v.w) * xa.w;
+      }
+    }
+    acc = group_sum<64>(acc);
+    const float out = resid ? resid[row] + acc : acc;
+    if (lane == 0) y[row] = out;
+    if (argmax) {
+      const unsigned long long k = argmax_key(out, row);
+      best = k > best ? k : best;
+    }
+  }
+  if (argmax && lane == 0 && best) atomicMax(argmax, best);
+}
+
+// The decode step's last launch closes the step: after every workgroup has
+// folded its rows into the packed argmax, the last one turns it into the next
+// token (first maximum wins, /root/reference/src/cli/main.cpp:126-132) and
+// advances the device-side position.
+__global__ void k_step_close(StepState* st, int32_t* out_tokens, int max_steps) {
+  const int tok = argmax_index(st->key);
+  if (st->step < max_steps) out_tokens[st->step] = tok;
+  st->step += 1;
+  st->token = tok;
+  st->pos += 1;
+}
+
+int pow2_at_least(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
+  if (a.type == KNJ_TYPE_Q4_K) {
+    const int nslices = a.n_in / 64;
+    if (nslices <= 64) {
+      const int lpr = pow2_at_least(nslices);
+      const int rpw = 64 / lpr;
+      const int steps_total = (a.n_out + rpw - 1) / rpw;  // wave-steps
+      const int rs = steps_total <= 4 * 1024 ? 1 : (steps_total <= 4 * 2048 ? 2 : 4);
+      const int grid = (steps_total + 4 * rs - 1) / (4 * rs);
+#define GQ(L, R)                                                                            \
+  if (lpr == L && rs == R) {                                                                \
+    hipLaunchKernelGGL((k_gemv_q4k<L, R>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,    \
+                       a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y);                        \
+    return hipGetLastError();                                                               \
+  }
+      GQ(4, 1) GQ(4, 2) GQ(4, 4) GQ(8, 1) GQ(8, 2) GQ(8, 4) GQ(16, 1) GQ(16, 2) GQ(16, 4)
+      GQ(32, 1) GQ(32, 2) GQ(32, 4) GQ(64, 1) GQ(64, 2) GQ(64, 4)
+#undef GQ
+      return hipErrorInvalidValue;
+    }
+    const size_t lds = (size_t)xpad_size(a.n_in) * 4;
+    const int grid = std::max(1, std::min(2048, (a.n_out + 3) / 4));
+    hipLaunchKernelGGL(k_gemv_q4k_wide, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, a.x,
+                       a.norm_w, a.eps, a.resid, a.y);
+    return hipGetLastError();
+  }
+  if (a.type == KNJ_TYPE_Q6_K) {
+    const int lpr = std::min(64, pow2_at_least(8 * (a.n_in / KNJ_QK)));
+    const size_t lds = (size_t)a.n_in * 4;
+    const int rows_per_block = 4 * (64 / lpr);
+    const int grid = std::max(1, std::min(4096, (a.n_out + rows_per_block - 1) / rows_per_block));
+#define G6(L)                                                                                 \
+  if (lpr == L) {                                                                             \
+    hipLaunchKernelGGL(k_gemv_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, \
+                       a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);                     \
+    return hipGetLastError();                                                                 \
+  }
+    G6(8) G6(16) G6(32) G6(64)
+#undef G6
+    return hipErrorInvalidValue;
+  }
+  if (a.type == KNJ_TYPE_BF16 && a.n_in % 512 == 0 && a.n_in <= 4096) {
+    const int nj = a.n_in / 512;
+    constexpr int RS = 4;
+    const int waves_needed = (a.n_out + RS - 1) / RS;
+    const int grid = std::max(1, std::min(1024, (waves_needed + 3) / 4));
+#define GB(J)                                                                                   \
+  if (nj == J) {                                                                                \
+    hipLaunchKernelGGL((k_gemv_bf16<J, RS>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,     \
+                       a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);             \
+    return hipGetLastError();                                                                   \
+  }
+    GB(1) GB(2) GB(4) GB(8)
+#undef GB
+    if (nj == 3 || nj > 4) { /* fall through to the generic kernel */ }
+  }
+  const size_t lds = (size_t)a.n_in * 4;
+  const int grid = std::max(1, std::min(4096, (a.n_out + 3) / 4));
+  if (a.type == KNJ_TYPE_BF16) {
+    hipLaunchKernelGGL(k_gemv_plain<true>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out,
+                       a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
+  } else {
+    hipLaunchKernelGGL(k_gemv_plain<false>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in,
+                       a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_step_close(StepState* st, int32_t* out_tokens, int max_steps, hipStream_t s) {
+  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(1), 0, s, st, out_tokens, max_steps);
+  return hipGetLastError();
+}
+
+}  // namespace knj

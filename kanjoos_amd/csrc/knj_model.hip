@@ -15,6 +15,7 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -59,26 +60,6 @@ __global__ void k_fill_ones(float* p, uint64_t n) {
   if (i < n) p[i] = 1.0f;
 }
 
-// ----------------------------------------------------------- step bookkeeping
-
-struct StepState {
-  int32_t token;              // token fed to the next step
-  int32_t pos;                // position of the next step
-  int32_t step;               // index into out_tokens
-  int32_t pad;
-  unsigned long long key;     // packed argmax of the LM head
-};
-
-__global__ void k_step_begin(StepState* st) { st->key = 0ull; }
-
-__global__ void k_step_end(StepState* st, int32_t* out_tokens, int max_steps) {
-  const int32_t tok = (int32_t)(0xFFFFFFFFu - (uint32_t)(st->key & 0xFFFFFFFFull));
-  if (st->step < max_steps) out_tokens[st->step] = tok;
-  st->step += 1;
-  st->token = tok;
-  st->pos += 1;
-}
-
 }  // namespace
 }  // namespace knj
 
@@ -104,6 +85,7 @@ struct knj_model {
   int pos = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  bool use_graph = true;  // KNJ_NO_GRAPH=1 launches the step's kernels directly
   std::vector<void*> owned;
 };
 
@@ -118,11 +100,12 @@ int alloc(knj_model* m, void** p, uint64_t bytes) {
 int validate(const knj_model_config* c) {
   KNJ_CHECK_ARG(c, "null config");
   KNJ_CHECK_ARG(c->n_layer > 0 && c->n_embd > 0 && c->n_vocab > 0, "empty model");
-  KNJ_CHECK_ARG(c->n_embd % 256 == 0 && c->n_embd <= 16384, "n_embd must be a multiple of 256, <= 16384");
-  KNJ_CHECK_ARG(c->head_dim > 0 && c->head_dim <= 128 && c->head_dim % 8 == 0,
-                "head_dim must be a multiple of 8, <= 128");
-  KNJ_CHECK_ARG(c->n_head_kv > 0 && c->n_head % c->n_head_kv == 0 && c->n_head / c->n_head_kv <= 8,
-                "n_head must be a multiple of n_head_kv with a group of at most 8");
+  KNJ_CHECK_ARG(c->n_embd % 256 == 0 && c->n_embd <= 4096, "n_embd must be a multiple of 256, <= 4096");
+  KNJ_CHECK_ARG(c->head_dim == 64 || c->head_dim == 128, "head_dim must be 64 or 128");
+  KNJ_CHECK_ARG(c->n_head_kv > 0 && c->n_head_kv <= 64 && c->n_head % c->n_head_kv == 0 &&
+                    c->n_head / c->n_head_kv <= 8,
+                "n_head must be a multiple of n_head_kv (<= 64) with a group of at most 8");
+  KNJ_CHECK_ARG((int64_t)c->n_head * c->head_dim <= 16384, "q_dim must be at most 16384");
   KNJ_CHECK_ARG(((int64_t)c->n_head * c->head_dim) % 256 == 0, "q_dim must be a multiple of 256");
   KNJ_CHECK_ARG(c->n_ff > 0 && c->n_ff % 256 == 0, "n_ff must be a multiple of 256");
   KNJ_CHECK_ARG(c->n_expert > 0 && c->n_expert <= 256, "n_expert must be in [1, 256]");
@@ -171,8 +154,9 @@ int setup(knj_model* m) {
   if ((rc = alloc(m, (void**)&m->st, sizeof(StepState)))) return rc;
   m->max_steps = std::max(c.n_ctx, 1);
   if ((rc = alloc(m, (void**)&m->out_tokens, (uint64_t)m->max_steps * 4))) return rc;
-  if ((rc = alloc(m, (void**)&m->counter, 256))) return rc;
-  KNJ_HIP(hipMemset(m->counter, 0, 256));
+  // tickets: [0] router, [64 + h] attention of kv head h
+  if ((rc = alloc(m, (void**)&m->counter, 4096))) return rc;
+  KNJ_HIP(hipMemset(m->counter, 0, 4096));
   KNJ_HIP(hipMemset(m->kv_k, 0, kv * 2));
   KNJ_HIP(hipMemset(m->kv_v, 0, kv * 2));
   KNJ_HIP(hipMemset(m->st, 0, sizeof(StepState)));
@@ -261,13 +245,11 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
                reinterpret_cast<const float*>(img + lo.attn_norm), c.rms_eps, nullptr, m->qkv, nullptr};
   KNJ_HIP(launch_gemv(qkv, s));
   const uint64_t kv_layer = (uint64_t)il * c.n_head_kv * c.n_ctx * D;
-  QkRopeArgs qr{m->qkv, m->qkv + QD, m->qkv + QD + KVD,
-                reinterpret_cast<const float*>(img + lo.q_norm),
-                reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos, m->rope_sin,
-                &m->st->pos, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head, c.n_head_kv, D, c.n_ctx};
-  KNJ_HIP(launch_qk_rope_append(qr, s));
-  AttnArgs at{m->qkv, m->kv_k + kv_layer, m->kv_v + kv_layer, &m->st->pos, 1, 0, c.n_head, c.n_head_kv,
-              D, c.n_ctx, 1.0f / std::sqrt((float)D), m->attn_part, m->ctx};
+  AttnArgs at{m->qkv, m->qkv + QD, m->qkv + QD + KVD,
+              reinterpret_cast<const float*>(img + lo.q_norm),
+              reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos, m->rope_sin,
+              &m->st->pos, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head, c.n_head_kv, D, c.n_ctx,
+              1.0f / std::sqrt((float)D), m->attn_part, m->counter + 64, m->ctx};
   KNJ_HIP(launch_attention(at, s));
   GemvArgs o{c.type_attn, img + lo.wo, QD, H, m->ctx, nullptr, 0.0f, m->x, m->x, nullptr};
   KNJ_HIP(launch_gemv(o, s));
@@ -287,28 +269,27 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
 
 int enqueue_step(knj_model* m, hipStream_t s) {
   const knj_model_config& c = m->c;
-  hipLaunchKernelGGL(k_step_begin, dim3(1), dim3(1), 0, s, m->st);
-  KNJ_HIP(hipGetLastError());
-  KNJ_HIP(launch_embed(c.type_embd, m->image + m->off_embd, c.n_embd, &m->st->token, m->x, s));
+  KNJ_HIP(launch_embed(c.type_embd, m->image + m->off_embd, c.n_embd, m->st, m->x, s));
   for (int il = 0; il < c.n_layer; ++il) {
     int rc = enqueue_layer(m, il, s);
     if (rc) return rc;
   }
-  GemvArgs head{c.type_head, m->image + m->off_head, c.n_embd, c.n_vocab, m->x,
-                reinterpret_cast<const float*>(m->image + m->off_onorm), c.rms_eps, nullptr,
-                m->logits, &m->st->key};
   if (c.type_head == KNJ_TYPE_Q4_K) {
     set_error("a Q4_K LM head has no fused argmax; use BF16 or Q6_K");
     return KNJ_E_ARG;
   }
+  GemvArgs head{c.type_head, m->image + m->off_head, c.n_embd, c.n_vocab, m->x,
+                reinterpret_cast<const float*>(m->image + m->off_onorm), c.rms_eps, nullptr,
+                m->logits, &m->st->key};
   KNJ_HIP(launch_gemv(head, s));
-  hipLaunchKernelGGL(k_step_end, dim3(1), dim3(1), 0, s, m->st, m->out_tokens, m->max_steps);
-  KNJ_HIP(hipGetLastError());
+  KNJ_HIP(launch_step_close(m->st, m->out_tokens, m->max_steps, s));
   return KNJ_OK;
 }
 
 int ensure_graph(knj_model* m) {
-  if (m->exec) return KNJ_OK;
+  const char* ng = std::getenv("KNJ_NO_GRAPH");
+  m->use_graph = !(ng && ng[0] == '1');
+  if (!m->use_graph || m->exec) return KNJ_OK;
   KNJ_HIP(hipStreamBeginCapture(m->stream, hipStreamCaptureModeThreadLocal));
   const int rc = enqueue_step(m, m->stream);
   hipGraph_t g = nullptr;
@@ -320,6 +301,12 @@ int ensure_graph(knj_model* m) {
   if (e != hipSuccess) return hip_fail(e, "hipStreamEndCapture");
   m->graph = g;
   KNJ_HIP(hipGraphInstantiate(&m->exec, g, nullptr, nullptr, 0));
+  return KNJ_OK;
+}
+
+int run_step(knj_model* m) {
+  if (!m->use_graph) return enqueue_step(m, m->stream);
+  KNJ_HIP(hipGraphLaunch(m->exec, m->stream));
   return KNJ_OK;
 }
 
@@ -436,7 +423,7 @@ int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_
   for (int t = 0; t < n; ++t) {
     int rc = set_state(m, tokens[t], 0);
     if (rc) return rc;
-    KNJ_HIP(hipGraphLaunch(m->exec, m->stream));
+    if ((rc = run_step(m))) return rc;
     m->pos += 1;
   }
   if (logits_host) {
@@ -457,7 +444,8 @@ int knj_model_decode_greedy(knj_model* m, int32_t first, int steps, int32_t* out
   }
   int rc = set_state(m, first, 0);
   if (rc) return rc;
-  for (int i = 0; i < steps; ++i) KNJ_HIP(hipGraphLaunch(m->exec, m->stream));
+  for (int i = 0; i < steps; ++i)
+    if ((rc = run_step(m))) return rc;
   m->pos += steps;
   KNJ_HIP(hipMemcpyAsync(out_tokens, m->out_tokens, (uint64_t)steps * 4, hipMemcpyDeviceToHost, m->stream));
   KNJ_HIP(hipStreamSynchronize(m->stream));
@@ -513,7 +501,8 @@ int knj_model_time_decode(knj_model* m, int iters, float* ms_out) {
   KNJ_HIP(hipEventCreate(&a));
   KNJ_HIP(hipEventCreate(&b));
   KNJ_HIP(hipEventRecord(a, m->stream));
-  for (int i = 0; i < iters; ++i) KNJ_HIP(hipGraphLaunch(m->exec, m->stream));
+  for (int i = 0; i < iters; ++i)
+    if ((rc = run_step(m))) return rc;
   KNJ_HIP(hipEventRecord(b, m->stream));
   KNJ_HIP(hipEventSynchronize(b));
   KNJ_HIP(hipEventElapsedTime(ms_out, a, b));

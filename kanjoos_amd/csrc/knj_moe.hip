@@ -1,0 +1,392 @@
+// kanjoos_amd/csrc/knj_moe.hip -- router and expert FFN kernels of the batch-1 MoE layer.
+//
+// Device side of Model::moe (/root/reference/src/model/model.cpp:399-510):
+//   router     logits = W_r . RMSNorm(x), softmax over all experts, top-k by
+//              probability with ties to the lower index, weights renormalised
+//              over the kept k (model.cpp:420-460);
+//   gate/up    g = W_gate[e] . hx, u = W_up[e] . hx, act = silu(g) * u
+//              (model.cpp:477-493);
+//   down       y_e = W_down[e] . act_e, out = resid + sum_e w_e * y_e with the
+//              experts summed in ascending index (the scatter order of
+//              model.cpp:464-508).
+#include "knj_common.h"
+#include "knj_dev.h"
+
+namespace knj {
+namespace {
+
+using namespace dev;
+
+// ------------------------------------------------------------------ router
+// One wave per expert row (4 per workgroup).  Each wave normalises x itself
+// (no workgroup barrier before the dot); workgroup 0 publishes hx.  The last
+// workgroup to finish ranks all experts: rank(e) = #{e' : p' > p or (p' == p
+// and e' < e)}, which is exactly the reference's repeated-argmax order.
+__global__ __launch_bounds__(kBlock) void k_router(RouterArgs a) {
+  __shared__ float probs[256];
+  __shared__ float red[8];
+  __shared__ unsigned int flag;
+  __shared__ float chosen_p[16];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x * (kBlock / 64) + wave;
+  const int H = a.n_embd;
+  const int nj = H / 256;  // float4 per lane
+  float4 wv[16];
+  if (e < a.n_expert) {
+    const float* wr = a.router_w + (uint64_t)e * H;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < nj) wv[j] = *reinterpret_cast<const float4*>(wr + 4 * lane + 256 * j);
+  }
+  float4 xv[16];
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    if (j < nj) {
+      xv[j] = *reinterpret_cast<const float4*>(a.x + 4 * lane + 256 * j);
+      ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+    }
+  if (a.norm_w) {
+    ss = group_sum<64>(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < nj) {
+        const float4 nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * lane + 256 * j);
+        xv[j].x = xv[j].x * scale * nw.x;
+        xv[j].y = xv[j].y * scale * nw.y;
+        xv[j].z = xv[j].z * scale * nw.z;
+        xv[j].w = xv[j].w * scale * nw.w;
+      }
+  }
+  if (blockIdx.x == 0 && wave == 0) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < nj) *reinterpret_cast<float4*>(a.hx + 4 * lane + 256 * j) = xv[j];
+  }
+  if (e < a.n_expert) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j)
+      if (j < nj) {
+        acc += wv[j].x * xv[j].x;
+        acc += wv[j].y * xv[j].y;
+        acc += wv[j].z * xv[j].z;
+        acc += wv[j].w * xv[j].w;
+      }
+    acc = group_sum<64>(acc);
+    if (lane == 0) a.logits[e] = acc;
+  }
+  if (!last_block_done(a.counter, gridDim.x, &flag)) return;
+  // softmax over all experts
+  const int t = threadIdx.x;
+  const float lg = t < a.n_expert ? ld_acquire_f(a.logits + t) : -INFINITY;
+  float mx = group_max<64>(lg);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  const float ex = t < a.n_expert ? expf(lg - mx) : 0.0f;
+  const float sum = block_sum(ex, red);
+  const float p = t < a.n_expert ? ex / sum : -1.0f;
+  probs[t] = p;
+  __syncthreads();
+  if (t < a.n_expert) {
+    int rank = 0;
+    for (int o = 0; o < a.n_expert; ++o) {
+      const float q = probs[o];
+      rank += (q > p || (q == p && o < t)) ? 1 : 0;
+    }
+    if (rank < a.k) {
+      a.topk_idx[rank] = t;
+      chosen_p[rank] = p;
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    float keep = 0.0f;
+    for (int k = 0; k < a.k; ++k) keep += chosen_p[k];
+    const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
+    for (int k = 0; k < a.k; ++k) a.topk_w[k] = chosen_p[k] * inv;
+  }
+}
+
+// ------------------------------------------------------------------ gate/up
+// Wave = one (expert slot, row) pair: lanes [0,32) the gate row, [32,64) the
+// up row, one 64-weight slice per lane (n_embd <= 2048).  RS pairs per wave,
+// their weights requested as soon as the expert index is known.
+template <int RS>
+__global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
+  __shared__ float xs[xpad_size(2048)];
+  __shared__ float red[8];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, sub = lane & 31;
+  const int nslices = a.n_embd >> 6;
+  const bool active = sub < nslices;
+  const uint64_t rb = (uint64_t)(a.n_embd >> 8) * KNJ_Q4K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_ff;
+  const int npairs = a.k * a.n_ff;
+  const int pair0 = (blockIdx.x * (kBlock / 64) + wave) * RS;
+  const int b = sub >> 2, g = sub & 3;
+  const uint8_t* base = half ? a.up : a.gate;
+  Q4Slice q[RS];
+#pragma unroll
+  for (int st = 0; st < RS; ++st) {
+    const int pr = pair0 + st;
+    if (active && pr < npairs) {
+      const int kk = pr / a.n_ff, row = pr - kk * a.n_ff;
+      const int e = a.topk_idx[kk];
+      q[st] = q4k_load(base + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+    }
+  }
+  stage_x(a.hx, nullptr, 0.0f, a.n_embd, xs, red);
+  XSlice xv;
+  if (active) xslice_load(xs, sub, xv);
+#pragma unroll
+  for (int st = 0; st < RS; ++st) {
+    const int pr = pair0 + st;
+    float acc = (active && pr < npairs) ? q4k_dot(q[st], g, xv) : 0.0f;
+    acc = group_sum<32>(acc);
+    const float u = __shfl(acc, 32, 64);
+    if (lane == 0 && pr < npairs) {
+      const float silu = acc / (1.0f + expf(-acc));
+      a.act[pr] = silu * u;  // act is [k][n_ff], pr = kk*n_ff + row
+    }
+  }
+}
+
+// Reference-shaped fallback for n_embd > 2048: 32 lanes per row, loop.
+__global__ __launch_bounds__(kBlock) void k_expert_gateup_wide(ExpertArgs a) {
+  extern __shared__ float xw[];
+  const int H = a.n_embd;
+  for (int i = 4 * threadIdx.x; i < H; i += 4 * kBlock)
+    *reinterpret_cast<float4*>(xw + xpad(i)) = *reinterpret_cast<const float4*>(a.hx + i);
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int half = lane >> 5, sub = lane & 31;
+  const int nslices = H >> 6;
+  const uint64_t rb = (uint64_t)(H >> 8) * KNJ_Q4K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_ff;
+  const int npairs = a.k * a.n_ff;
+  for (int pr = blockIdx.x * (kBlock / 64) + wave; pr < npairs; pr += gridDim.x * (kBlock / 64)) {
+    const int kk = pr / a.n_ff, row = pr - kk * a.n_ff;
+    const int e = a.topk_idx[kk];
+    const uint8_t* rp = (half ? a.up : a.gate) + (uint64_t)e * slab + (uint64_t)row * rb;
+    float acc = 0.0f;
+    for (int s = sub; s < nslices; s += 32) {
+      XSlice xv;
+      xslice_load(xw, s, xv);
+      acc += q4k_dot(q4k_load(rp + (uint64_t)(s >> 2) * KNJ_Q4K_BLOCK, s & 3), s & 3, xv);
+    }
+    acc = group_sum<32>(acc);
+    const float u = __shfl(acc, 32, 64);
+    if (lane == 0) a.act[pr] = (acc / (1.0f + expf(-acc))) * u;
+  }
+}
+
+// Ordered weighted sum of the k expert outputs of one row (ascending expert
+// index) plus the residual.  dots[kk] and the expert ids are per slot.
+__device__ __forceinline__ float combine_sorted(const float* dots, const int32_t* idx,
+                                                const float* wts, int k) {
+  float o = 0.0f;
+  int prev = -1;
+  for (int r = 0; r < k; ++r) {
+    int pick = -1, best = 0x7FFFFFFF;
+    for (int kk = 0; kk < k; ++kk) {
+      const int ek = idx[kk];
+      if (ek > prev && ek < best) {
+        best = ek;
+        pick = kk;
+      }
+    }
+    prev = best;
+    o = __fadd_rn(o, __fmul_rn(wts[pick], dots[pick]));
+  }
+  return o;
+}
+
+// ------------------------------------------------------------------ down (Q4_K)
+// Wave = one output row for all k experts: 16-lane group gi takes expert slots
+// gi, gi+4, ...; one 64-weight slice per lane (n_ff <= 1024).  The k
+// activation vectors are staged in LDS once per workgroup.
+template <int KPG>
+__global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
+  extern __shared__ float acts[];  // [k][xpad_size(n_ff)]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int gi = lane >> 4, sub = lane & 15;
+  const int F = a.n_ff, K = a.k;
+  const int fpad = xpad_size(F);
+  const int nslices = F >> 6;
+  const bool active = sub < nslices;
+  const uint64_t rb = (uint64_t)(F >> 8) * KNJ_Q4K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_embd;
+  const int row = blockIdx.x * (kBlock / 64) + wave;
+  const int b = sub >> 2, g = sub & 3;
+  Q4Slice q[KPG];
+  int eid[KPG];
+#pragma unroll
+  for (int j = 0; j < KPG; ++j) {
+    const int kk = gi + 4 * j;
+    eid[j] = kk < K ? a.topk_idx[kk] : -1;
+    if (active && kk < K && row < a.n_embd)
+      q[j] = q4k_load(a.down + (uint64_t)eid[j] * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+  }
+  for (int i = 4 * threadIdx.x; i < K * F; i += 4 * kBlock) {
+    const int kk = i / F, c = i - kk * F;
+    *reinterpret_cast<float4*>(acts + kk * fpad + xpad(c)) = *reinterpret_cast<const float4*>(a.act + i);
+  }
+  __syncthreads();
+  float dot[KPG];
+#pragma unroll
+  for (int j = 0; j < KPG; ++j) {
+    const int kk = gi + 4 * j;
+    float acc = 0.0f;
+    if (active && kk < K && row < a.n_embd) {
+      XSlice xv;
+      xslice_load(acts + kk * fpad, sub, xv);
+      acc = q4k_dot(q[j], g, xv);
+    }
+    dot[j] = group_sum<16>(acc);
+  }
+  if (row >= a.n_embd) return;
+  // gather the k dots into lane 0 in slot order
+  float dots[16];
+  int32_t ids[16];
+  float wts[16];
+#pragma unroll
+  for (int j = 0; j < KPG; ++j)
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+      const int kk = gg + 4 * j;
+      const float v = __shfl(dot[j], 16 * gg, 64);
+      if (kk < 16) dots[kk] = v;
+    }
+  if (lane != 0) return;
+  for (int kk = 0; kk < K; ++kk) {
+    ids[kk] = a.topk_idx[kk];
+    wts[kk] = a.topk_w[kk];
+  }
+  const float o = combine_sorted(dots, ids, wts, K);
+  const float v = a.resid ? __fadd_rn(a.resid[row], o) : o;
+  a.out[row] = v;
+  if (a.hidden_copy) a.hidden_copy[row] = v;
+}
+
+// ------------------------------------------------------------------ down (Q6_K)
+// Tasks (expert slot, row), LPR lanes each over the 8 quarters per block.
+template <int LPR>
+__global__ __launch_bounds__(kBlock) void k_expert_down_q6k(ExpertArgs a, int rows_per_block) {
+  extern __shared__ float smem[];
+  const int F = a.n_ff, K = a.k;
+  float* acts = smem;                  // [K][F]
+  float* dots = acts + K * F;          // [K][rows_per_block]
+  for (int i = threadIdx.x; i < K * F; i += blockDim.x) acts[i] = a.act[i];
+  __syncthreads();
+  const int row_base = blockIdx.x * rows_per_block;
+  const int nb = F / KNJ_QK;
+  const int nq = 8 * nb;
+  const uint64_t rbytes = (uint64_t)nb * KNJ_Q6K_BLOCK;
+  const uint64_t slab = rbytes * (uint64_t)a.n_embd;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane % LPR, tsub = lane / LPR;
+  constexpr int TPW = 64 / LPR;
+  const int ntasks = K * rows_per_block;
+  for (int t0 = wave * TPW; t0 < ntasks; t0 += (kBlock / 64) * TPW) {
+    const int t = t0 + tsub;
+    float acc = 0.0f;
+    const int kk = t / rows_per_block, r = t % rows_per_block;
+    const int row = row_base + r;
+    if (t < ntasks && row < a.n_embd) {
+      const int e = a.topk_idx[kk];
+      const uint8_t* rp = a.down + (uint64_t)e * slab + (uint64_t)row * rbytes;
+      const float* xk = acts + kk * F;
+      for (int s = sub; s < nq; s += LPR) {
+        const int bb = s >> 3, hf = (s >> 2) & 1, tq = s & 3;
+        acc += q6k_quarter(rp + (uint64_t)bb * KNJ_Q6K_BLOCK, hf, tq, xk + bb * KNJ_QK + 128 * hf + 32 * tq);
+      }
+    }
+    acc = group_sum<LPR>(acc);
+    if (sub == 0 && t < ntasks) dots[kk * rows_per_block + r] = acc;
+  }
+  __syncthreads();
+  for (int r = threadIdx.x; r < rows_per_block; r += blockDim.x) {
+    const int row = row_base + r;
+    if (row >= a.n_embd) break;
+    float d[16], w[16];
+    int32_t ids[16];
+    for (int kk = 0; kk < K; ++kk) {
+      d[kk] = dots[kk * rows_per_block + r];
+      ids[kk] = a.topk_idx[kk];
+      w[kk] = a.topk_w[kk];
+    }
+    const float o = combine_sorted(d, ids, w, K);
+    const float v = a.resid ? __fadd_rn(a.resid[row], o) : o;
+    a.out[row] = v;
+    if (a.hidden_copy) a.hidden_copy[row] = v;
+  }
+}
+
+int pow2_at_least(int v) {
+  int p = 1;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+}  // namespace
+
+hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
+  const int grid = (a.n_expert + 3) / 4;
+  hipLaunchKernelGGL(k_router, dim3(grid), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s) {
+  const int npairs = a.k * a.n_ff;
+  if (a.n_embd <= 2048) {
+    constexpr int RS = 2;
+    const int grid = (npairs + 4 * RS - 1) / (4 * RS);
+    hipLaunchKernelGGL(k_expert_gateup<RS>, dim3(grid), dim3(kBlock), 0, s, a);
+    return hipGetLastError();
+  }
+  const size_t lds = (size_t)xpad_size(a.n_embd) * 4;
+  const int grid = std::min(2048, (npairs + 3) / 4);
+  hipLaunchKernelGGL(k_expert_gateup_wide, dim3(grid), dim3(kBlock), lds, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s) {
+  if (a.type_down == KNJ_TYPE_Q4_K && a.n_ff <= 1024) {
+    const int kpg = (a.k + 3) / 4;
+    const size_t lds = (size_t)a.k * xpad_size(a.n_ff) * 4;
+    const int grid = (a.n_embd + 3) / 4;
+#define GD(J)                                                                       \
+  if (kpg == J) {                                                                   \
+    hipLaunchKernelGGL(k_expert_down<J>, dim3(grid), dim3(kBlock), lds, s, a);      \
+    return hipGetLastError();                                                       \
+  }
+    GD(1) GD(2) GD(3) GD(4)
+#undef GD
+    return hipErrorInvalidValue;
+  }
+  if (a.type_down != KNJ_TYPE_Q6_K) return hipErrorInvalidValue;
+  const int lpr = std::min(64, pow2_at_least(8 * (a.n_ff / KNJ_QK)));
+  const int rows_per_block = 8;
+  const size_t lds = ((size_t)a.k * a.n_ff + (size_t)a.k * rows_per_block) * 4;
+  const int grid = (a.n_embd + rows_per_block - 1) / rows_per_block;
+#define GQ(L)                                                                                   \
+  if (lpr == L) {                                                                               \
+    hipLaunchKernelGGL(k_expert_down_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a, rows_per_block); \
+    return hipGetLastError();                                                                   \
+  }
+  GQ(8) GQ(16) GQ(32) GQ(64)
+#undef GQ
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_experts(const ExpertArgs& a, hipStream_t s) {
+  const hipError_t e = launch_expert_gateup(a, s);
+  if (e != hipSuccess) return e;
+  return launch_expert_down(a, s);
+}
+
+}  // namespace knj
