@@ -171,16 +171,17 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       es[h0 * kChunk + lane] = e0;
       if (h1 < G) es[h1 * kChunk + lane] = e1;
       if (lane == 0) {
-        part[h0 * hstride + 0] = m0;
-        part[h0 * hstride + 1] = l0;
+        publish(part + h0 * hstride + 0, m0);
+        publish(part + h0 * hstride + 1, l0);
         if (h1 < G) {
-          part[h1 * hstride + 0] = m1;
-          part[h1 * hstride + 1] = l1;
+          publish(part + h1 * hstride + 0, m1);
+          publish(part + h1 * hstride + 1, l1);
         }
       }
       // 5) sum a*v for the wave's two heads; lane owns dims (2*lane, 2*lane+1)
       if (2 * lane < D) {
         float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
+#pragma unroll 8
         for (int p = 0; p < cnt; ++p) {
           const uint32_t vv = *reinterpret_cast<const uint32_t*>(vs + p * ROWH + 2 * lane);
           const float v0 = h2f(vv), v1 = h2f(vv >> 16);
@@ -193,44 +194,67 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
             a11 += eb * v1;
           }
         }
-        part[h0 * hstride + 2 + 2 * lane] = a00;
-        part[h0 * hstride + 3 + 2 * lane] = a01;
+        publish(part + h0 * hstride + 2 + 2 * lane, a00);
+        publish(part + h0 * hstride + 3 + 2 * lane, a01);
         if (h1 < G) {
-          part[h1 * hstride + 2 + 2 * lane] = a10;
-          part[h1 * hstride + 3 + 2 * lane] = a11;
+          publish(part + h1 * hstride + 2 + 2 * lane, a10);
+          publish(part + h1 * hstride + 3 + 2 * lane, a11);
         }
       }
     }
   } else {
     for (int i = tid; i < G * (D + 2); i += kBlock) {
       const int g = i / (D + 2), j = i % (D + 2);
-      part[g * hstride + j] = (j == 0) ? -INFINITY : 0.0f;
+      publish(part + g * hstride + j, (j == 0) ? -INFINITY : 0.0f);
     }
   }
 
-  // 6) merge: the last workgroup of this kv head combines all splits
+  // 6) merge: the last workgroup of this kv head combines all splits.  Only
+  // splits that hold positions (ceil(n_kv / chunk)) are read; per head the
+  // split maxima and sums go through LDS, then each thread folds its 4 dims
+  // over the splits in ascending order.
   if (!last_block_done(a.counter + kvh, n_split, &flag)) return;
-  // thread -> (head h = tid / 32, dims 4*(tid%32) ..) for D = 128; D = 64 uses 16 threads/head
-  constexpr int TPH = D / 4;
+  __shared__ float ms[8][64];   // exp(m_s - M) per head and split (<= 64 live splits per pass)
+  const int live = min(n_split, (n_kv + kChunk - 1) / kChunk);
+  constexpr int TPH = D / 4;  // threads per head in the fold
   const int h = tid / TPH, c = tid % TPH;
-  if (h >= G) return;
-  const float* ph = a.partial + (uint64_t)(kvh * G + h) * n_split * (D + 2);
+  const bool hv = h < G;
+  const float* ph = a.partial + (uint64_t)(kvh * G + (hv ? h : 0)) * n_split * (D + 2);
+  // per-head max over live splits
   float M = -INFINITY;
-  for (int s = c; s < n_split; s += TPH) M = fmaxf(M, ld_acquire_f(ph + (uint64_t)s * (D + 2)));
+  if (hv)
+    for (int s2 = c; s2 < live; s2 += TPH) M = fmaxf(M, ld_acquire_f(ph + (uint64_t)s2 * (D + 2)));
   M = group_max<TPH>(M);
-  float L = 0.0f;
   float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s = 0; s < n_split; ++s) {
-    const float m = ld_acquire_f(ph + (uint64_t)s * (D + 2));
-    if (m == -INFINITY) continue;
-    const float f = expf(m - M);
-    L += ld_acquire_f(ph + (uint64_t)s * (D + 2) + 1) * f;
-    const float* pa = ph + (uint64_t)s * (D + 2) + 2 + 4 * c;
-    acc.x += ld_acquire_f(pa + 0) * f;
-    acc.y += ld_acquire_f(pa + 1) * f;
-    acc.z += ld_acquire_f(pa + 2) * f;
-    acc.w += ld_acquire_f(pa + 3) * f;
+  float L = 0.0f;
+  for (int base = 0; base < live; base += 64) {
+    const int nb = min(64, live - base);
+    // weights f_s = exp(m_s - M) and the sum L = sum l_s f_s for this pass
+    float lpart = 0.0f;
+    if (hv)
+      for (int s2 = c; s2 < nb; s2 += TPH) {
+        const float m = ld_acquire_f(ph + (uint64_t)(base + s2) * (D + 2));
+        const float f = (m == -INFINITY) ? 0.0f : expf(m - M);
+        ms[h][s2] = f;
+        lpart += ld_acquire_f(ph + (uint64_t)(base + s2) * (D + 2) + 1) * f;
+      }
+    lpart = group_sum<TPH>(lpart);
+    __syncthreads();
+    if (hv) {
+      L += lpart;
+#pragma unroll 4
+      for (int s2 = 0; s2 < nb; ++s2) {
+        const float f = ms[h][s2];
+        const float* pa = ph + (uint64_t)(base + s2) * (D + 2) + 2 + 4 * c;
+        acc.x += ld_acquire_f(pa + 0) * f;
+        acc.y += ld_acquire_f(pa + 1) * f;
+        acc.z += ld_acquire_f(pa + 2) * f;
+        acc.w += ld_acquire_f(pa + 3) * f;
+      }
+    }
+    __syncthreads();
   }
+  if (!hv) return;
   float4 o;
   o.x = acc.x / L;
   o.y = acc.y / L;

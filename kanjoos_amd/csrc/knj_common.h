@@ -54,8 +54,10 @@ struct GemvArgs {
   float eps;
   const float* resid;       // optional: y = resid + W x
   float* y;                 // output (n_out)
-  unsigned long long* argmax_key;  // optional: packed (value, index) maximum of y
+  unsigned long long* argmax_key;  // optional: per-workgroup packed (value, index)
+                                   // maxima of y, at most kMaxKeys slots
 };
+constexpr int kMaxKeys = 4096;
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
 
 hipError_t launch_dequant(int type, const uint8_t* w, uint64_t n, float* out, hipStream_t s);
@@ -127,9 +129,10 @@ struct StepState {
   int32_t pad;
   unsigned long long key;
 };
-hipError_t launch_step_close(StepState* st, int32_t* out_tokens, int max_steps, hipStream_t s);
+hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int32_t* out_tokens,
+                             int max_steps, hipStream_t s);
 
-// Embedding row of st->token into x; also clears st->key for the LM head.
+// Embedding row of st->token into x.
 hipError_t launch_embed(int type, const uint8_t* table, int n_embd, StepState* st, float* x,
                         hipStream_t s);
 

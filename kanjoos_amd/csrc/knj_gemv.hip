@@ -156,14 +156,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q6k(const uint8_t* __restrict__
       }
     }
   }
-  if (argmax) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const unsigned long long t = __shfl_xor(best, o, 64);
-      best = t > best ? t : best;
-    }
-    if (lane == 0 && best) atomicMax(argmax, best);
-  }
+  if (argmax) block_argmax_store(best, argmax);
 }
 
 // BF16 rows (the LM head): 8 weights per lane per 16-byte load, NJ loads per
@@ -242,7 +235,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_bf16(const uint8_t* __restrict_
 #pragma unroll
       for (int j = 0; j < NJ; ++j) cur[r][j] = nxt[r][j];
   }
-  if (argmax && lane == 0 && best) atomicMax(argmax, best);
+  if (argmax) block_argmax_store(best, argmax);
 }
 
 // BF16 / F32 rows of any width (multiple of 8 / 4): one wave per row.
@@ -310,15 +303,34 @@ __global__ __launch_bounds__(kBlock) void k_gemv_plain(const uint8_t* __restrict
       best = k > best ? k : best;
     }
   }
-  if (argmax && lane == 0 && best) atomicMax(argmax, best);
+  if (argmax) block_argmax_store(best, argmax);
 }
 
-// The decode step's last launch closes the step: after every workgroup has
-// folded its rows into the packed argmax, the last one turns it into the next
-// token (first maximum wins, /root/reference/src/cli/main.cpp:126-132) and
-// advances the device-side position.
-__global__ void k_step_close(StepState* st, int32_t* out_tokens, int max_steps) {
-  const int tok = argmax_index(st->key);
+// The decode step's last launch closes the step: the per-workgroup argmax keys
+// of the LM head (kMaxKeys slots, unused ones zero) are reduced to the next
+// token (first maximum wins, /root/reference/src/cli/main.cpp:126-132) and the
+// device-side position advances.
+__global__ __launch_bounds__(kBlock) void k_step_close(StepState* st, const unsigned long long* keys,
+                                                       int32_t* out_tokens, int max_steps) {
+  unsigned long long best = 0;
+#pragma unroll
+  for (int j = 0; j < kMaxKeys / kBlock; ++j) {
+    const unsigned long long k = keys[threadIdx.x + kBlock * j];
+    best = k > best ? k : best;
+  }
+  __shared__ unsigned long long wb[4];
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const unsigned long long t = __shfl_xor(best, o, 64);
+    best = t > best ? t : best;
+  }
+  if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x != 0) return;
+  for (int w = 1; w < 4; ++w) best = wb[w] > best ? wb[w] : best;
+  best = wb[0] > best ? wb[0] : best;
+  const int tok = argmax_index(best);
+  st->key = best;
   if (st->step < max_steps) out_tokens[st->step] = tok;
   st->step += 1;
   st->token = tok;
@@ -363,7 +375,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
     const int lpr = std::min(64, pow2_at_least(8 * (a.n_in / KNJ_QK)));
     const size_t lds = (size_t)a.n_in * 4;
     const int rows_per_block = 4 * (64 / lpr);
-    const int grid = std::max(1, std::min(4096, (a.n_out + rows_per_block - 1) / rows_per_block));
+    const int grid = std::max(1, std::min(kMaxKeys, (a.n_out + rows_per_block - 1) / rows_per_block));
 #define G6(L)                                                                                 \
   if (lpr == L) {                                                                             \
     hipLaunchKernelGGL(k_gemv_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, \
@@ -378,7 +390,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
     const int nj = a.n_in / 512;
     constexpr int RS = 4;
     const int waves_needed = (a.n_out + RS - 1) / RS;
-    const int grid = std::max(1, std::min(1024, (waves_needed + 3) / 4));
+    const int grid = std::max(1, std::min(512, (waves_needed + 3) / 4));
 #define GB(J)                                                                                   \
   if (nj == J) {                                                                                \
     hipLaunchKernelGGL((k_gemv_bf16<J, RS>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,     \
@@ -390,7 +402,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
     if (nj == 3 || nj > 4) { /* fall through to the generic kernel */ }
   }
   const size_t lds = (size_t)a.n_in * 4;
-  const int grid = std::max(1, std::min(4096, (a.n_out + 3) / 4));
+  const int grid = std::max(1, std::min(kMaxKeys, (a.n_out + 3) / 4));
   if (a.type == KNJ_TYPE_BF16) {
     hipLaunchKernelGGL(k_gemv_plain<true>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out,
                        a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
@@ -401,8 +413,9 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_step_close(StepState* st, int32_t* out_tokens, int max_steps, hipStream_t s) {
-  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(1), 0, s, st, out_tokens, max_steps);
+hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int32_t* out_tokens,
+                             int max_steps, hipStream_t s) {
+  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(kBlock), 0, s, st, keys, out_tokens, max_steps);
   return hipGetLastError();
 }
 

@@ -36,13 +36,11 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm(const float* __restrict__ x,
   for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * scale * w[i];
 }
 
-// Embedding row of the step's token (model.cpp:527-537), and reset of the
-// step's argmax so the LM head can fold into it.
+// Embedding row of the step's token (model.cpp:527-537).
 __global__ void k_embed(int type, const uint8_t* __restrict__ table, int n_embd, StepState* st,
                         float* __restrict__ x) {
   const int id = st->token;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
-  if (i == 0) st->key = 0ull;
   if (i >= n_embd) return;
   const uint64_t idx = (uint64_t)id * n_embd + i;
   if (type == KNJ_TYPE_BF16)

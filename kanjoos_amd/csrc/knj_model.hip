@@ -80,6 +80,7 @@ struct knj_model {
   uint16_t *kv_k = nullptr, *kv_v = nullptr;
   StepState* st = nullptr;
   int32_t* out_tokens = nullptr;
+  unsigned long long* keys = nullptr;  // LM-head per-workgroup argmax keys
   int max_steps = 0;
   unsigned int* counter = nullptr;
   int pos = 0;
@@ -154,6 +155,8 @@ int setup(knj_model* m) {
   if ((rc = alloc(m, (void**)&m->st, sizeof(StepState)))) return rc;
   m->max_steps = std::max(c.n_ctx, 1);
   if ((rc = alloc(m, (void**)&m->out_tokens, (uint64_t)m->max_steps * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->keys, (uint64_t)kMaxKeys * 8))) return rc;
+  KNJ_HIP(hipMemset(m->keys, 0, (uint64_t)kMaxKeys * 8));
   // tickets: [0] router, [64 + h] attention of kv head h
   if ((rc = alloc(m, (void**)&m->counter, 4096))) return rc;
   KNJ_HIP(hipMemset(m->counter, 0, 4096));
@@ -280,9 +283,9 @@ int enqueue_step(knj_model* m, hipStream_t s) {
   }
   GemvArgs head{c.type_head, m->image + m->off_head, c.n_embd, c.n_vocab, m->x,
                 reinterpret_cast<const float*>(m->image + m->off_onorm), c.rms_eps, nullptr,
-                m->logits, &m->st->key};
+                m->logits, m->keys};
   KNJ_HIP(launch_gemv(head, s));
-  KNJ_HIP(launch_step_close(m->st, m->out_tokens, m->max_steps, s));
+  KNJ_HIP(launch_step_close(m->st, m->keys, m->out_tokens, m->max_steps, s));
   return KNJ_OK;
 }
 

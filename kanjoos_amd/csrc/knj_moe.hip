@@ -23,7 +23,7 @@ using namespace dev;
 // workgroup to finish ranks all experts: rank(e) = #{e' : p' > p or (p' == p
 // and e' < e)}, which is exactly the reference's repeated-argmax order.
 __global__ __launch_bounds__(kBlock) void k_router(RouterArgs a) {
-  __shared__ float probs[256];
+  __shared__ __align__(16) float probs[256];
   __shared__ float red[8];
   __shared__ unsigned int flag;
   __shared__ float chosen_p[16];
@@ -75,7 +75,7 @@ __global__ __launch_bounds__(kBlock) void k_router(RouterArgs a) {
         acc += wv[j].w * xv[j].w;
       }
     acc = group_sum<64>(acc);
-    if (lane == 0) a.logits[e] = acc;
+    if (lane == 0) publish(a.logits + e, acc);
   }
   if (!last_block_done(a.counter, gridDim.x, &flag)) return;
   // softmax over all experts
@@ -92,10 +92,15 @@ __global__ __launch_bounds__(kBlock) void k_router(RouterArgs a) {
   probs[t] = p;
   __syncthreads();
   if (t < a.n_expert) {
+    // four candidates per LDS read, independent iterations
     int rank = 0;
-    for (int o = 0; o < a.n_expert; ++o) {
-      const float q = probs[o];
-      rank += (q > p || (q == p && o < t)) ? 1 : 0;
+#pragma unroll 8
+    for (int o = 0; o < 256; o += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(probs + o);
+      rank += (q.x > p || (q.x == p && o < t)) ? 1 : 0;
+      rank += (q.y > p || (q.y == p && o + 1 < t)) ? 1 : 0;
+      rank += (q.z > p || (q.z == p && o + 2 < t)) ? 1 : 0;
+      rank += (q.w > p || (q.w == p && o + 3 < t)) ? 1 : 0;
     }
     if (rank < a.k) {
       a.topk_idx[rank] = t;
@@ -231,9 +236,25 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
     if (active && kk < K && row < a.n_embd)
       q[j] = q4k_load(a.down + (uint64_t)eid[j] * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
   }
-  for (int i = 4 * threadIdx.x; i < K * F; i += 4 * kBlock) {
-    const int kk = i / F, c = i - kk * F;
-    *reinterpret_cast<float4*>(acts + kk * fpad + xpad(c)) = *reinterpret_cast<const float4*>(a.act + i);
+  // stage the k activation vectors: 4 loads in flight per thread per round
+  // (named registers: an indexed array here was placed in scratch memory)
+  for (int base = 4 * threadIdx.x; base < K * F; base += 16 * kBlock) {
+    const int n = K * F;
+    const int i0 = base, i1 = base + 4 * kBlock, i2 = base + 8 * kBlock, i3 = base + 12 * kBlock;
+    const float4 v0 = *reinterpret_cast<const float4*>(a.act + i0);
+    const float4 v1 = *reinterpret_cast<const float4*>(a.act + (i1 < n ? i1 : i0));
+    const float4 v2 = *reinterpret_cast<const float4*>(a.act + (i2 < n ? i2 : i0));
+    const float4 v3 = *reinterpret_cast<const float4*>(a.act + (i3 < n ? i3 : i0));
+    auto put = [&](int i, const float4& v) {
+      if (i < n) {
+        const int kk = i / F, c = i - kk * F;
+        *reinterpret_cast<float4*>(acts + kk * fpad + xpad(c)) = v;
+      }
+    };
+    put(i0, v0);
+    put(i1, v1);
+    put(i2, v2);
+    put(i3, v3);
   }
   __syncthreads();
   float dot[KPG];
