@@ -1,0 +1,89 @@
+// include/knj/model.h -- C++ host interface of the device decode step.
+//
+// Keeps the shape of the reference's model-step interface
+// (/root/reference/src/model/model.h:32-163): ModelGeometry, Model::Options,
+// Model::open -> forward(tokens, n) -> logits of the last token, reset(),
+// pos(), geom(), threads().  The weights and the KV cache live on the GPU; the
+// arithmetic runs in the gfx950 kernels behind include/knj_capi.h, which this
+// class calls.  Errors are std::runtime_error, as in the reference (context
+// exhausted, token out of range, bad geometry).
+#pragma once
+
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "../knj_capi.h"
+
+namespace knj {
+
+struct ModelGeometry {
+  int n_layer = 0;
+  int n_embd = 0;
+  int n_head = 0;
+  int n_head_kv = 0;
+  int head_dim = 0;
+  int n_ff_exp = 0;
+  int n_expert = 0;
+  int n_expert_used = 0;
+  int n_vocab = 0;
+  int n_ctx_train = 0;
+  float rms_eps = 1e-6f;
+  float rope_base = 1e6f;
+  bool rope_split_halves = true;  // ggml NEOX pairing (i, i + d/2), the only one qwen3moe uses
+
+  int q_dim() const { return n_head * head_dim; }
+  int kv_dim() const { return n_head_kv * head_dim; }
+  std::string describe() const;
+};
+
+class Model {
+ public:
+  struct Options {
+    int n_ctx = 2048;
+    int threads = 0;  // accepted for interface compatibility; the step runs on the GPU
+  };
+
+  // Synthetic weights (seeded, include/knj_synth.h) of the given geometry and
+  // quantisation, generated on the GPU.
+  static std::unique_ptr<Model> open_synthetic(const knj_model_config& cfg, uint64_t seed,
+                                               const Options& opt);
+  // A weight image laid out as include/knj_model.h describes.
+  static std::unique_ptr<Model> open_image(const knj_model_config& cfg, const void* image,
+                                           uint64_t bytes, const Options& opt);
+
+  ~Model();
+  Model(const Model&) = delete;
+  Model& operator=(const Model&) = delete;
+
+  const ModelGeometry& geom() const { return g_; }
+  int n_ctx() const { return n_ctx_; }
+  int pos() const;
+  int threads() const { return 1; }
+
+  // Drops the KV cache and returns to position 0.
+  void reset();
+
+  // Runs `n` tokens starting at the current position; returns n_vocab logits
+  // of the last token, valid until the next call.
+  const float* forward(const int32_t* tokens, int n);
+
+  // Greedy decode on the device: feeds `first`, returns `steps` argmax tokens.
+  std::vector<int32_t> decode_greedy(int32_t first, int steps);
+
+  knj_model* handle() const { return m_; }
+
+ private:
+  Model() = default;
+  knj_model* m_ = nullptr;
+  ModelGeometry g_;
+  int n_ctx_ = 0;
+  std::vector<float> logits_;
+};
+
+// Throws std::runtime_error with knj_last_error() when rc != KNJ_OK.
+void check(int rc, const char* what);
+
+}  // namespace knj

@@ -28,13 +28,24 @@ HIP_FLAGS = [
 ]
 
 
+HOST = os.path.join(HERE, "host")
+RUN = os.path.join(HERE, "kanjoos-run")
+
+
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    """HIP device+host sources, then the plain C++ host classes (compiled by
+    hipcc as host code)."""
+    hip = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    return hip + [os.path.join(HOST, "knj_host.cpp")]
 
 
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *HIP_FLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [HIPCC, "-O2", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include"),
+               "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *HIP_FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr}")
@@ -54,8 +65,15 @@ def build(verbose: bool = True) -> str:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    # the command-line driver, linked against the library (rpath $ORIGIN)
+    cmd = [HIPCC, "-O2", "-std=c++17", "-I", os.path.join(ROOT, "include"),
+           os.path.join(HOST, "kanjoos_run.cpp"), "-o", RUN, "-L", HERE, "-lkanjoos_amd",
+           "-Wl,-rpath,$ORIGIN"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"kanjoos-run link failed:\n{r.stderr}")
     if verbose:
-        print(f"built {LIB}")
+        print(f"built {LIB} and {RUN}")
     return LIB
 
 

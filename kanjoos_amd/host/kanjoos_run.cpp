@@ -1,0 +1,102 @@
+// kanjoos_amd/host/kanjoos_run.cpp -- command-line driver of the device decode step.
+//
+// The shape of the reference's kanjoos-run prefill -> greedy decode loop and its
+// --bench PP TG mode (/root/reference/src/cli/main.cpp:245-279, 451-568), over
+// the C++ Model class; weights are the seeded synthetic Qwen3-30B-A3B-shaped
+// model (no GGUF loading in this build).
+//
+//   kanjoos-run [--layers N] [--ctx N] [--seed S] [--prompt N] [--n-predict N]
+//               [--bench PP TG] [--small]
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <random>
+#include <string>
+#include <vector>
+
+#include "../../include/knj/backend.h"
+#include "../../include/knj/model.h"
+
+int main(int argc, char** argv) {
+  int layers = 48, ctx = 4352, prompt = 16, n_predict = 32, pp = 0, tg = 0;
+  uint64_t seed = 0;
+  bool small = false;
+  for (int i = 1; i < argc; ++i) {
+    const std::string a = argv[i];
+    auto next = [&](const char* name) {
+      if (i + 1 >= argc) {
+        std::fprintf(stderr, "%s needs a value\n", name);
+        std::exit(2);
+      }
+      return std::atoi(argv[++i]);
+    };
+    if (a == "--layers") layers = next("--layers");
+    else if (a == "--ctx") ctx = next("--ctx");
+    else if (a == "--seed") seed = (uint64_t)next("--seed");
+    else if (a == "--prompt") prompt = next("--prompt");
+    else if (a == "--n-predict") n_predict = next("--n-predict");
+    else if (a == "--small") small = true;
+    else if (a == "--bench") {
+      pp = next("--bench");
+      tg = next("--bench");
+    } else {
+      std::fprintf(stderr, "unknown argument %s\n", a.c_str());
+      return 2;
+    }
+  }
+  auto backend = knj::Backend::create(0);
+  if (!backend) {
+    std::fprintf(stderr, "device refused: %s\n", knj::Backend::knj_last_refusal());
+    return 6;
+  }
+  knj_model_config c{};
+  c.n_layer = layers; c.n_embd = 2048; c.n_head = 32; c.n_head_kv = 4; c.head_dim = 128;
+  c.n_ff = 768; c.n_expert = 128; c.n_expert_used = 8; c.n_vocab = 151936; c.n_ctx = ctx;
+  c.rms_eps = 1e-6f; c.rope_base = 1e6f; c.type_embd = KNJ_TYPE_BF16; c.type_attn = KNJ_TYPE_Q4_K;
+  c.type_gate_up = KNJ_TYPE_Q4_K; c.type_down = KNJ_TYPE_Q4_K; c.type_head = KNJ_TYPE_BF16;
+  c.init_std = 0.02f;
+  if (small) {
+    c.n_embd = 512; c.n_head = 8; c.n_head_kv = 2; c.head_dim = 64; c.n_ff = 256;
+    c.n_expert = 16; c.n_expert_used = 4; c.n_vocab = 4096;
+  }
+  try {
+    knj::Model::Options opt;
+    opt.n_ctx = ctx;
+    auto m = knj::Model::open_synthetic(c, seed, opt);
+    std::printf("%s\n", m->geom().describe().c_str());
+    std::mt19937 rng((uint32_t)seed);
+    auto run_prompt = [&](int n) {
+      std::vector<int32_t> toks((size_t)n);
+      for (auto& t : toks) t = (int32_t)(rng() % (uint32_t)c.n_vocab);
+      const float* lg = m->forward(toks.data(), n);
+      int best = 0;
+      for (int v = 1; v < c.n_vocab; ++v)
+        if (lg[v] > lg[best]) best = v;  // first maximum wins (main.cpp:126-132)
+      return best;
+    };
+    using clk = std::chrono::steady_clock;
+    if (pp > 0 || tg > 0) {
+      const auto t0 = clk::now();
+      const int first = run_prompt(pp > 0 ? pp : 1);
+      const auto t1 = clk::now();
+      const auto out = m->decode_greedy(first, tg > 0 ? tg : 1);
+      const auto t2 = clk::now();
+      const double pp_s = std::chrono::duration<double>(t1 - t0).count();
+      const double tg_s = std::chrono::duration<double>(t2 - t1).count();
+      std::printf("bench: pp %d tokens %.1f tok/s, tg %d tokens %.1f tok/s (%.3f ms/token)\n", pp,
+                  pp / pp_s, tg, tg / tg_s, 1000.0 * tg_s / tg);
+      (void)out;
+      return 0;
+    }
+    const int first = run_prompt(prompt);
+    const auto out = m->decode_greedy(first, n_predict);
+    std::printf("tokens:");
+    for (int32_t t : out) std::printf(" %d", t);
+    std::printf("\n");
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "%s\n", e.what());
+    return 9;
+  }
+  return 0;
+}

@@ -1,0 +1,160 @@
+// kanjoos_amd/host/knj_host.cpp -- C++ host classes (Model, Backend) over the C ABI.
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/knj/backend.h"
+#include "../../include/knj/model.h"
+
+namespace knj {
+
+void check(int rc, const char* what) {
+  if (rc != KNJ_OK) {
+    throw std::runtime_error(std::string("model: ") + what + ": " + knj_last_error());
+  }
+}
+
+std::string ModelGeometry::describe() const {
+  char buf[512];
+  std::snprintf(buf, sizeof(buf),
+                "layers=%d hidden=%d heads=%d/%d head_dim=%d q_dim=%d kv_dim=%d\n"
+                "  experts=%d top_k=%d expert_ff=%d vocab=%d ctx=%d rms_eps=%.3g rope_base=%.6g",
+                n_layer, n_embd, n_head, n_head_kv, head_dim, q_dim(), kv_dim(), n_expert,
+                n_expert_used, n_ff_exp, n_vocab, n_ctx_train, rms_eps, rope_base);
+  return buf;
+}
+
+namespace {
+ModelGeometry geometry_of(const knj_model_config& c) {
+  ModelGeometry g;
+  g.n_layer = c.n_layer;
+  g.n_embd = c.n_embd;
+  g.n_head = c.n_head;
+  g.n_head_kv = c.n_head_kv;
+  g.head_dim = c.head_dim;
+  g.n_ff_exp = c.n_ff;
+  g.n_expert = c.n_expert;
+  g.n_expert_used = c.n_expert_used;
+  g.n_vocab = c.n_vocab;
+  g.n_ctx_train = c.n_ctx;
+  g.rms_eps = c.rms_eps;
+  g.rope_base = c.rope_base;
+  return g;
+}
+}  // namespace
+
+std::unique_ptr<Model> Model::open_synthetic(const knj_model_config& cfg, uint64_t seed,
+                                             const Options& opt) {
+  if (opt.n_ctx <= 0) throw std::runtime_error("model: n_ctx must be positive");
+  knj_model_config c = cfg;
+  c.n_ctx = opt.n_ctx;
+  std::unique_ptr<Model> m(new Model());
+  check(knj_model_create_synthetic(&c, seed, &m->m_), "open");
+  m->g_ = geometry_of(c);
+  m->n_ctx_ = c.n_ctx;
+  m->logits_.assign((size_t)c.n_vocab, 0.0f);
+  return m;
+}
+
+std::unique_ptr<Model> Model::open_image(const knj_model_config& cfg, const void* image,
+                                         uint64_t bytes, const Options& opt) {
+  if (opt.n_ctx <= 0) throw std::runtime_error("model: n_ctx must be positive");
+  knj_model_config c = cfg;
+  c.n_ctx = opt.n_ctx;
+  std::unique_ptr<Model> m(new Model());
+  check(knj_model_create_from_image(&c, image, bytes, &m->m_), "open");
+  m->g_ = geometry_of(c);
+  m->n_ctx_ = c.n_ctx;
+  m->logits_.assign((size_t)c.n_vocab, 0.0f);
+  return m;
+}
+
+Model::~Model() {
+  if (m_) knj_model_free(m_);
+}
+
+int Model::pos() const { return knj_model_pos(m_); }
+
+void Model::reset() { check(knj_model_reset(m_), "reset"); }
+
+const float* Model::forward(const int32_t* tokens, int n) {
+  if (n <= 0) throw std::runtime_error("model: forward needs at least one token");
+  if (pos() + n > n_ctx_) {
+    throw std::runtime_error("model: context exhausted (" + std::to_string(pos()) + " + " +
+                             std::to_string(n) + " > " + std::to_string(n_ctx_) + ")");
+  }
+  for (int t = 0; t < n; ++t)
+    if (tokens[t] < 0 || tokens[t] >= g_.n_vocab) throw std::runtime_error("model: token id out of range");
+  check(knj_model_forward(m_, tokens, n, logits_.data()), "forward");
+  return logits_.data();
+}
+
+std::vector<int32_t> Model::decode_greedy(int32_t first, int steps) {
+  std::vector<int32_t> out((size_t)steps);
+  check(knj_model_decode_greedy(m_, first, steps, out.data()), "decode");
+  return out;
+}
+
+// ------------------------------------------------------------------ Backend
+namespace {
+thread_local char g_refusal[256] = "";
+}
+
+const char* Backend::knj_last_refusal() { return g_refusal; }
+
+std::unique_ptr<Backend> Backend::create(int device) {
+  DeviceCaps c;
+  const int rc = knj_device_open(device);
+  if (rc != KNJ_OK) {
+    std::snprintf(g_refusal, sizeof(g_refusal), "%s", knj_last_error());
+    return nullptr;
+  }
+  if (knj_device_caps_get(&c.caps) != KNJ_OK) {
+    std::snprintf(g_refusal, sizeof(g_refusal), "%s", knj_last_error());
+    return nullptr;
+  }
+  c.arch_ok = true;
+  g_refusal[0] = '\0';
+  return std::unique_ptr<Backend>(new Backend(c));
+}
+
+std::unique_ptr<Backend> Backend::from_caps(const DeviceCaps& caps) {
+  g_refusal[0] = '\0';
+  return std::unique_ptr<Backend>(new Backend(caps));
+}
+
+bool Backend::would_instantiate(KnjCap cap) const noexcept {
+  if (!caps_.arch_ok) return false;
+  switch (cap) {
+    case KnjCap::Wave64: return caps_.caps.wave_size == 64;
+    case KnjCap::MfmaBf16: return caps_.caps.has_mfma_bf16 != 0;
+    case KnjCap::MfmaI8: return caps_.caps.has_mfma_i8 != 0;
+    case KnjCap::Fp8: return caps_.caps.has_fp8 != 0;
+    case KnjCap::Dot4I32I8: return true;
+  }
+  return false;
+}
+
+bool Backend::launch_expert_gemv(const ExpertPlan& p) {
+  if (!would_instantiate(KnjCap::Wave64)) return false;
+  return knj_moe_decode_layer(p.x, p.norm_w, p.eps, p.router_w, p.gate, p.up, p.down,
+                              p.type_gate_up, p.type_down, p.n_embd, p.n_ff, p.n_expert, p.k,
+                              p.resid, p.out, p.logits, p.topk_idx, p.topk_w, p.stream) == KNJ_OK;
+}
+
+bool Backend::launch_attention(const AttentionPlan& p) {
+  if (!would_instantiate(KnjCap::Wave64)) return false;
+  return knj_attention_step(p.q, p.k, p.v, p.q_norm, p.k_norm, p.eps, p.rope_base, p.pos,
+                            p.n_head, p.n_head_kv, p.head_dim, p.n_ctx, p.k_cache, p.v_cache,
+                            p.out, p.stream) == KNJ_OK;
+}
+
+void Backend::launch_kv_write(const KvWritePlan& p) {
+  AttentionPlan a = p.attn;
+  a.out = p.scratch_out;
+  (void)launch_attention(a);
+}
+
+}  // namespace knj

@@ -173,3 +173,17 @@ def test_small_model_greedy_parity(device, cfgkw):
     want = om.greedy([int(np.argmax(lw))], 64)
     got = gm.decode_greedy(int(np.argmax(lg)), 64)
     assert list(got) == list(want)
+
+
+def test_cpp_driver_runs(device):
+    """The C++ Model/Backend classes end to end through kanjoos-run (small geometry)."""
+    import os
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(K.LIB_PATH), "kanjoos-run")
+    r = subprocess.run([exe, "--small", "--layers", "2", "--ctx", "64", "--prompt", "8",
+                        "--n-predict", "16"], capture_output=True, text=True, timeout=60)
+    say(r.stdout + r.stderr)
+    assert r.returncode == 0
+    toks = r.stdout.strip().splitlines()[-1].split()
+    assert toks[0] == "tokens:" and len(toks) == 17
