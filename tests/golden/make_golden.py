@@ -1,0 +1,82 @@
+#!/usr/bin/env python3
+"""Writes the golden fixtures under tests/golden/ from the CPU oracle.
+
+  config1.json      BASELINE config 1 at seed 0: router logits, top-8 indices and
+                    weights, and the MoE output of one layer (x ~ N(0,1), RMSNorm
+                    weight 1, router f32 ~ N(0,0.02), 128 Q4_K experts).
+  full_greedy.json  BASELINE config 3's model (48 layers, seed 0): 64 greedy
+                    tokens after the prompt [1, 2, 3, 4], with the top-1/top-2
+                    logit margin of every step.
+
+The oracle restates the reference's CPU forward pass (oracle/); the weights come
+from the seeded generator in include/knj_synth.h, which the GPU reproduces bit
+for bit.  Usage: python tests/golden/make_golden.py [config1] [full]
+"""
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+
+import oracle as O  # noqa: E402
+
+SEED = 0
+
+
+def config1_inputs(n_embd=2048, n_ff=768, n_expert=128, type_down=O.TYPE_Q4_K, layer=0):
+    x = O.synth_f32(O.tensor_key(SEED, layer, "input"), n_embd)
+    router = O.synth_tensor(O.tensor_key(SEED, layer, "router"), O.TYPE_F32, n_embd, n_expert)
+    gate = np.concatenate([O.synth_tensor(O.tensor_key(SEED, layer, "gate", e), O.TYPE_Q4_K, n_embd, n_ff)
+                           for e in range(n_expert)])
+    up = np.concatenate([O.synth_tensor(O.tensor_key(SEED, layer, "up", e), O.TYPE_Q4_K, n_embd, n_ff)
+                         for e in range(n_expert)])
+    down = np.concatenate([O.synth_tensor(O.tensor_key(SEED, layer, "down", e), type_down, n_ff, n_embd)
+                           for e in range(n_expert)])
+    return x, router, gate, up, down
+
+
+def config1():
+    x, router, gate, up, down = config1_inputs()
+    hx = O.rmsnorm(x, np.ones(2048, np.float32), 1e-6)
+    out, logits, ti, tw = O.moe(hx, router, gate, up, down, 2048, 768, 128, 8)
+    return {"seed": SEED, "x_sha": _sha(x), "logits": logits[0].tolist(), "topk_idx": ti[0].tolist(),
+            "topk_w": tw[0].tolist(), "out": out[0].tolist()}
+
+
+def _sha(a):
+    import hashlib
+
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+def full_greedy(steps=64, prompt=(1, 2, 3, 4)):
+    cfg = O.make_config(n_ctx=128)
+    t0 = time.time()
+    om = O.OracleModel(cfg, seed=SEED)
+    print(f"weights generated in {time.time() - t0:.0f} s", flush=True)
+    logits = om.forward(list(prompt))
+    toks, margins = [], []
+    for i in range(steps):
+        top2 = np.partition(logits, -2)[-2:]
+        margins.append(float(top2.max() - top2.min()))
+        tok = int(np.argmax(logits))
+        toks.append(tok)
+        if i + 1 < steps:
+            logits = om.forward([tok])
+        print(f"step {i}: token {tok} margin {margins[-1]:.4g}", flush=True)
+    return {"seed": SEED, "prompt": list(prompt), "tokens": toks, "margins": margins,
+            "config": cfg.as_dict()}
+
+
+if __name__ == "__main__":
+    which = sys.argv[1:] or ["config1", "full"]
+    if "config1" in which:
+        with open(os.path.join(HERE, "config1.json"), "w") as f:
+            json.dump(config1(), f)
+    if "full" in which:
+        with open(os.path.join(HERE, "full_greedy.json"), "w") as f:
+            json.dump(full_greedy(), f)

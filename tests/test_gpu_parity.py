@@ -4,6 +4,9 @@ Bars (BASELINE north star): dequantised weights and top-k indices bit-exact;
 fp32 outputs within 1e-5 relative RMSE (the reference's metric,
 tests/host_oracle.h:143-171); greedy tokens identical.
 """
+import json
+import os
+
 import numpy as np
 import pytest
 
@@ -187,3 +190,62 @@ def test_cpp_driver_runs(device):
     assert r.returncode == 0
     toks = r.stdout.strip().splitlines()[-1].split()
     assert toks[0] == "tokens:" and len(toks) == 17
+
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_config1_against_golden(device):
+    """BASELINE config 1 on the GPU against the committed oracle fixture."""
+    want = json.load(open(os.path.join(GOLDEN, "config1.json")))
+    n_embd, n_ff, n_expert, k = 2048, 768, 128, 8
+    x, router, gate, up, down = moe_layer_inputs()
+    d = {n: K.DeviceBuffer.from_array(a) for n, a in
+         dict(x=x, router=router, gate=gate, up=up, down=down, ones=np.ones(n_embd, np.float32)).items()}
+    out, logits = K.DeviceBuffer(4 * n_embd), K.DeviceBuffer(4 * n_expert)
+    ti, tw = K.DeviceBuffer(4 * k), K.DeviceBuffer(4 * k)
+    K.moe_decode_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], n_embd, n_ff, n_expert, k,
+                       out, logits, ti, tw, norm_w=d["ones"], eps=1e-6)
+    assert list(ti.download(np.int32)) == want["topk_idx"]
+    assert rel_rmse(out.download(np.float32), want["out"]) <= 1e-5
+
+
+def full_config(**kw):
+    return dict(n_ctx=160, **kw)
+
+
+@pytest.fixture(scope="module")
+def full_pair(device):
+    """The 48-layer Qwen3-30B-A3B-shaped model on the GPU (seed 0) and the CPU
+    oracle over the same (downloaded) weight image."""
+    say("full model: generating 18 GB of weights on the GPU")
+    gm = K.Model.synthetic(K.qwen3_30b_a3b(**full_config()), seed=SEED)
+    img = gm.download_image()
+    om = O.OracleModel(O.make_config(**full_config()), seed=SEED, image=img, threads=16)
+    yield gm, om, img
+    gm.close()
+    om.close()
+
+
+def test_full_model_step_parity(full_pair):
+    """Per-layer hidden states (all 48 layers) and top-8 choices on the full model."""
+    gm, om, _ = full_pair
+    gm.reset()
+    om.reset()
+    worst, lg, lw = step_parity(om, gm, [1, 2, 3], 48)
+    say(f"full model: worst per-layer rel-RMSE {worst:.3g}")
+
+
+def test_full_model_greedy_golden(device):
+    """64 greedy tokens of the full model against the oracle's committed tokens."""
+    path = os.path.join(GOLDEN, "full_greedy.json")
+    if not os.path.exists(path):
+        pytest.skip("full_greedy.json not generated")
+    want = json.load(open(path))
+    gm = K.Model.synthetic(K.qwen3_30b_a3b(**full_config()), seed=want["seed"])
+    lg = gm.forward(want["prompt"])
+    first = int(np.argmax(lg))
+    assert first == want["tokens"][0]
+    got = [first] + list(gm.decode_greedy(first, len(want["tokens"]) - 1))
+    gm.close()
+    assert got == want["tokens"]
