@@ -6,12 +6,12 @@
 // query head h (kv head h / group) scores q.k * 1/sqrt(D) over positions
 // 0..pos, softmax, and sum a*v.
 //
-// One fused launch, split-KV: workgroup (kv head, split) owns 64 cache slots.
-// It normalises and rotates the `group` query heads itself, stages its K and V
+// Split-KV in two launches.  Workgroup (kv head, split) owns 64 cache slots:
+// it normalises and rotates the `group` query heads itself, stages its K and V
 // slots in LDS (the slot being written this step comes from registers, and
 // only the workgroup that owns it writes it to the cache), and emits a partial
-// record {max, sum, sum a*v} per query head.  The last workgroup of each kv
-// head merges that head's partials in ascending split order.
+// record {max, sum, sum a*v} per query head.  A second launch merges each
+// head's partials.
 #include "knj_common.h"
 #include "knj_dev.h"
 
@@ -25,14 +25,12 @@ constexpr int kChunk = 64;
 // q/k normalisation + rotation of one head held as 4 floats per thread in a
 // group of D/4 threads: returns the thread's 4 outputs (elements 4c..4c+3).
 template <int D>
-__device__ __forceinline__ float4 norm_rope4(float4 v, int c, const float* __restrict__ nw,
-                                             float eps, const float* __restrict__ cs,
-                                             const float* __restrict__ sn) {
+__device__ __forceinline__ float4 norm_rope4(float4 v, int c, float4 w, float eps, float4 cs,
+                                             float4 sn) {
   constexpr int T = D / 4;  // threads per head
   float ss = v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
   ss = group_sum<T>(ss);
   const float scale = 1.0f / sqrtf(ss / (float)D + eps);
-  const float4 w = *reinterpret_cast<const float4*>(nw + 4 * c);
   float4 n;
   n.x = v.x * scale * w.x;
   n.y = v.y * scale * w.y;
@@ -45,21 +43,12 @@ __device__ __forceinline__ float4 norm_rope4(float4 v, int c, const float* __res
   p.z = __shfl_xor(n.z, T / 2, 64);
   p.w = __shfl_xor(n.w, T / 2, 64);
   const bool lo = c < T / 2;
-  const int i0 = lo ? 4 * c : 4 * c - D / 2;  // rotation index of element x
+  // (x0, x1) -> (x0*c - x1*s, x0*s + x1*c) with x0 the low-half element
   float4 out;
-  const float e[4] = {n.x, n.y, n.z, n.w};
-  const float q[4] = {p.x, p.y, p.z, p.w};
-  float r[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float cc = cs[i0 + k], s = sn[i0 + k];
-    // (x0, x1) -> (x0*c - x1*s, x0*s + x1*c) with x0 the low-half element
-    r[k] = lo ? (e[k] * cc - q[k] * s) : (q[k] * s + e[k] * cc);
-  }
-  out.x = r[0];
-  out.y = r[1];
-  out.z = r[2];
-  out.w = r[3];
+  out.x = lo ? (n.x * cs.x - p.x * sn.x) : (p.x * sn.x + n.x * cs.x);
+  out.y = lo ? (n.y * cs.y - p.y * sn.y) : (p.y * sn.y + n.y * cs.y);
+  out.z = lo ? (n.z * cs.z - p.z * sn.z) : (p.z * sn.z + n.z * cs.z);
+  out.w = lo ? (n.w * cs.w - p.w * sn.w) : (p.w * sn.w + n.w * cs.w);
   return out;
 }
 
@@ -71,55 +60,59 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   __shared__ uint16_t ks[kChunk * ROWH];
   __shared__ uint16_t vs[kChunk * ROWH];
   __shared__ float es[8 * kChunk];       // exp(score - max) per head
-  __shared__ unsigned int flag;
   const int kvh = blockIdx.x, split = blockIdx.y, n_split = gridDim.y;
   const int G = a.n_head / a.n_head_kv;
-  const int pos = *a.pos;
-  const int n_kv = pos + 1;
-  const int p0 = split * kChunk;
-  const int cnt = min(kChunk, n_kv - p0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int p0 = split * kChunk;
   uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
   uint16_t* vc = a.v_cache + (uint64_t)kvh * a.n_ctx * D;
   float* part = a.partial + ((uint64_t)(kvh * G) * n_split + split) * (D + 2);
   const uint64_t hstride = (uint64_t)n_split * (D + 2);
+  // 1) every load that does not depend on the position first: this chunk's
+  // cache slots (16 bytes per load; rows past the valid length are dropped
+  // later), the raw query/key/value and the norm weights
+  constexpr int PER = (kChunk * D * 2) / (16 * kBlock);  // loads per thread per matrix
+  static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
+  // (named registers rather than an array: an array live across the query
+  // pass below was placed in scratch memory)
+  uint4 k0, k1, k2, k3, v0, v1, v2, v3;
+  auto ld = [&](int j, uint4& kk, uint4& vv) {
+    const int c16 = tid + kBlock * j;
+    const int p = min(p0 + (c16 * 8) / D, a.n_ctx - 1), off = (c16 * 8) % D;
+    kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)p * D + off);
+    vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)p * D + off);
+  };
+  ld(0, k0, v0);
+  ld(1, k1, v1);
+  if constexpr (PER > 2) {
+    ld(2, k2, v2);
+    ld(3, k3, v3);
+  }
+  const int qh = min(tid / T, G - 1), qc = tid % T;
+  const float4 qraw = *reinterpret_cast<const float4*>(a.q + (uint64_t)(kvh * G + qh) * D + 4 * qc);
+  const float4 qnw = *reinterpret_cast<const float4*>(a.q_norm + 4 * qc);
+  const float4 kraw = *reinterpret_cast<const float4*>(a.k + (uint64_t)kvh * D + 4 * qc);
+  const float4 vraw = *reinterpret_cast<const float4*>(a.v + (uint64_t)kvh * D + 4 * qc);
+  const float4 knw = *reinterpret_cast<const float4*>(a.k_norm + 4 * qc);
+  const int pos = *a.pos;
+  const int n_kv = pos + 1;
+  const int cnt = min(kChunk, n_kv - p0);
 
   if (cnt > 0) {
-    // 1) cache loads for this chunk (16 bytes per load, 64*D*2 bytes each of K, V)
-    constexpr int PER = (kChunk * D * 2) / (16 * kBlock);  // loads per thread per matrix
-    static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
-    // (named registers rather than an array: an array live across the query
-    // pass below was placed in scratch memory)
-    uint4 k0, k1, k2, k3, v0, v1, v2, v3;
-    auto ld = [&](int j, uint4& kk, uint4& vv) {
-      const int c16 = tid + kBlock * j;
-      const int p = min((c16 * 8) / D, cnt - 1), off = (c16 * 8) % D;
-      kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)(p0 + p) * D + off);
-      vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)(p0 + p) * D + off);
-    };
-    ld(0, k0, v0);
-    ld(1, k1, v1);
-    if constexpr (PER > 2) {
-      ld(2, k2, v2);
-      ld(3, k3, v3);
-    }
     // 2) queries of this kv head: 4 floats per thread, T threads per head
-    const float* cs = a.rope_cos + (uint64_t)pos * (D / 2);
-    const float* sn = a.rope_sin + (uint64_t)pos * (D / 2);
+    const int ri = (qc < T / 2) ? 4 * qc : 4 * qc - D / 2;  // rotation index of element 4qc
+    const float4 cs = *reinterpret_cast<const float4*>(a.rope_cos + (uint64_t)pos * (D / 2) + ri);
+    const float4 sn = *reinterpret_cast<const float4*>(a.rope_sin + (uint64_t)pos * (D / 2) + ri);
     if (tid < G * T) {
-      const int h = tid / T, c = tid % T;
-      const float4 v = *reinterpret_cast<const float4*>(a.q + (uint64_t)(kvh * G + h) * D + 4 * c);
-      const float4 r = norm_rope4<D>(v, c, a.q_norm, a.eps, cs, sn);
-      *reinterpret_cast<float4*>(qs + h * D + 4 * c) = r;
+      const float4 r = norm_rope4<D>(qraw, qc, qnw, a.eps, cs, sn);
+      *reinterpret_cast<float4*>(qs + qh * D + 4 * qc) = r;
     }
     // 3) the slot written this step, if it is in this chunk
     if (pos >= p0 && pos < p0 + cnt && tid < T) {
       const int c = tid;
-      const float4 v = *reinterpret_cast<const float4*>(a.k + (uint64_t)kvh * D + 4 * c);
-      const float4 r = norm_rope4<D>(v, c, a.k_norm, a.eps, cs, sn);
-      const float4 vv = *reinterpret_cast<const float4*>(a.v + (uint64_t)kvh * D + 4 * c);
+      const float4 r = norm_rope4<D>(kraw, c, knw, a.eps, cs, sn);
       const uint16_t kh[4] = {f2h(r.x), f2h(r.y), f2h(r.z), f2h(r.w)};
-      const uint16_t vh[4] = {f2h(vv.x), f2h(vv.y), f2h(vv.z), f2h(vv.w)};
+      const uint16_t vh[4] = {f2h(vraw.x), f2h(vraw.y), f2h(vraw.z), f2h(vraw.w)};
       const int lp = pos - p0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
@@ -171,11 +164,11 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       es[h0 * kChunk + lane] = e0;
       if (h1 < G) es[h1 * kChunk + lane] = e1;
       if (lane == 0) {
-        publish(part + h0 * hstride + 0, m0);
-        publish(part + h0 * hstride + 1, l0);
+        *(part + h0 * hstride + 0) = m0;
+        *(part + h0 * hstride + 1) = l0;
         if (h1 < G) {
-          publish(part + h1 * hstride + 0, m1);
-          publish(part + h1 * hstride + 1, l1);
+          *(part + h1 * hstride + 0) = m1;
+          *(part + h1 * hstride + 1) = l1;
         }
       }
       // 5) sum a*v for the wave's two heads; lane owns dims (2*lane, 2*lane+1)
@@ -194,73 +187,77 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
             a11 += eb * v1;
           }
         }
-        publish(part + h0 * hstride + 2 + 2 * lane, a00);
-        publish(part + h0 * hstride + 3 + 2 * lane, a01);
+        *(part + h0 * hstride + 2 + 2 * lane) = a00;
+        *(part + h0 * hstride + 3 + 2 * lane) = a01;
         if (h1 < G) {
-          publish(part + h1 * hstride + 2 + 2 * lane, a10);
-          publish(part + h1 * hstride + 3 + 2 * lane, a11);
+          *(part + h1 * hstride + 2 + 2 * lane) = a10;
+          *(part + h1 * hstride + 3 + 2 * lane) = a11;
         }
       }
     }
   } else {
     for (int i = tid; i < G * (D + 2); i += kBlock) {
       const int g = i / (D + 2), j = i % (D + 2);
-      publish(part + g * hstride + j, (j == 0) ? -INFINITY : 0.0f);
+      *(part + g * hstride + j) = (j == 0) ? -INFINITY : 0.0f;
     }
   }
 
-  // 6) merge: the last workgroup of this kv head combines all splits.  Only
-  // splits that hold positions (ceil(n_kv / chunk)) are read; per head the
-  // split maxima and sums go through LDS, then each thread folds its 4 dims
-  // over the splits in ascending order.
-  if (!last_block_done(a.counter + kvh, n_split, &flag)) return;
-  __shared__ float ms[8][64];   // exp(m_s - M) per head and split (<= 64 live splits per pass)
+}
+
+// Merge of the split partials of one query head (one workgroup per head):
+// M = max m_s, f_s = exp(m_s - M), out = sum_s acc_s f_s / sum_s l_s f_s over
+// the splits that hold positions.  Threads [0, D) and [D, 2D) each fold half of
+// the splits (all loads issued before the sums); the halves are added in split
+// order.
+template <int D>
+__global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) {
+  __shared__ float fs[1024];
+  __shared__ float red[8];
+  const int h = blockIdx.x, tid = threadIdx.x;
+  const int n_kv = *a.pos + 1;
   const int live = min(n_split, (n_kv + kChunk - 1) / kChunk);
-  constexpr int TPH = D / 4;  // threads per head in the fold
-  const int h = tid / TPH, c = tid % TPH;
-  const bool hv = h < G;
-  const float* ph = a.partial + (uint64_t)(kvh * G + (hv ? h : 0)) * n_split * (D + 2);
-  // per-head max over live splits
+  const float* ph = a.partial + (uint64_t)h * n_split * (D + 2);
+  float m_own[4], l_own[4];
   float M = -INFINITY;
-  if (hv)
-    for (int s2 = c; s2 < live; s2 += TPH) M = fmaxf(M, ld_acquire_f(ph + (uint64_t)s2 * (D + 2)));
-  M = group_max<TPH>(M);
-  float4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  float L = 0.0f;
-  for (int base = 0; base < live; base += 64) {
-    const int nb = min(64, live - base);
-    // weights f_s = exp(m_s - M) and the sum L = sum l_s f_s for this pass
-    float lpart = 0.0f;
-    if (hv)
-      for (int s2 = c; s2 < nb; s2 += TPH) {
-        const float m = ld_acquire_f(ph + (uint64_t)(base + s2) * (D + 2));
-        const float f = (m == -INFINITY) ? 0.0f : expf(m - M);
-        ms[h][s2] = f;
-        lpart += ld_acquire_f(ph + (uint64_t)(base + s2) * (D + 2) + 1) * f;
-      }
-    lpart = group_sum<TPH>(lpart);
-    __syncthreads();
-    if (hv) {
-      L += lpart;
-#pragma unroll 4
-      for (int s2 = 0; s2 < nb; ++s2) {
-        const float f = ms[h][s2];
-        const float* pa = ph + (uint64_t)(base + s2) * (D + 2) + 2 + 4 * c;
-        acc.x += ld_acquire_f(pa + 0) * f;
-        acc.y += ld_acquire_f(pa + 1) * f;
-        acc.z += ld_acquire_f(pa + 2) * f;
-        acc.w += ld_acquire_f(pa + 3) * f;
-      }
-    }
-    __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s2 = tid + kBlock * j;
+    m_own[j] = s2 < live ? ph[(uint64_t)s2 * (D + 2)] : -INFINITY;
+    l_own[j] = s2 < live ? ph[(uint64_t)s2 * (D + 2) + 1] : 0.0f;
+    M = fmaxf(M, m_own[j]);
   }
-  if (!hv) return;
-  float4 o;
-  o.x = acc.x / L;
-  o.y = acc.y / L;
-  o.z = acc.z / L;
-  o.w = acc.w / L;
-  *reinterpret_cast<float4*>(a.out + (uint64_t)(kvh * G + h) * D + 4 * c) = o;
+  M = group_max<64>(M);
+  if ((tid & 63) == 0) red[tid >> 6] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float lsum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s2 = tid + kBlock * j;
+    if (s2 < live) {
+      const float f = m_own[j] == -INFINITY ? 0.0f : expf(m_own[j] - M);
+      fs[s2] = f;
+      lsum += l_own[j] * f;
+    }
+  }
+  const float L = block_sum(lsum, red);  // includes the barrier that publishes fs
+  const int d = tid % D, part = tid / D;  // part 0/1 for D = 128; 0..3 for D = 64
+  constexpr int NP = kBlock / D;
+  const int per = (live + NP - 1) / NP;
+  const int s0 = part * per, s1 = min(live, s0 + per);
+  float acc = 0.0f;
+#pragma unroll 8
+  for (int s2 = s0; s2 < s1; ++s2) acc += ph[(uint64_t)s2 * (D + 2) + 2 + d] * fs[s2];
+  // fold the parts in order: part 0 + part 1 (+ 2 + 3)
+  __shared__ float parts[kBlock];
+  parts[tid] = acc;
+  __syncthreads();
+  if (tid < D) {
+    float o = parts[tid];
+    for (int q = 1; q < NP; ++q) o += parts[tid + q * D];
+    a.out[(uint64_t)h * D + tid] = o / L;
+  }
 }
 
 }  // namespace
@@ -269,10 +266,13 @@ int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   const int n_split = attn_splits(a.n_ctx);
+  if (n_split > 1024) return hipErrorInvalidValue;
   if (a.head_dim == 128) {
     hipLaunchKernelGGL(k_attention<128>, dim3(a.n_head_kv, n_split), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_head), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
     hipLaunchKernelGGL(k_attention<64>, dim3(a.n_head_kv, n_split), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_attn_merge<64>, dim3(a.n_head), dim3(kBlock), 0, s, a, n_split);
   } else {
     return hipErrorInvalidValue;
   }

@@ -72,15 +72,20 @@ struct RouterArgs {
   int n_embd, n_expert, k;
   float* hx;              // normalised x written for the expert kernels
   float* logits;          // [n_expert]
-  int32_t* topk_idx;      // [k], selection order
+  int32_t* topk_idx;      // [k], selection order (null: logits only)
   float* topk_w;          // [k]
   unsigned int* counter;  // zero-initialised ticket, left at zero on exit
 };
 hipError_t launch_router(const RouterArgs& a, hipStream_t s);
+// Softmax + top-k of n_expert logits by one workgroup (the C-ABI router).
+hipError_t launch_topk(const float* logits, int n_expert, int k, int32_t* idx, float* w,
+                       hipStream_t s);
 
 struct ExpertArgs {
-  const float* hx;        // [n_embd] normalised input
-  const int32_t* topk_idx;
+  const float* hx;        // [n_embd] input of gate/up: RMSNorm(hx, norm_w) when norm_w is
+  const float* norm_w;    // set (the residual stream and ffn_norm), else used as is
+  float eps;
+  const int32_t* topk_idx;  // routing (launch_topk's output)
   const float* topk_w;
   const uint8_t* gate;    // [n_expert] slabs
   const uint8_t* up;
@@ -113,7 +118,6 @@ struct AttnArgs {
   int n_head, n_head_kv, head_dim, n_ctx;
   float scale;
   float* partial;            // [n_head][n_split][D + 2] scratch
-  unsigned int* counter;     // n_head_kv zero-initialised tickets
   float* out;                // [n_head][D]
 };
 int attn_splits(int n_ctx);
@@ -129,8 +133,11 @@ struct StepState {
   int32_t pad;
   unsigned long long key;
 };
-hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int32_t* out_tokens,
-                             int max_steps, hipStream_t s);
+hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int nkeys,
+                             int32_t* out_tokens, int max_steps, hipStream_t s);
+// Workgroups launch_gemv uses for an n_out x n_in GEMV of `type` (the number of
+// argmax keys it writes).
+int gemv_grid(int type, int n_in, int n_out);
 
 // Embedding row of st->token into x.
 hipError_t launch_embed(int type, const uint8_t* table, int n_embd, StepState* st, float* x,

@@ -190,6 +190,49 @@ __device__ __forceinline__ void xslice_load(const float* xs_pad, int slice, XSli
   x.s1 = b;
 }
 
+// The 64 activations of slice `slice` read straight from global memory into
+// registers, optionally RMS-normalised.  The sum of squares is reduced over the
+// W lanes of the row group, which together hold all of x (n_in <= 64*W); lanes
+// with no slice contribute zero.  No LDS and no workgroup barrier.
+template <int W>
+__device__ __forceinline__ void xslice_global(const float* __restrict__ x,
+                                              const float* __restrict__ nw, float eps, int n,
+                                              int slice, bool active, XSlice& xv) {
+  float ss = 0.0f;
+  const float* p = x + 64 * slice;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float4 t = active ? *reinterpret_cast<const float4*>(p + 4 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    xv.v[4 * k] = t.x;
+    xv.v[4 * k + 1] = t.y;
+    xv.v[4 * k + 2] = t.z;
+    xv.v[4 * k + 3] = t.w;
+  }
+  if (nw) {
+#pragma unroll
+    for (int l = 0; l < 64; ++l) ss += xv.v[l] * xv.v[l];
+    ss = group_sum<W>(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    const float* q = nw + 64 * slice;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float4 w = active ? *reinterpret_cast<const float4*>(q + 4 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
+      xv.v[4 * k] = xv.v[4 * k] * scale * w.x;
+      xv.v[4 * k + 1] = xv.v[4 * k + 1] * scale * w.y;
+      xv.v[4 * k + 2] = xv.v[4 * k + 2] * scale * w.z;
+      xv.v[4 * k + 3] = xv.v[4 * k + 3] * scale * w.w;
+    }
+  }
+  float a = 0.0f, b = 0.0f;
+#pragma unroll
+  for (int l = 0; l < 32; ++l) {
+    a += xv.v[l];
+    b += xv.v[32 + l];
+  }
+  xv.s0 = a;
+  xv.s1 = b;
+}
+
 __device__ __forceinline__ void q4k_codes16(uint4 q, const float* xlo, const float* xhi, float& slo,
                                             float& shi) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};

@@ -285,9 +285,9 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
   RouterArgs ra{x, norm_w, eps, router_w, n_embd, n_expert, k, hx, logits, topk_idx, topk_w,
                 device_counters()};
   KNJ_HIP(launch_router(ra, s));
-  ExpertArgs ea{hx,    topk_idx, topk_w, (const uint8_t*)gate, (const uint8_t*)up,
-                (const uint8_t*)down, type_gate_up, type_down, n_embd, n_ff, n_expert, k, act,
-                resid, out, nullptr};
+  ExpertArgs ea{x, norm_w, eps, topk_idx, topk_w, (const uint8_t*)gate,
+                (const uint8_t*)up, (const uint8_t*)down, type_gate_up, type_down, n_embd, n_ff,
+                n_expert, k, act, resid, out, nullptr};
   KNJ_HIP(launch_experts(ea, s));
   return KNJ_OK;
 }
@@ -326,8 +326,7 @@ int knj_attention_step(const float* q, const float* k, const float* v, const flo
   const float* cs = (const float*)((uintptr_t)dtab - (uintptr_t)pos * half * 4);
   const float* sn = (const float*)((uintptr_t)(dtab + half) - (uintptr_t)pos * half * 4);
   AttnArgs a{q, k, v, q_norm, k_norm, eps, cs, sn, dpos, k_cache, v_cache, n_head, n_head_kv,
-             head_dim, n_ctx, 1.0f / std::sqrt((float)head_dim), (float*)(scr + 1024),
-             device_counters() + 64, out};
+             head_dim, n_ctx, 1.0f / std::sqrt((float)head_dim), (float*)(scr + 1024), out};
   KNJ_HIP(launch_attention(a, s));
   KNJ_HIP(hipStreamSynchronize(s));  // the host table must outlive the copy
   return KNJ_OK;

@@ -32,16 +32,16 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__
   const uint64_t rb = (uint64_t)(n_in >> 8) * KNJ_Q4K_BLOCK;
   const int row0 = (blockIdx.x * (kBlock / 64) + wave) * (RS * RPW);
   const bool active = sub < nslices;
-  const int b = sub >> 2, g = sub & 3;
+  const int b = active ? (sub >> 2) : 0, g = sub & 3;
   Q4Slice q[RS];
 #pragma unroll
   for (int st = 0; st < RS; ++st) {
-    const int row = row0 + st * RPW + rsub;
-    if (active && row < n_out) q[st] = q4k_load(w + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+    const int row = min(row0 + st * RPW + rsub, n_out - 1);  // valid address; extra rows dropped
+    q[st] = q4k_load(w + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
   }
   stage_x(x, nw, eps, n_in, xs, red);
   XSlice xv;
-  if (active) xslice_load(xs, sub, xv);
+  xslice_load(xs, active ? sub : 0, xv);
 #pragma unroll
   for (int st = 0; st < RS; ++st) {
     const int row = row0 + st * RPW + rsub;
@@ -170,8 +170,6 @@ __global__ __launch_bounds__(kBlock) void k_gemv_bf16(const uint8_t* __restrict_
                                                       const float* __restrict__ resid,
                                                       float* __restrict__ y,
                                                       unsigned long long* argmax) {
-  __shared__ float xs[xpad_size(4096)];
-  __shared__ float red[8];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int nwaves = gridDim.x * (kBlock / 64);
   const int wave_g = blockIdx.x * (kBlock / 64) + wave;
@@ -181,18 +179,36 @@ __global__ __launch_bounds__(kBlock) void k_gemv_bf16(const uint8_t* __restrict_
 #pragma unroll
   for (int r = 0; r < RS; ++r)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-      if (base + r < n_out)
-        cur[r][j] = *reinterpret_cast<const uint4*>(w + (uint64_t)(base + r) * rb + 16 * (lane + 64 * j));
-  stage_x(x, nw, eps, n_in, xs, red);
+    for (int j = 0; j < NJ; ++j) {
+      const int row = min(base + r, n_out - 1);
+      cur[r][j] = *reinterpret_cast<const uint4*>(w + (uint64_t)row * rb + 16 * (lane + 64 * j));
+    }
+  // the lane's 8*NJ activations straight into registers; the wave holds all of
+  // x, so the RMSNorm sum is a wave reduction
   float xv[NJ][8];
+  float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int i = 8 * lane + 512 * j;
-    const float4 a = *reinterpret_cast<const float4*>(xs + xpad(i));
-    const float4 c = *reinterpret_cast<const float4*>(xs + xpad(i + 4));
+    const float4 a = *reinterpret_cast<const float4*>(x + i);
+    const float4 c = *reinterpret_cast<const float4*>(x + i + 4);
     xv[j][0] = a.x; xv[j][1] = a.y; xv[j][2] = a.z; xv[j][3] = a.w;
     xv[j][4] = c.x; xv[j][5] = c.y; xv[j][6] = c.z; xv[j][7] = c.w;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) ss += xv[j][k] * xv[j][k];
+  }
+  if (nw) {
+    ss = group_sum<64>(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)n_in + eps);
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int i = 8 * lane + 512 * j;
+      const float4 a = *reinterpret_cast<const float4*>(nw + i);
+      const float4 c = *reinterpret_cast<const float4*>(nw + i + 4);
+      const float wv[8] = {a.x, a.y, a.z, a.w, c.x, c.y, c.z, c.w};
+#pragma unroll
+      for (int k = 0; k < 8; ++k) xv[j][k] = xv[j][k] * scale * wv[k];
+    }
   }
   unsigned long long best = 0;
   for (; base < n_out; base += nwaves * RS) {
@@ -311,11 +327,12 @@ __global__ __launch_bounds__(kBlock) void k_gemv_plain(const uint8_t* __restrict
 // token (first maximum wins, /root/reference/src/cli/main.cpp:126-132) and the
 // device-side position advances.
 __global__ __launch_bounds__(kBlock) void k_step_close(StepState* st, const unsigned long long* keys,
-                                                       int32_t* out_tokens, int max_steps) {
+                                                       int nkeys, int32_t* out_tokens, int max_steps) {
   unsigned long long best = 0;
 #pragma unroll
   for (int j = 0; j < kMaxKeys / kBlock; ++j) {
-    const unsigned long long k = keys[threadIdx.x + kBlock * j];
+    const int i = threadIdx.x + kBlock * j;
+    const unsigned long long k = i < nkeys ? keys[i] : 0ull;
     best = k > best ? k : best;
   }
   __shared__ unsigned long long wb[4];
@@ -344,6 +361,21 @@ int pow2_at_least(int v) {
 }
 
 }  // namespace
+
+// Grids of the argmax-capable GEMVs (Q6_K, BF16, F32); one key per workgroup.
+int gemv_grid(int type, int n_in, int n_out) {
+  if (type == KNJ_TYPE_Q6_K) {
+    const int lpr = std::min(64, pow2_at_least(8 * (n_in / KNJ_QK)));
+    const int rows_per_block = 4 * (64 / lpr);
+    return std::max(1, std::min(kMaxKeys, (n_out + rows_per_block - 1) / rows_per_block));
+  }
+  if (type == KNJ_TYPE_BF16 && n_in % 512 == 0 && n_in <= 4096 && n_in / 512 != 3) {
+    constexpr int RS = 4;
+    const int waves_needed = (n_out + RS - 1) / RS;
+    return std::max(1, std::min(512, (waves_needed + 3) / 4));
+  }
+  return std::max(1, std::min(kMaxKeys, (n_out + 3) / 4));
+}
 
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (a.type == KNJ_TYPE_Q4_K) {
@@ -374,8 +406,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
   if (a.type == KNJ_TYPE_Q6_K) {
     const int lpr = std::min(64, pow2_at_least(8 * (a.n_in / KNJ_QK)));
     const size_t lds = (size_t)a.n_in * 4;
-    const int rows_per_block = 4 * (64 / lpr);
-    const int grid = std::max(1, std::min(kMaxKeys, (a.n_out + rows_per_block - 1) / rows_per_block));
+    const int grid = gemv_grid(a.type, a.n_in, a.n_out);
 #define G6(L)                                                                                 \
   if (lpr == L) {                                                                             \
     hipLaunchKernelGGL(k_gemv_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, \
@@ -386,11 +417,10 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
 #undef G6
     return hipErrorInvalidValue;
   }
-  if (a.type == KNJ_TYPE_BF16 && a.n_in % 512 == 0 && a.n_in <= 4096) {
+  if (a.type == KNJ_TYPE_BF16 && a.n_in % 512 == 0 && a.n_in <= 4096 && a.n_in / 512 != 3) {
     const int nj = a.n_in / 512;
     constexpr int RS = 4;
-    const int waves_needed = (a.n_out + RS - 1) / RS;
-    const int grid = std::max(1, std::min(512, (waves_needed + 3) / 4));
+    const int grid = gemv_grid(a.type, a.n_in, a.n_out);
 #define GB(J)                                                                                   \
   if (nj == J) {                                                                                \
     hipLaunchKernelGGL((k_gemv_bf16<J, RS>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,     \
@@ -399,10 +429,9 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
   }
     GB(1) GB(2) GB(4) GB(8)
 #undef GB
-    if (nj == 3 || nj > 4) { /* fall through to the generic kernel */ }
   }
   const size_t lds = (size_t)a.n_in * 4;
-  const int grid = std::max(1, std::min(kMaxKeys, (a.n_out + 3) / 4));
+  const int grid = gemv_grid(KNJ_TYPE_F32, a.n_in, a.n_out);
   if (a.type == KNJ_TYPE_BF16) {
     hipLaunchKernelGGL(k_gemv_plain<true>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out,
                        a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
@@ -413,9 +442,10 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int32_t* out_tokens,
-                             int max_steps, hipStream_t s) {
-  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(kBlock), 0, s, st, keys, out_tokens, max_steps);
+hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int nkeys,
+                             int32_t* out_tokens, int max_steps, hipStream_t s) {
+  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(kBlock), 0, s, st, keys, nkeys, out_tokens,
+                     max_steps);
   return hipGetLastError();
 }
 

@@ -252,7 +252,7 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
               reinterpret_cast<const float*>(img + lo.q_norm),
               reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos, m->rope_sin,
               &m->st->pos, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head, c.n_head_kv, D, c.n_ctx,
-              1.0f / std::sqrt((float)D), m->attn_part, m->counter + 64, m->ctx};
+              1.0f / std::sqrt((float)D), m->attn_part, m->ctx};
   KNJ_HIP(launch_attention(at, s));
   GemvArgs o{c.type_attn, img + lo.wo, QD, H, m->ctx, nullptr, 0.0f, m->x, m->x, nullptr};
   KNJ_HIP(launch_gemv(o, s));
@@ -262,8 +262,10 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
                 m->topk_idx + (uint64_t)il * c.n_expert_used, m->topk_w + (uint64_t)il * c.n_expert_used,
                 m->counter};
   KNJ_HIP(launch_router(ra, s));
-  ExpertArgs ea{m->hx, m->topk_idx + (uint64_t)il * c.n_expert_used,
-                m->topk_w + (uint64_t)il * c.n_expert_used, img + lo.gate, img + lo.up, img + lo.down,
+  int32_t* ti = m->topk_idx + (uint64_t)il * c.n_expert_used;
+  float* tw = m->topk_w + (uint64_t)il * c.n_expert_used;
+  ExpertArgs ea{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps, ti, tw,
+                img + lo.gate, img + lo.up, img + lo.down,
                 c.type_gate_up, c.type_down, H, c.n_ff, c.n_expert, c.n_expert_used, m->act, m->x,
                 m->x, m->hidden + (uint64_t)il * H};
   KNJ_HIP(launch_experts(ea, s));
@@ -285,7 +287,8 @@ int enqueue_step(knj_model* m, hipStream_t s) {
                 reinterpret_cast<const float*>(m->image + m->off_onorm), c.rms_eps, nullptr,
                 m->logits, m->keys};
   KNJ_HIP(launch_gemv(head, s));
-  KNJ_HIP(launch_step_close(m->st, m->keys, m->out_tokens, m->max_steps, s));
+  KNJ_HIP(launch_step_close(m->st, m->keys, gemv_grid(c.type_head, c.n_embd, c.n_vocab),
+                            m->out_tokens, m->max_steps, s));
   return KNJ_OK;
 }
 
@@ -525,7 +528,7 @@ int knj_model_time_experts(knj_model* m, int iters, float* us_gateup, float* us_
     for (int i = 0; i < iters; ++i) {
       const int il = i % c.n_layer;  // rotate so repeats come from HBM
       const knj_layer_offsets& lo = m->lo[il];
-      ExpertArgs ea{m->hx, m->topk_idx + (uint64_t)il * c.n_expert_used,
+      ExpertArgs ea{m->hx, nullptr, 0.0f, m->topk_idx + (uint64_t)il * c.n_expert_used,
                     m->topk_w + (uint64_t)il * c.n_expert_used, m->image + lo.gate, m->image + lo.up,
                     m->image + lo.down, c.type_gate_up, c.type_down, c.n_embd, c.n_ff, c.n_expert,
                     c.n_expert_used, m->act, nullptr, m->ctx, nullptr};

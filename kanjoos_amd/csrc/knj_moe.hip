@@ -17,18 +17,78 @@ namespace {
 
 using namespace dev;
 
+// Softmax over the n_expert logits and the top-k by rank: rank(e) = #{e' :
+// p' > p or (p' == p and e' < e)}, which is exactly the reference's repeated
+// strict-'>' argmax order (model.cpp:442-451); the kept weights are
+// renormalised by their sum in selection order (model.cpp:452-458).  All 256
+// threads of the workgroup take part; results land in LDS.
+template <bool COHERENT>
+__device__ __forceinline__ void router_topk(const float* __restrict__ logits, int n_expert, int k, int* sel_idx,
+                            float* sel_w, float* probs, float* red) {
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const float lg = t < n_expert ? (COHERENT ? ld_acquire_f(logits + t) : logits[t]) : -INFINITY;
+  float mx = group_max<64>(lg);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  const float ex = t < n_expert ? expf(lg - mx) : 0.0f;
+  const float sum = block_sum(ex, red);
+  const float p = t < n_expert ? ex / sum : -1.0f;
+  probs[t] = p;
+  __syncthreads();
+  // rank(e) = #{e' : key(e') > key(e)} with key = (probability bits << 8) |
+  // (255 - e): probabilities are non-negative, so their bit patterns order like
+  // the values, and the low byte breaks ties toward the lower index.  Two
+  // threads per expert (n_expert <= 128) each count half of the candidates,
+  // with every LDS read of a pass issued before its compares.
+  __shared__ int rank_half[256];
+  __shared__ unsigned long long keys[256];
+  const int E2 = n_expert <= 128 ? 2 : 1;
+  const int e = E2 == 2 ? (t & 127) : t;
+  const int part = E2 == 2 ? (t >> 7) : 0;
+  if (t < n_expert) keys[t] = ((unsigned long long)__float_as_uint(p) << 8) | (unsigned)(255 - t);
+  __syncthreads();
+  int rank = 0;
+  if (e < n_expert) {
+    const unsigned long long me = keys[e];
+    const int per = (n_expert + E2 - 1) / E2;
+    const int lo = part * per, hi = min(n_expert, lo + per);
+    for (int base = lo; base < hi; base += 64) {
+      unsigned long long kv[64];
+#pragma unroll
+      for (int j = 0; j < 64; ++j) kv[j] = keys[min(base + j, 255)];
+#pragma unroll
+      for (int j = 0; j < 64; ++j) rank += (base + j < hi && kv[j] > me) ? 1 : 0;
+    }
+  }
+  rank_half[t] = rank;
+  __syncthreads();
+  if (t < n_expert) {
+    const int r = E2 == 2 ? rank_half[t] + rank_half[t + 128] : rank_half[t];
+    if (r < k) {
+      sel_idx[r] = t;
+      sel_w[r] = p;
+    }
+  }
+  __syncthreads();
+  if (t == 0) {
+    float keep = 0.0f;
+    for (int q = 0; q < k; ++q) keep += sel_w[q];
+    const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
+    for (int q = 0; q < k; ++q) sel_w[q] = sel_w[q] * inv;
+  }
+  __syncthreads();
+}
+
 // ------------------------------------------------------------------ router
 // One wave per expert row (4 per workgroup).  Each wave normalises x itself
-// (no workgroup barrier before the dot); workgroup 0 publishes hx.  The last
-// workgroup to finish ranks all experts: rank(e) = #{e' : p' > p or (p' == p
-// and e' < e)}, which is exactly the reference's repeated-argmax order.
+// (no workgroup barrier before the dot); workgroup 0 writes hx.  The logits
+// are published (agent-scope stores) and, when a routing output is given, the
+// last workgroup to finish computes softmax and top-k (router_topk).
 __global__ __launch_bounds__(kBlock) void k_router(RouterArgs a) {
-  __shared__ __align__(16) float probs[256];
-  __shared__ float red[8];
-  __shared__ unsigned int flag;
-  __shared__ float chosen_p[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int e = blockIdx.x * (kBlock / 64) + wave;
+  const int e = blockIdx.x * (blockDim.x / 64) + wave;
   const int H = a.n_embd;
   const int nj = H / 256;  // float4 per lane
   float4 wv[16];
@@ -77,42 +137,32 @@ __global__ __launch_bounds__(kBlock) void k_router(RouterArgs a) {
     acc = group_sum<64>(acc);
     if (lane == 0) publish(a.logits + e, acc);
   }
+  if (!a.topk_idx) return;
+  // the last workgroup to finish turns the logits into the routing
+  __shared__ unsigned int flag;
+  __shared__ __align__(16) float probs[256];
+  __shared__ float red[8];
+  __shared__ int sel_idx[16];
+  __shared__ float sel_w[16];
   if (!last_block_done(a.counter, gridDim.x, &flag)) return;
-  // softmax over all experts
-  const int t = threadIdx.x;
-  const float lg = t < a.n_expert ? ld_acquire_f(a.logits + t) : -INFINITY;
-  float mx = group_max<64>(lg);
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-  const float ex = t < a.n_expert ? expf(lg - mx) : 0.0f;
-  const float sum = block_sum(ex, red);
-  const float p = t < a.n_expert ? ex / sum : -1.0f;
-  probs[t] = p;
-  __syncthreads();
-  if (t < a.n_expert) {
-    // four candidates per LDS read, independent iterations
-    int rank = 0;
-#pragma unroll 8
-    for (int o = 0; o < 256; o += 4) {
-      const float4 q = *reinterpret_cast<const float4*>(probs + o);
-      rank += (q.x > p || (q.x == p && o < t)) ? 1 : 0;
-      rank += (q.y > p || (q.y == p && o + 1 < t)) ? 1 : 0;
-      rank += (q.z > p || (q.z == p && o + 2 < t)) ? 1 : 0;
-      rank += (q.w > p || (q.w == p && o + 3 < t)) ? 1 : 0;
-    }
-    if (rank < a.k) {
-      a.topk_idx[rank] = t;
-      chosen_p[rank] = p;
-    }
+  router_topk<true>(a.logits, a.n_expert, a.k, sel_idx, sel_w, probs, red);
+  if (threadIdx.x < a.k) {
+    a.topk_idx[threadIdx.x] = sel_idx[threadIdx.x];
+    a.topk_w[threadIdx.x] = sel_w[threadIdx.x];
   }
-  __syncthreads();
-  if (t == 0) {
-    float keep = 0.0f;
-    for (int k = 0; k < a.k; ++k) keep += chosen_p[k];
-    const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
-    for (int k = 0; k < a.k; ++k) a.topk_w[k] = chosen_p[k] * inv;
+}
+
+// Stand-alone top-k (the C-ABI router): one workgroup.
+__global__ __launch_bounds__(kBlock) void k_topk(const float* __restrict__ logits, int n_expert,
+                                                 int k, int32_t* topk_idx, float* topk_w) {
+  __shared__ __align__(16) float probs[256];
+  __shared__ float red[8];
+  __shared__ int sel_idx[16];
+  __shared__ float sel_w[16];
+  router_topk<false>(logits, n_expert, k, sel_idx, sel_w, probs, red);
+  if (threadIdx.x < k) {
+    topk_idx[threadIdx.x] = sel_idx[threadIdx.x];
+    topk_w[threadIdx.x] = sel_w[threadIdx.x];
   }
 }
 
@@ -124,6 +174,9 @@ template <int RS>
 __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   __shared__ float xs[xpad_size(2048)];
   __shared__ float red[8];
+  __shared__ int sel_idx[16];
+  if (threadIdx.x < a.k) sel_idx[threadIdx.x] = a.topk_idx[threadIdx.x];
+  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, sub = lane & 31;
   const int nslices = a.n_embd >> 6;
@@ -134,23 +187,24 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   const int pair0 = (blockIdx.x * (kBlock / 64) + wave) * RS;
   const int b = sub >> 2, g = sub & 3;
   const uint8_t* base = half ? a.up : a.gate;
-  Q4Slice q[RS];
-#pragma unroll
-  for (int st = 0; st < RS; ++st) {
-    const int pr = pair0 + st;
-    if (active && pr < npairs) {
-      const int kk = pr / a.n_ff, row = pr - kk * a.n_ff;
-      const int e = a.topk_idx[kk];
-      q[st] = q4k_load(base + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
-    }
-  }
-  stage_x(a.hx, nullptr, 0.0f, a.n_embd, xs, red);
+  static_assert(RS == 2, "two row pairs per wave");
+  // named registers (an indexed array was placed in scratch memory here)
+  Q4Slice q0, q1;
+  auto load_pair = [&](int pr, Q4Slice& q) {
+    const int prc = min(pr, npairs - 1);  // always a valid row; unused results are dropped
+    const int kk = prc / a.n_ff, row = prc - kk * a.n_ff;
+    const int e = sel_idx[kk];
+    q = q4k_load(base + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)(active ? b : 0) * KNJ_Q4K_BLOCK, g);
+  };
+  load_pair(pair0, q0);
+  load_pair(pair0 + 1, q1);
+  stage_x(a.hx, a.norm_w, a.eps, a.n_embd, xs, red);
   XSlice xv;
-  if (active) xslice_load(xs, sub, xv);
+  xslice_load(xs, active ? sub : 0, xv);
 #pragma unroll
   for (int st = 0; st < RS; ++st) {
     const int pr = pair0 + st;
-    float acc = (active && pr < npairs) ? q4k_dot(q[st], g, xv) : 0.0f;
+    float acc = (active && pr < npairs) ? q4k_dot(st == 0 ? q0 : q1, g, xv) : 0.0f;
     acc = group_sum<32>(acc);
     const float u = __shfl(acc, 32, 64);
     if (lane == 0 && pr < npairs) {
@@ -163,9 +217,30 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
 // Reference-shaped fallback for n_embd > 2048: 32 lanes per row, loop.
 __global__ __launch_bounds__(kBlock) void k_expert_gateup_wide(ExpertArgs a) {
   extern __shared__ float xw[];
+  __shared__ float red[8];
+  __shared__ int sel_idx[16];
+  if (threadIdx.x < a.k) sel_idx[threadIdx.x] = a.topk_idx[threadIdx.x];
+  __syncthreads();
   const int H = a.n_embd;
-  for (int i = 4 * threadIdx.x; i < H; i += 4 * kBlock)
-    *reinterpret_cast<float4*>(xw + xpad(i)) = *reinterpret_cast<const float4*>(a.hx + i);
+  float ss = 0.0f;
+  for (int i = 4 * threadIdx.x; i < H; i += 4 * kBlock) {
+    const float4 v = *reinterpret_cast<const float4*>(a.hx + i);
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+    *reinterpret_cast<float4*>(xw + xpad(i)) = v;
+  }
+  if (a.norm_w) {
+    ss = block_sum(ss, red);
+    const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
+    for (int i = 4 * threadIdx.x; i < H; i += 4 * kBlock) {
+      float4 v = *reinterpret_cast<float4*>(xw + xpad(i));
+      const float4 w = *reinterpret_cast<const float4*>(a.norm_w + i);
+      v.x = v.x * scale * w.x;
+      v.y = v.y * scale * w.y;
+      v.z = v.z * scale * w.z;
+      v.w = v.w * scale * w.w;
+      *reinterpret_cast<float4*>(xw + xpad(i)) = v;
+    }
+  }
   __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int half = lane >> 5, sub = lane & 31;
@@ -175,7 +250,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup_wide(ExpertArgs a) {
   const int npairs = a.k * a.n_ff;
   for (int pr = blockIdx.x * (kBlock / 64) + wave; pr < npairs; pr += gridDim.x * (kBlock / 64)) {
     const int kk = pr / a.n_ff, row = pr - kk * a.n_ff;
-    const int e = a.topk_idx[kk];
+    const int e = sel_idx[kk];
     const uint8_t* rp = (half ? a.up : a.gate) + (uint64_t)e * slab + (uint64_t)row * rb;
     float acc = 0.0f;
     for (int s = sub; s < nslices; s += 32) {
@@ -212,32 +287,35 @@ __device__ __forceinline__ float combine_sorted(const float* dots, const int32_t
 
 // ------------------------------------------------------------------ down (Q4_K)
 // Wave = one output row for all k experts: 16-lane group gi takes expert slots
-// gi, gi+4, ...; one 64-weight slice per lane (n_ff <= 1024).  The k
-// activation vectors are staged in LDS once per workgroup.
+// gi, gi+4, ...; one 64-weight slice per lane (n_ff <= 1024).  The k activation
+// vectors are staged in LDS once per workgroup.  Slot order is then folded
+// into ascending expert order by lane 0.
 template <int KPG>
 __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   extern __shared__ float acts[];  // [k][xpad_size(n_ff)]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int gi = lane >> 4, sub = lane & 15;
   const int F = a.n_ff, K = a.k;
-  const int fpad = xpad_size(F);
   const int nslices = F >> 6;
   const bool active = sub < nslices;
   const uint64_t rb = (uint64_t)(F >> 8) * KNJ_Q4K_BLOCK;
   const uint64_t slab = rb * (uint64_t)a.n_embd;
-  const int row = blockIdx.x * (kBlock / 64) + wave;
-  const int b = sub >> 2, g = sub & 3;
-  Q4Slice q[KPG];
+  const int row = min((int)(blockIdx.x * (kBlock / 64) + wave), a.n_embd - 1);
+  const bool row_ok = (int)(blockIdx.x * (kBlock / 64) + wave) < a.n_embd;
+  const int b = active ? (sub >> 2) : 0, g = sub & 3;
   int eid[KPG];
 #pragma unroll
   for (int j = 0; j < KPG; ++j) {
-    const int kk = gi + 4 * j;
-    eid[j] = kk < K ? a.topk_idx[kk] : -1;
-    if (active && kk < K && row < a.n_embd)
-      q[j] = q4k_load(a.down + (uint64_t)eid[j] * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+    const int kk = min(gi + 4 * j, K - 1);
+    eid[j] = a.topk_idx[kk];
   }
-  // stage the k activation vectors: 4 loads in flight per thread per round
-  // (named registers: an indexed array here was placed in scratch memory)
+  Q4Slice q[KPG];
+#pragma unroll
+  for (int j = 0; j < KPG; ++j)
+    q[j] = q4k_load(a.down + (uint64_t)eid[j] * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+  // stage the k activation vectors once per workgroup: 4 loads in flight per
+  // thread per round (named registers: an indexed array was placed in scratch)
+  const int fpad = xpad_size(F);
   for (int base = 4 * threadIdx.x; base < K * F; base += 16 * kBlock) {
     const int n = K * F;
     const int i0 = base, i1 = base + 4 * kBlock, i2 = base + 8 * kBlock, i3 = base + 12 * kBlock;
@@ -261,15 +339,12 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
 #pragma unroll
   for (int j = 0; j < KPG; ++j) {
     const int kk = gi + 4 * j;
-    float acc = 0.0f;
-    if (active && kk < K && row < a.n_embd) {
-      XSlice xv;
-      xslice_load(acts + kk * fpad, sub, xv);
-      acc = q4k_dot(q[j], g, xv);
-    }
+    XSlice xv;
+    xslice_load(acts + min(kk, K - 1) * fpad, active ? sub : 0, xv);
+    const float acc = (active && kk < K) ? q4k_dot(q[j], g, xv) : 0.0f;
     dot[j] = group_sum<16>(acc);
   }
-  if (row >= a.n_embd) return;
+  if (!row_ok) return;
   // gather the k dots into lane 0 in slot order
   float dots[16];
   int32_t ids[16];
@@ -356,8 +431,14 @@ int pow2_at_least(int v) {
 }  // namespace
 
 hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
-  const int grid = (a.n_expert + 3) / 4;
-  hipLaunchKernelGGL(k_router, dim3(grid), dim3(kBlock), 0, s, a);
+  // four rows (waves) per workgroup; the last workgroup also ranks the experts
+  hipLaunchKernelGGL(k_router, dim3((a.n_expert + 3) / 4), dim3(kBlock), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_topk(const float* logits, int n_expert, int k, int32_t* idx, float* w,
+                       hipStream_t s) {
+  hipLaunchKernelGGL(k_topk, dim3(1), dim3(kBlock), 0, s, logits, n_expert, k, idx, w);
   return hipGetLastError();
 }
 
@@ -378,8 +459,8 @@ hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s) {
 hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s) {
   if (a.type_down == KNJ_TYPE_Q4_K && a.n_ff <= 1024) {
     const int kpg = (a.k + 3) / 4;
-    const size_t lds = (size_t)a.k * xpad_size(a.n_ff) * 4;
     const int grid = (a.n_embd + 3) / 4;
+    const size_t lds = (size_t)a.k * xpad_size(a.n_ff) * 4;
 #define GD(J)                                                                       \
   if (kpg == J) {                                                                   \
     hipLaunchKernelGGL(k_expert_down<J>, dim3(grid), dim3(kBlock), lds, s, a);      \

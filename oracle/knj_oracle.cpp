@@ -385,6 +385,13 @@ void moe(Pool& pool, const float* hx, int m, int H, int F, int E, int K, const f
   }
 }
 
+void synth_serial(uint64_t key, int type, uint64_t n_in, uint64_t n_rows, float sd, uint8_t* out) {
+  float tmp[KNJ_QK];
+  const uint64_t nblk = n_rows * (n_in / KNJ_QK);
+  const uint64_t bb = knj_row_bytes(type, KNJ_QK);
+  for (uint64_t b = 0; b < nblk; ++b) knj_synth_quant_block(key, type, n_in, b, sd, tmp, out + b * bb);
+}
+
 void synth_tensor(Pool& pool, uint64_t key, int type, uint64_t n_in, uint64_t n_rows, float sd,
                   uint8_t* out) {
   if (type == KNJ_TYPE_Q4_K || type == KNJ_TYPE_Q6_K) {
@@ -445,14 +452,19 @@ void synth_model(Pool& pool, const knj_model_config* c, uint64_t seed, uint8_t* 
                  (uint64_t)c->n_expert, sd, img + lo.router);
     const uint64_t sgu = knj_row_bytes(c->type_gate_up, H) * F;
     const uint64_t sdn = knj_row_bytes(c->type_down, F) * H;
-    for (int e = 0; e < c->n_expert; ++e) {
-      synth_tensor(pool, knj_tensor_key(seed, il, KNJ_T_GATE, e), c->type_gate_up, H, F, sd,
-                   img + lo.gate + e * sgu);
-      synth_tensor(pool, knj_tensor_key(seed, il, KNJ_T_UP, e), c->type_gate_up, H, F, sd,
-                   img + lo.up + e * sgu);
-      synth_tensor(pool, knj_tensor_key(seed, il, KNJ_T_DOWN, e), c->type_down, F, H, sd,
-                   img + lo.down + e * sdn);
-    }
+    // one task per (expert, tensor): the expert slabs are the bulk of the image
+    pool.for_each(3 * c->n_expert, [&](int task) {
+      const int e = task / 3, which = task % 3;
+      if (which == 0)
+        synth_serial(knj_tensor_key(seed, il, KNJ_T_GATE, e), c->type_gate_up, H, F, sd,
+                     img + lo.gate + e * sgu);
+      else if (which == 1)
+        synth_serial(knj_tensor_key(seed, il, KNJ_T_UP, e), c->type_gate_up, H, F, sd,
+                     img + lo.up + e * sgu);
+      else
+        synth_serial(knj_tensor_key(seed, il, KNJ_T_DOWN, e), c->type_down, F, H, sd,
+                     img + lo.down + e * sdn);
+    });
   }
   fill_ones(img + off_onorm, H);
   synth_tensor(pool, knj_tensor_key(seed, -1, KNJ_T_HEAD, -1), c->type_head, H, V, sd, img + off_head);

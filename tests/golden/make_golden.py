@@ -75,8 +75,10 @@ def full_greedy(steps=64, prompt=(1, 2, 3, 4)):
 if __name__ == "__main__":
     which = sys.argv[1:] or ["config1", "full"]
     if "config1" in which:
+        data = config1()
         with open(os.path.join(HERE, "config1.json"), "w") as f:
-            json.dump(config1(), f)
+            json.dump(data, f)
     if "full" in which:
+        data = full_greedy()
         with open(os.path.join(HERE, "full_greedy.json"), "w") as f:
-            json.dump(full_greedy(), f)
+            json.dump(data, f)
