@@ -22,6 +22,19 @@ using namespace dev;
 
 constexpr int kChunk = 64;
 
+#ifdef KNJ_ATTN_STAMPS
+__device__ unsigned long long g_attn_stamps[16];
+#define STAMP(i)                                                                     \
+  do {                                                                               \
+    if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0)                      \
+      g_attn_stamps[i] = __builtin_amdgcn_s_memrealtime();                           \
+  } while (0)
+#else
+#define STAMP(i) \
+  do {           \
+  } while (0)
+#endif
+
 // q/k normalisation + rotation of one head held as 4 floats per thread in a
 // group of D/4 threads: returns the thread's 4 outputs (elements 4c..4c+3).
 template <int D>
@@ -52,16 +65,27 @@ __device__ __forceinline__ float4 norm_rope4(float4 v, int c, float4 w, float ep
   return out;
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One 16x16x4 f32 matrix-core step: acc[i] += sum_k A[4*(l/16)+i][k] B[k][l%16]
+// where lane l supplies A[l%16][l/16] in `a` and B[l/16][l%16] in `b`.
+__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+}
+
 template <int D>
 __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
-  constexpr int ROWH = D + 8;            // f16 elements per LDS row (16-byte pad)
+  constexpr int ROWH = D + 8;            // f16 elements per K/V LDS row (16-byte pad)
+  constexpr int QROW = D + 4;            // floats per query row
+  constexpr int EROW = kChunk + 4;       // floats per score row
   constexpr int T = D / 4;               // threads per head for the q pass
-  __shared__ float qs[8 * D];            // normalised, rotated queries
+  __shared__ float qs[8 * QROW];         // normalised, rotated queries
   __shared__ uint16_t ks[kChunk * ROWH];
   __shared__ uint16_t vs[kChunk * ROWH];
-  __shared__ float es[8 * kChunk];       // exp(score - max) per head
+  __shared__ float es[8 * EROW];         // scores, then exp(score - max), per head
   const int kvh = blockIdx.x, split = blockIdx.y, n_split = gridDim.y;
   const int G = a.n_head / a.n_head_kv;
+  STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int p0 = split * kChunk;
   uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
@@ -70,7 +94,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   const uint64_t hstride = (uint64_t)n_split * (D + 2);
   // 1) every load that does not depend on the position first: this chunk's
   // cache slots (16 bytes per load; rows past the valid length are dropped
-  // later), the raw query/key/value and the norm weights
+  // later), the raw query/key/value, the norm weights and the RoPE row
   constexpr int PER = (kChunk * D * 2) / (16 * kBlock);  // loads per thread per matrix
   static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
   // (named registers rather than an array: an array live across the query
@@ -94,18 +118,19 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   const float4 kraw = *reinterpret_cast<const float4*>(a.k + (uint64_t)kvh * D + 4 * qc);
   const float4 vraw = *reinterpret_cast<const float4*>(a.v + (uint64_t)kvh * D + 4 * qc);
   const float4 knw = *reinterpret_cast<const float4*>(a.k_norm + 4 * qc);
+  const int ri = (qc < T / 2) ? 4 * qc : 4 * qc - D / 2;  // rotation index of element 4qc
+  const float4 cs = *reinterpret_cast<const float4*>(a.rope_cos + ri);
+  const float4 sn = *reinterpret_cast<const float4*>(a.rope_sin + ri);
   const int pos = *a.pos;
   const int n_kv = pos + 1;
   const int cnt = min(kChunk, n_kv - p0);
+  STAMP(1);
 
   if (cnt > 0) {
     // 2) queries of this kv head: 4 floats per thread, T threads per head
-    const int ri = (qc < T / 2) ? 4 * qc : 4 * qc - D / 2;  // rotation index of element 4qc
-    const float4 cs = *reinterpret_cast<const float4*>(a.rope_cos + (uint64_t)pos * (D / 2) + ri);
-    const float4 sn = *reinterpret_cast<const float4*>(a.rope_sin + (uint64_t)pos * (D / 2) + ri);
     if (tid < G * T) {
       const float4 r = norm_rope4<D>(qraw, qc, qnw, a.eps, cs, sn);
-      *reinterpret_cast<float4*>(qs + qh * D + 4 * qc) = r;
+      *reinterpret_cast<float4*>(qs + qh * QROW + 4 * qc) = r;
     }
     // 3) the slot written this step, if it is in this chunk
     if (pos >= p0 && pos < p0 + cnt && tid < T) {
@@ -122,10 +147,17 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         vs[lp * ROWH + 4 * c + k] = vh[k];
       }
     }
+    STAMP(2);
+    // cache rows past the valid length become zeros: the value product below
+    // runs over all 64 rows with weight 0 there
     auto st = [&](int j, const uint4& kk, const uint4& vv) {
       const int c16 = tid + kBlock * j;
       const int p = (c16 * 8) / D, off = (c16 * 8) % D;
-      if (p < cnt && p0 + p != pos) {
+      if (p >= cnt) {
+        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = z;
+        *reinterpret_cast<uint4*>(vs + p * ROWH + off) = z;
+      } else if (p0 + p != pos) {
         *reinterpret_cast<uint4*>(ks + p * ROWH + off) = kk;
         *reinterpret_cast<uint4*>(vs + p * ROWH + off) = vv;
       }
@@ -137,32 +169,47 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       st(3, k3, v3);
     }
     __syncthreads();
-    // 4) scores: wave w owns heads 2w, 2w+1; lane = position
+    STAMP(3);
+    // 4) scores on the matrix cores: wave w computes S[p][h] for the 16 slots
+    // 16w..16w+15 (rows) and the query heads (columns, zero past G).  Lane
+    // (r = l%16, kq = l/16) contributes dims kq*D/4 .. kq*D/4 + D/4 - 1.
+    const int r = lane & 15, kq = lane >> 4;
+    const bool hv = r < G;
+    {
+      const uint16_t* krow = ks + (16 * wave + r) * ROWH + kq * (D / 4);
+      const float* qrow = qs + min(r, G - 1) * QROW + kq * (D / 4);
+      f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t8 = 0; t8 < D / 4; t8 += 8) {
+        const uint4 kk = *reinterpret_cast<const uint4*>(krow + t8);
+        const float4 qa = *reinterpret_cast<const float4*>(qrow + t8);
+        const float4 qb = *reinterpret_cast<const float4*>(qrow + t8 + 4);
+        sa = mfma4(h2f(kk.x), hv ? qa.x : 0.0f, sa);
+        sb = mfma4(h2f(kk.x >> 16), hv ? qa.y : 0.0f, sb);
+        sa = mfma4(h2f(kk.y), hv ? qa.z : 0.0f, sa);
+        sb = mfma4(h2f(kk.y >> 16), hv ? qa.w : 0.0f, sb);
+        sa = mfma4(h2f(kk.z), hv ? qb.x : 0.0f, sa);
+        sb = mfma4(h2f(kk.z >> 16), hv ? qb.y : 0.0f, sb);
+        sa = mfma4(h2f(kk.w), hv ? qb.z : 0.0f, sa);
+        sb = mfma4(h2f(kk.w >> 16), hv ? qb.w : 0.0f, sb);
+      }
+      if (hv) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) es[r * EROW + 16 * wave + 4 * kq + i] = (sa[i] + sb[i]) * a.scale;
+      }
+    }
+    __syncthreads();
+    // 5) softmax of the chunk: wave w owns heads 2w, 2w+1; lane = slot
     const int h0 = 2 * wave, h1 = 2 * wave + 1;
     if (h0 < G) {
-      float s0 = 0.0f, s1 = 0.0f;
-      if (lane < cnt) {
-        const uint16_t* kr16 = ks + lane * ROWH;
-#pragma unroll 2
-        for (int d8 = 0; d8 < D; d8 += 8) {
-          const uint4 kk = *reinterpret_cast<const uint4*>(kr16 + d8);
-          const float kf[8] = {h2f(kk.x), h2f(kk.x >> 16), h2f(kk.y), h2f(kk.y >> 16),
-                               h2f(kk.z), h2f(kk.z >> 16), h2f(kk.w), h2f(kk.w >> 16)};
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            s0 += qs[h0 * D + d8 + i] * kf[i];
-            if (h1 < G) s1 += qs[h1 * D + d8 + i] * kf[i];
-          }
-        }
-      }
-      s0 = lane < cnt ? s0 * a.scale : -INFINITY;
-      s1 = (lane < cnt && h1 < G) ? s1 * a.scale : -INFINITY;
+      const float s0 = lane < cnt ? es[h0 * EROW + lane] : -INFINITY;
+      const float s1 = (lane < cnt && h1 < G) ? es[h1 * EROW + lane] : -INFINITY;
       const float m0 = group_max<64>(s0), m1 = group_max<64>(s1);
       const float e0 = lane < cnt ? expf(s0 - m0) : 0.0f;
       const float e1 = (lane < cnt && h1 < G) ? expf(s1 - m1) : 0.0f;
       const float l0 = group_sum<64>(e0), l1 = group_sum<64>(e1);
-      es[h0 * kChunk + lane] = e0;
-      if (h1 < G) es[h1 * kChunk + lane] = e1;
+      es[h0 * EROW + lane] = e0;
+      if (h1 < G) es[h1 * EROW + lane] = e1;
       if (lane == 0) {
         *(part + h0 * hstride + 0) = m0;
         *(part + h0 * hstride + 1) = l0;
@@ -171,59 +218,72 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
           *(part + h1 * hstride + 1) = l1;
         }
       }
-      // 5) sum a*v for the wave's two heads; lane owns dims (2*lane, 2*lane+1)
-      if (2 * lane < D) {
-        float a00 = 0.0f, a01 = 0.0f, a10 = 0.0f, a11 = 0.0f;
-#pragma unroll 8
-        for (int p = 0; p < cnt; ++p) {
-          const uint32_t vv = *reinterpret_cast<const uint32_t*>(vs + p * ROWH + 2 * lane);
-          const float v0 = h2f(vv), v1 = h2f(vv >> 16);
-          const float ea = es[h0 * kChunk + p];
-          a00 += ea * v0;
-          a01 += ea * v1;
-          if (h1 < G) {
-            const float eb = es[h1 * kChunk + p];
-            a10 += eb * v0;
-            a11 += eb * v1;
-          }
-        }
-        *(part + h0 * hstride + 2 + 2 * lane) = a00;
-        *(part + h0 * hstride + 3 + 2 * lane) = a01;
-        if (h1 < G) {
-          *(part + h1 * hstride + 2 + 2 * lane) = a10;
-          *(part + h1 * hstride + 3 + 2 * lane) = a11;
+    }
+    __syncthreads();
+    STAMP(4);
+    // 6) sum e*v on the matrix cores: O[h][d] over the 64 slots.  Wave w owns
+    // dims 32w .. 32w+31 as two column tiles, even dims and odd dims, so one
+    // 32-bit LDS read feeds both; lane (r, kq) contributes slots kq*16 .. +15.
+    if (32 * wave < D) {
+      const int d = 32 * wave + 2 * r;
+      const float* erow = es + min(r, G - 1) * EROW + kq * 16;
+      const uint16_t* vcol = vs + (kq * 16) * ROWH + d;
+      f32x4 oe = {0.0f, 0.0f, 0.0f, 0.0f}, oo = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int t4 = 0; t4 < 16; t4 += 4) {
+        const float4 ev = *reinterpret_cast<const float4*>(erow + t4);
+        const float e4[4] = {hv ? ev.x : 0.0f, hv ? ev.y : 0.0f, hv ? ev.z : 0.0f, hv ? ev.w : 0.0f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t vv = *reinterpret_cast<const uint32_t*>(vcol + (t4 + i) * ROWH);
+          oe = mfma4(e4[i], h2f(vv), oe);
+          oo = mfma4(e4[i], h2f(vv >> 16), oo);
         }
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * kq + i;
+        if (h < G) *reinterpret_cast<float2*>(part + h * hstride + 2 + d) = make_float2(oe[i], oo[i]);
+      }
     }
+    STAMP(5);
   } else {
     for (int i = tid; i < G * (D + 2); i += kBlock) {
       const int g = i / (D + 2), j = i % (D + 2);
       *(part + g * hstride + j) = (j == 0) ? -INFINITY : 0.0f;
     }
   }
-
 }
 
 // Merge of the split partials of one query head (one workgroup per head):
-// M = max m_s, f_s = exp(m_s - M), out = sum_s acc_s f_s / sum_s l_s f_s over
-// the splits that hold positions.  Threads [0, D) and [D, 2D) each fold half of
-// the splits (all loads issued before the sums); the halves are added in split
-// order.
+// M = max m_s, f_s = exp(m_s - M), out = sum_s acc_s f_s / sum_s l_s f_s.
+// Every split's record is written on every call (splits past the position
+// hold m = -inf, l = 0, acc = 0), so no load here waits on the position.
+// Threads [0, D), [D, 2D) .. each fold a contiguous range of splits in order
+// (the first CH accumulator loads are issued before the max/sum pass); the
+// ranges are added in split order.
 template <int D>
 __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) {
+  constexpr int NP = kBlock / D;  // 2 for D = 128, 4 for D = 64
+  constexpr int CH = 16;
   __shared__ float fs[1024];
   __shared__ float red[8];
+  __shared__ float parts[kBlock];
   const int h = blockIdx.x, tid = threadIdx.x;
-  const int n_kv = *a.pos + 1;
-  const int live = min(n_split, (n_kv + kChunk - 1) / kChunk);
   const float* ph = a.partial + (uint64_t)h * n_split * (D + 2);
+  const int d = tid % D, pt = tid / D;
+  const int per = (n_split + NP - 1) / NP;
+  const int s0 = pt * per, s1 = min(n_split, s0 + per);
+  float r[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) r[j] = s0 + j < s1 ? ph[(uint64_t)(s0 + j) * (D + 2) + 2 + d] : 0.0f;
   float m_own[4], l_own[4];
   float M = -INFINITY;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int s2 = tid + kBlock * j;
-    m_own[j] = s2 < live ? ph[(uint64_t)s2 * (D + 2)] : -INFINITY;
-    l_own[j] = s2 < live ? ph[(uint64_t)s2 * (D + 2) + 1] : 0.0f;
+    m_own[j] = s2 < n_split ? ph[(uint64_t)s2 * (D + 2)] : -INFINITY;
+    l_own[j] = s2 < n_split ? ph[(uint64_t)s2 * (D + 2) + 1] : 0.0f;
     M = fmaxf(M, m_own[j]);
   }
   M = group_max<64>(M);
@@ -235,22 +295,25 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int s2 = tid + kBlock * j;
-    if (s2 < live) {
+    if (s2 < n_split) {
       const float f = m_own[j] == -INFINITY ? 0.0f : expf(m_own[j] - M);
       fs[s2] = f;
       lsum += l_own[j] * f;
     }
   }
   const float L = block_sum(lsum, red);  // includes the barrier that publishes fs
-  const int d = tid % D, part = tid / D;  // part 0/1 for D = 128; 0..3 for D = 64
-  constexpr int NP = kBlock / D;
-  const int per = (live + NP - 1) / NP;
-  const int s0 = part * per, s1 = min(live, s0 + per);
   float acc = 0.0f;
-#pragma unroll 8
-  for (int s2 = s0; s2 < s1; ++s2) acc += ph[(uint64_t)s2 * (D + 2) + 2 + d] * fs[s2];
-  // fold the parts in order: part 0 + part 1 (+ 2 + 3)
-  __shared__ float parts[kBlock];
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+    if (s0 + j < s1) acc += r[j] * fs[s0 + j];
+  for (int b = s0 + CH; b < s1; b += CH) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) r[j] = b + j < s1 ? ph[(uint64_t)(b + j) * (D + 2) + 2 + d] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+      if (b + j < s1) acc += r[j] * fs[b + j];
+  }
+  // fold the ranges in order: part 0 + part 1 (+ 2 + 3)
   parts[tid] = acc;
   __syncthreads();
   if (tid < D) {

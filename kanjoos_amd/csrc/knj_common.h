@@ -110,8 +110,8 @@ struct AttnArgs {
   const float* q_norm;       // [D]
   const float* k_norm;       // [D]
   float eps;
-  const float* rope_cos;     // [n_ctx][D/2], row `pos` (row 0 when rope_row0)
-  const float* rope_sin;
+  const float* rope_cos;     // [D/2] cos of this token's position
+  const float* rope_sin;     // [D/2] sin
   const int* pos;            // device position of this token (its cache slot)
   uint16_t* k_cache;         // [n_head_kv][n_ctx][D] of this layer
   uint16_t* v_cache;
@@ -139,8 +139,10 @@ hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int 
 // argmax keys it writes).
 int gemv_grid(int type, int n_in, int n_out);
 
-// Embedding row of st->token into x.
+// Embedding row of st->token into x; row st->pos of the RoPE tables into
+// rope_cur (cos then sin, `half` each; skipped when rope_cur is null).
 hipError_t launch_embed(int type, const uint8_t* table, int n_embd, StepState* st, float* x,
+                        const float* rope_cos, const float* rope_sin, int half, float* rope_cur,
                         hipStream_t s);
 
 }  // namespace knj

@@ -322,10 +322,7 @@ int knj_attention_step(const float* q, const float* k, const float* v, const flo
   float* dtab = (float*)scr;
   int* dpos = (int*)(scr + 2 * half * 4);
   KNJ_HIP(hipMemcpyAsync(scr, tab.data(), 2 * half * 4 + 4, hipMemcpyHostToDevice, s));
-  // the kernel reads row `pos` of the table: point the table base `pos` rows back
-  const float* cs = (const float*)((uintptr_t)dtab - (uintptr_t)pos * half * 4);
-  const float* sn = (const float*)((uintptr_t)(dtab + half) - (uintptr_t)pos * half * 4);
-  AttnArgs a{q, k, v, q_norm, k_norm, eps, cs, sn, dpos, k_cache, v_cache, n_head, n_head_kv,
+  AttnArgs a{q, k, v, q_norm, k_norm, eps, dtab, dtab + half, dpos, k_cache, v_cache, n_head, n_head_kv,
              head_dim, n_ctx, 1.0f / std::sqrt((float)head_dim), (float*)(scr + 1024), out};
   KNJ_HIP(launch_attention(a, s));
   KNJ_HIP(hipStreamSynchronize(s));  // the host table must outlive the copy

@@ -36,11 +36,19 @@ __global__ __launch_bounds__(kBlock) void k_rmsnorm(const float* __restrict__ x,
   for (int i = threadIdx.x; i < n; i += blockDim.x) out[i] = x[i] * scale * w[i];
 }
 
-// Embedding row of the step's token (model.cpp:527-537).
+// Embedding row of the step's token (model.cpp:527-537).  Workgroup 0 also
+// copies the RoPE cos/sin row of the step's position into `rope_cur`, so the
+// attention launches of every layer read it without a position-dependent load.
 __global__ void k_embed(int type, const uint8_t* __restrict__ table, int n_embd, StepState* st,
-                        float* __restrict__ x) {
+                        float* __restrict__ x, const float* __restrict__ rope_cos,
+                        const float* __restrict__ rope_sin, int half, float* __restrict__ rope_cur) {
   const int id = st->token;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (blockIdx.x == 0 && rope_cur && threadIdx.x < 2 * half) {
+    const int pos = st->pos, j = threadIdx.x % half;
+    const float* tab = threadIdx.x < half ? rope_cos : rope_sin;
+    rope_cur[threadIdx.x] = tab[(uint64_t)pos * half + j];
+  }
   if (i >= n_embd) return;
   const uint64_t idx = (uint64_t)id * n_embd + i;
   if (type == KNJ_TYPE_BF16)
@@ -64,9 +72,11 @@ hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, floa
 }
 
 hipError_t launch_embed(int type, const uint8_t* table, int n_embd, StepState* st, float* x,
+                        const float* rope_cos, const float* rope_sin, int half, float* rope_cur,
                         hipStream_t s) {
+  if (2 * half > 256) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_embed, dim3((n_embd + 255) / 256), dim3(256), 0, s, type, table, n_embd, st,
-                     x);
+                     x, rope_cos, rope_sin, half, rope_cur);
   return hipGetLastError();
 }
 

@@ -76,7 +76,7 @@ struct knj_model {
   float *x = nullptr, *qkv = nullptr, *ctx = nullptr, *hx = nullptr, *act = nullptr;
   float *logits = nullptr, *router_logits = nullptr, *hidden = nullptr, *topk_w = nullptr;
   int32_t* topk_idx = nullptr;
-  float *rope_cos = nullptr, *rope_sin = nullptr, *attn_part = nullptr;
+  float *rope_cos = nullptr, *rope_sin = nullptr, *rope_cur = nullptr, *attn_part = nullptr;
   uint16_t *kv_k = nullptr, *kv_v = nullptr;
   StepState* st = nullptr;
   int32_t* out_tokens = nullptr;
@@ -147,6 +147,7 @@ int setup(knj_model* m) {
   const int half = c.head_dim / 2;
   if ((rc = alloc(m, (void**)&m->rope_cos, (uint64_t)c.n_ctx * half * 4))) return rc;
   if ((rc = alloc(m, (void**)&m->rope_sin, (uint64_t)c.n_ctx * half * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->rope_cur, (uint64_t)2 * half * 4))) return rc;
   const int n_split = attn_splits(c.n_ctx);
   if ((rc = alloc(m, (void**)&m->attn_part, (uint64_t)c.n_head * n_split * (c.head_dim + 2) * 4))) return rc;
   const uint64_t kv = knj_kv_elems(&c);
@@ -250,7 +251,7 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
   const uint64_t kv_layer = (uint64_t)il * c.n_head_kv * c.n_ctx * D;
   AttnArgs at{m->qkv, m->qkv + QD, m->qkv + QD + KVD,
               reinterpret_cast<const float*>(img + lo.q_norm),
-              reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos, m->rope_sin,
+              reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cur, m->rope_cur + D / 2,
               &m->st->pos, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head, c.n_head_kv, D, c.n_ctx,
               1.0f / std::sqrt((float)D), m->attn_part, m->ctx};
   KNJ_HIP(launch_attention(at, s));
@@ -274,7 +275,8 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
 
 int enqueue_step(knj_model* m, hipStream_t s) {
   const knj_model_config& c = m->c;
-  KNJ_HIP(launch_embed(c.type_embd, m->image + m->off_embd, c.n_embd, m->st, m->x, s));
+  KNJ_HIP(launch_embed(c.type_embd, m->image + m->off_embd, c.n_embd, m->st, m->x, m->rope_cos,
+                       m->rope_sin, c.head_dim / 2, m->rope_cur, s));
   for (int il = 0; il < c.n_layer; ++il) {
     int rc = enqueue_layer(m, il, s);
     if (rc) return rc;

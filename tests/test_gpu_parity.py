@@ -249,3 +249,73 @@ def test_full_model_greedy_golden(device):
     got = [first] + list(gm.decode_greedy(first, len(want["tokens"]) - 1))
     gm.close()
     assert got == want["tokens"]
+
+
+def _attn_ref(q, k, v, qn, kn, eps, base, pos, n_head, n_kv, D, kc, vc):
+    """float64 restatement of the attention block (model.cpp:560-617): per-head
+    RMSNorm, NEOX RoPE, softmax(q.k/sqrt(D)) over slots 0..pos, sum a*v.  The
+    rotation angle is formed in float32 as the reference's table is
+    (model.cpp:227-230): at base 1e6 a float64 angle differs from it by up to
+    pos * 6e-8 rad, far above the tolerance."""
+    half = D // 2
+    f = np.float32
+    # powf of exact exponents: the float64 power rounded once to float32 (numpy's
+    # own float32 power may differ from it by a few ulp)
+    inv = (float(f(base)) ** (-2.0 * np.arange(half) / D)).astype(f)
+    th = (f(pos) * inv).astype(np.float64)
+    c, s = np.cos(th), np.sin(th)
+
+    def norm_rope(x, w):
+        x = x.astype(np.float64)
+        x = x / np.sqrt((x * x).mean(-1, keepdims=True) + eps) * w
+        x0, x1 = x[..., :half], x[..., half:]
+        return np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], -1)
+
+    qr = norm_rope(q.reshape(n_head, D), qn)
+    kr = norm_rope(k.reshape(n_kv, D), kn)
+    G = n_head // n_kv
+    out = np.zeros((n_head, D))
+    for h in range(n_head):
+        g = h // G
+        K_ = kc[g, :pos + 1].astype(np.float64)
+        V_ = vc[g, :pos + 1].astype(np.float64)
+        sc = K_ @ qr[h] / np.sqrt(D)
+        a = np.exp(sc - sc.max())
+        out[h] = (a / a.sum()) @ V_
+    return out, kr
+
+
+@pytest.mark.parametrize("n_head,n_kv,D", [(32, 4, 128), (16, 2, 64), (12, 4, 128), (8, 8, 64)])
+@pytest.mark.parametrize("pos", [0, 63, 64, 130, 199])
+def test_attention_step(device, n_head, n_kv, D, pos):
+    """knj_attention_step against a float64 reference: cache append and output."""
+    say(f"attention n_head={n_head} n_kv={n_kv} D={D} pos={pos}")
+    n_ctx, eps, base = 200, 1e-6, 1e6
+    rng = np.random.default_rng(1000 * pos + D + n_head)
+    q = rng.standard_normal(n_head * D).astype(np.float32)
+    k = rng.standard_normal(n_kv * D).astype(np.float32)
+    v = rng.standard_normal(n_kv * D).astype(np.float32)
+    qn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kn = (1 + 0.1 * rng.standard_normal(D)).astype(np.float32)
+    kc = (rng.standard_normal((n_kv, n_ctx, D)) * 0.7).astype(np.float16)
+    vc = rng.standard_normal((n_kv, n_ctx, D)).astype(np.float16)
+    bufs = [K.DeviceBuffer.from_array(a) for a in (q, k, v, qn, kn)]
+    dkc, dvc = K.DeviceBuffer.from_array(kc.view(np.uint16)), K.DeviceBuffer.from_array(vc.view(np.uint16))
+    dout = K.DeviceBuffer(4 * n_head * D)
+    K.attention_step(*bufs, eps, base, pos, n_head, n_kv, D, n_ctx, dkc, dvc, dout)
+    got_kc = dkc.download(np.uint16).view(np.float16).reshape(n_kv, n_ctx, D)
+    got_vc = dvc.download(np.uint16).view(np.float16).reshape(n_kv, n_ctx, D)
+    out = dout.download(np.float32).reshape(n_head, D)
+    # appended slot: v rounded to f16; k normalised + rotated, within one f16 ulp
+    want_kc, want_vc = kc.copy(), vc.copy()
+    want_vc[:, pos] = v.reshape(n_kv, D).astype(np.float16)
+    _, kr = _attn_ref(q, k, v, qn, kn, eps, base, pos, n_head, n_kv, D, want_kc, want_vc)
+    assert np.array_equal(got_vc.view(np.uint16), want_vc.view(np.uint16))
+    kdiff = np.abs(got_kc[:, pos].astype(np.float64) - kr)
+    assert np.all(kdiff <= np.spacing(np.abs(kr).astype(np.float16)).astype(np.float64) * 0.5 + 1e-6)
+    others = np.ones(n_ctx, bool)
+    others[pos] = False
+    assert np.array_equal(got_kc[:, others].view(np.uint16), kc[:, others].view(np.uint16))
+    # output against the reference over the cache as the device wrote it
+    ref_out, _ = _attn_ref(q, k, v, qn, kn, eps, base, pos, n_head, n_kv, D, got_kc, got_vc)
+    assert rel_rmse(out, ref_out) <= 1e-5
