@@ -22,18 +22,6 @@ using namespace dev;
 
 constexpr int kChunk = 64;
 
-#ifdef KNJ_ATTN_STAMPS
-__device__ unsigned long long g_attn_stamps[16];
-#define STAMP(i)                                                                     \
-  do {                                                                               \
-    if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0)                      \
-      g_attn_stamps[i] = __builtin_amdgcn_s_memrealtime();                           \
-  } while (0)
-#else
-#define STAMP(i) \
-  do {           \
-  } while (0)
-#endif
 
 // q/k normalisation + rotation of one head held as 4 floats per thread in a
 // group of D/4 threads: returns the thread's 4 outputs (elements 4c..4c+3).
@@ -50,11 +38,16 @@ __device__ __forceinline__ float4 norm_rope4(float4 v, int c, float4 w, float ep
   n.z = v.z * scale * w.z;
   n.w = v.w * scale * w.w;
   // partner: elements 4c +- D/2 live in thread c +- T/2
+  static_assert(T == 16 || T == 32, "head_dim 64 or 128");
+  auto partner = [](float x) {
+    if constexpr (T == 32) return xor16_f(x);
+    else return dev::dpp_f<dev::kDppRor8>(x);
+  };
   float4 p;
-  p.x = __shfl_xor(n.x, T / 2, 64);
-  p.y = __shfl_xor(n.y, T / 2, 64);
-  p.z = __shfl_xor(n.z, T / 2, 64);
-  p.w = __shfl_xor(n.w, T / 2, 64);
+  p.x = partner(n.x);
+  p.y = partner(n.y);
+  p.z = partner(n.z);
+  p.w = partner(n.w);
   const bool lo = c < T / 2;
   // (x0, x1) -> (x0*c - x1*s, x0*s + x1*c) with x0 the low-half element
   float4 out;
@@ -85,7 +78,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   __shared__ float es[8 * EROW];         // scores, then exp(score - max), per head
   const int kvh = blockIdx.x, split = blockIdx.y, n_split = gridDim.y;
   const int G = a.n_head / a.n_head_kv;
-  STAMP(0);
+  KNJ_STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int p0 = split * kChunk;
   uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
@@ -124,7 +117,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   const int pos = *a.pos;
   const int n_kv = pos + 1;
   const int cnt = min(kChunk, n_kv - p0);
-  STAMP(1);
+  KNJ_STAMP(1);
 
   if (cnt > 0) {
     // 2) queries of this kv head: 4 floats per thread, T threads per head
@@ -147,7 +140,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         vs[lp * ROWH + 4 * c + k] = vh[k];
       }
     }
-    STAMP(2);
+    KNJ_STAMP(2);
     // cache rows past the valid length become zeros: the value product below
     // runs over all 64 rows with weight 0 there
     auto st = [&](int j, const uint4& kk, const uint4& vv) {
@@ -169,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       st(3, k3, v3);
     }
     __syncthreads();
-    STAMP(3);
+    KNJ_STAMP(3);
     // 4) scores on the matrix cores: wave w computes S[p][h] for the 16 slots
     // 16w..16w+15 (rows) and the query heads (columns, zero past G).  Lane
     // (r = l%16, kq = l/16) contributes dims kq*D/4 .. kq*D/4 + D/4 - 1.
@@ -220,7 +213,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       }
     }
     __syncthreads();
-    STAMP(4);
+    KNJ_STAMP(4);
     // 6) sum e*v on the matrix cores: O[h][d] over the 64 slots.  Wave w owns
     // dims 32w .. 32w+31 as two column tiles, even dims and odd dims, so one
     // 32-bit LDS read feeds both; lane (r, kq) contributes slots kq*16 .. +15.
@@ -246,7 +239,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
         if (h < G) *reinterpret_cast<float2*>(part + h * hstride + 2 + d) = make_float2(oe[i], oo[i]);
       }
     }
-    STAMP(5);
+    KNJ_STAMP(5);
   } else {
     for (int i = tid; i < G * (D + 2); i += kBlock) {
       const int g = i / (D + 2), j = i % (D + 2);

@@ -85,8 +85,10 @@ struct ExpertArgs {
   const float* hx;        // [n_embd] input of gate/up: RMSNorm(hx, norm_w) when norm_w is
   const float* norm_w;    // set (the residual stream and ffn_norm), else used as is
   float eps;
-  const int32_t* topk_idx;  // routing (launch_topk's output)
-  const float* topk_w;
+  const float* logits;    // router logits [n_expert]: when set, gate/up routes itself
+                          // (softmax + top-k in every wave) and writes topk_idx/topk_w
+  int32_t* topk_idx;      // routing [k], selection order (input when logits is null)
+  float* topk_w;
   const uint8_t* gate;    // [n_expert] slabs
   const uint8_t* up;
   const uint8_t* down;

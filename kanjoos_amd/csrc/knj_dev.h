@@ -13,6 +13,21 @@
 
 #include "../../include/knj_format.h"
 
+// Phase timestamps of workgroup 0 (thread 0) for timing builds that define
+// KNJ_STAMPS; compiled out otherwise.
+#ifdef KNJ_STAMPS
+__device__ unsigned long long g_knj_stamps[64];
+#define KNJ_STAMP(i)                                                                 \
+  do {                                                                               \
+    if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0)                      \
+      g_knj_stamps[i] = __builtin_amdgcn_s_memrealtime();                            \
+  } while (0)
+#else
+#define KNJ_STAMP(i) \
+  do {               \
+  } while (0)
+#endif
+
 namespace knj {
 namespace dev {
 
@@ -27,30 +42,107 @@ __device__ __forceinline__ uint16_t f2h(float v) {
   return __builtin_bit_cast(unsigned short, (_Float16)v);
 }
 
+// ---- cross-lane moves without the LDS crossbar.  Rows of 16 lanes exchange
+// through DPP (quad permutes, the 8- and 16-lane mirrors, row rotation); rows
+// and half-waves through the gfx950 permlane swaps.  Every lane of the group
+// taking part must be active.
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within 8
+constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within 16
+constexpr int kDppRor8 = 0x128;       // lane i <- (i + 8) % 16 within 16, i.e. i ^ 8
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)v, (int)v, CTRL, 0xF, 0xF, false);
+}
+
+// the value of lane l ^ 16
+__device__ __forceinline__ uint32_t xor16_u32(uint32_t v) {
+  // odd rows of the first result hold the even rows of v, even rows of the
+  // second result the odd rows
+  const auto p = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (__lane_id() & 16) ? p[0] : p[1];
+}
+
+// the value of lane l ^ 32
+__device__ __forceinline__ uint32_t xor32_u32(uint32_t v) {
+  const auto p = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (__lane_id() & 32) ? p[0] : p[1];
+}
+
+__device__ __forceinline__ float xor16_f(float v) { return __uint_as_float(xor16_u32(__float_as_uint(v))); }
+__device__ __forceinline__ float xor32_f(float v) { return __uint_as_float(xor32_u32(__float_as_uint(v))); }
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) { return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v))); }
+
+// Reduction over aligned groups of W lanes (W a power of two <= 64) as a
+// butterfly: partners are combined in both orders only by commutative ops, so
+// every lane of a group returns the same bits.
+template <int W, class Op>
+__device__ __forceinline__ float group_reduce(float v, Op op) {
+  static_assert(W >= 1 && W <= 64 && (W & (W - 1)) == 0, "group of 1..64 lanes");
+  if constexpr (W >= 2) v = op(v, dpp_f<kDppXor1>(v));
+  if constexpr (W >= 4) v = op(v, dpp_f<kDppXor2>(v));
+  if constexpr (W >= 8) v = op(v, dpp_f<kDppHalfMirror>(v));
+  if constexpr (W >= 16) v = op(v, dpp_f<kDppMirror>(v));
+  if constexpr (W >= 32) v = op(v, xor16_f(v));
+  if constexpr (W >= 64) v = op(v, xor32_f(v));
+  return v;
+}
+
 template <int W>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  return group_reduce<W>(v, [](float a, float b) { return a + b; });
 }
 
 template <int W>
 __device__ __forceinline__ float group_max(float v) {
-#pragma unroll
-  for (int o = W / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return group_reduce<W>(v, [](float a, float b) { return fmaxf(a, b); });
+}
+
+// Maximum of an unsigned 32-bit value over the wave; every lane returns it.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
+  v = max(v, dpp_u32<kDppXor1>(v));
+  v = max(v, dpp_u32<kDppXor2>(v));
+  v = max(v, dpp_u32<kDppHalfMirror>(v));
+  v = max(v, dpp_u32<kDppMirror>(v));
+  v = max(v, xor16_u32(v));
+  v = max(v, xor32_u32(v));
   return v;
 }
 
-// Sum over the workgroup: wave trees, then the waves in order.  Every thread
-// returns the same value.
+// Maximum of a 64-bit key over the wave; every lane returns it.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  auto step = [&](uint32_t lo, uint32_t hi) {
+    const unsigned long long t = ((unsigned long long)hi << 32) | lo;
+    v = t > v ? t : v;
+  };
+  step(dpp_u32<kDppXor1>((uint32_t)v), dpp_u32<kDppXor1>((uint32_t)(v >> 32)));
+  step(dpp_u32<kDppXor2>((uint32_t)v), dpp_u32<kDppXor2>((uint32_t)(v >> 32)));
+  step(dpp_u32<kDppHalfMirror>((uint32_t)v), dpp_u32<kDppHalfMirror>((uint32_t)(v >> 32)));
+  step(dpp_u32<kDppMirror>((uint32_t)v), dpp_u32<kDppMirror>((uint32_t)(v >> 32)));
+  step(xor16_u32((uint32_t)v), xor16_u32((uint32_t)(v >> 32)));
+  step(xor32_u32((uint32_t)v), xor32_u32((uint32_t)(v >> 32)));
+  return v;
+}
+
+// The value of lane `src` (the same for the whole wave) in every lane.
+__device__ __forceinline__ float lane_bcast(float v, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), src));
+}
+__device__ __forceinline__ int lane_bcast(int v, int src) { return __builtin_amdgcn_readlane(v, src); }
+
+// Sum over a workgroup of kBlock threads: wave trees, then the waves in order.
+// Every thread returns the same value.
 __device__ __forceinline__ float block_sum(float v, float* red) {
   v = group_sum<64>(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) red[wave] = v;
   __syncthreads();
   float t = 0.0f;
-  const int nw = (blockDim.x + 63) >> 6;
-  for (int i = 0; i < nw; ++i) t += red[i];
+#pragma unroll
+  for (int i = 0; i < kBlock / 64; ++i) t += red[i];
   __syncthreads();
   return t;
 }
@@ -99,22 +191,35 @@ __device__ __forceinline__ int xpad(int i) { return i + ((i >> 6) << 2); }
 constexpr int xpad_size(int n) { return n + (n >> 6) * 4; }
 
 // Stage x (n <= 4096 floats) into padded LDS, optionally RMS-normalised:
-// xs = x * (1/sqrt(sum(x^2)/n + eps)) * w.  All threads take part.
-__device__ __forceinline__ void stage_x(const float* __restrict__ x,
-                                        const float* __restrict__ nw, float eps, int n, float* xs,
-                                        float* red) {
-  float4 v[4];
-  float ss = 0.0f;
+// xs = x * (1/sqrt(sum(x^2)/n + eps)) * w.  All threads take part.  Split in
+// two so a kernel can issue the loads (x and the norm weight together) early
+// and do the reduction and LDS stores later.
+struct XRegs {
+  float4 v[4], w[4];
+};
+
+__device__ __forceinline__ void stage_x_load(const float* __restrict__ x,
+                                             const float* __restrict__ nw, int n, XRegs& r) {
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int i = 4 * threadIdx.x + 1024 * j;
     if (i < n) {
-      v[j] = *reinterpret_cast<const float4*>(x + i);
-      ss += v[j].x * v[j].x + v[j].y * v[j].y + v[j].z * v[j].z + v[j].w * v[j].w;
+      r.v[j] = *reinterpret_cast<const float4*>(x + i);
+      if (nw) r.w[j] = *reinterpret_cast<const float4*>(nw + i);
     }
   }
+}
+
+__device__ __forceinline__ void stage_x_store(const XRegs& r, bool norm, float eps, int n,
+                                              float* xs, float* red) {
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * threadIdx.x + 1024 * j;
+    if (i < n) ss += r.v[j].x * r.v[j].x + r.v[j].y * r.v[j].y + r.v[j].z * r.v[j].z + r.v[j].w * r.v[j].w;
+  }
   float scale = 1.0f;
-  if (nw) {
+  if (norm) {
     ss = block_sum(ss, red);
     scale = 1.0f / sqrtf(ss / (float)n + eps);
   }
@@ -122,18 +227,25 @@ __device__ __forceinline__ void stage_x(const float* __restrict__ x,
   for (int j = 0; j < 4; ++j) {
     const int i = 4 * threadIdx.x + 1024 * j;
     if (i < n) {
-      float4 o = v[j];
-      if (nw) {
-        const float4 w = *reinterpret_cast<const float4*>(nw + i);
-        o.x = v[j].x * scale * w.x;
-        o.y = v[j].y * scale * w.y;
-        o.z = v[j].z * scale * w.z;
-        o.w = v[j].w * scale * w.w;
+      float4 o = r.v[j];
+      if (norm) {
+        o.x = r.v[j].x * scale * r.w[j].x;
+        o.y = r.v[j].y * scale * r.w[j].y;
+        o.z = r.v[j].z * scale * r.w[j].z;
+        o.w = r.v[j].w * scale * r.w[j].w;
       }
       *reinterpret_cast<float4*>(xs + xpad(i)) = o;
     }
   }
   __syncthreads();
+}
+
+__device__ __forceinline__ void stage_x(const float* __restrict__ x,
+                                        const float* __restrict__ nw, float eps, int n, float* xs,
+                                        float* red) {
+  XRegs r;
+  stage_x_load(x, nw, n, r);
+  stage_x_store(r, nw != nullptr, eps, n, xs, red);
 }
 
 // ---------------------------------------------------------------- Q4_K slices
@@ -299,11 +411,7 @@ __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
 __device__ __forceinline__ void block_argmax_store(unsigned long long best,
                                                    unsigned long long* keys) {
   __shared__ unsigned long long wbest[4];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long t = __shfl_xor(best, o, 64);
-    best = t > best ? t : best;
-  }
+  best = wave_max_u64(best);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) wbest[wave] = best;
   __syncthreads();

@@ -282,10 +282,11 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
   float* hx = (float*)device_scratch(bytes, s);
   if (!hx) return hip_fail(hipErrorOutOfMemory, "scratch");
   float* act = hx + n_embd;
-  RouterArgs ra{x, norm_w, eps, router_w, n_embd, n_expert, k, hx, logits, topk_idx, topk_w,
+  // logits only: the gate/up launch routes from them and writes topk_idx/topk_w
+  RouterArgs ra{x, norm_w, eps, router_w, n_embd, n_expert, k, hx, logits, nullptr, nullptr,
                 device_counters()};
   KNJ_HIP(launch_router(ra, s));
-  ExpertArgs ea{x, norm_w, eps, topk_idx, topk_w, (const uint8_t*)gate,
+  ExpertArgs ea{x, norm_w, eps, logits, topk_idx, topk_w, (const uint8_t*)gate,
                 (const uint8_t*)up, (const uint8_t*)down, type_gate_up, type_down, n_embd, n_ff,
                 n_expert, k, act, resid, out, nullptr};
   KNJ_HIP(launch_experts(ea, s));

@@ -336,11 +336,7 @@ __global__ __launch_bounds__(kBlock) void k_step_close(StepState* st, const unsi
     best = k > best ? k : best;
   }
   __shared__ unsigned long long wb[4];
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const unsigned long long t = __shfl_xor(best, o, 64);
-    best = t > best ? t : best;
-  }
+  best = wave_max_u64(best);
   if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
   __syncthreads();
   if (threadIdx.x != 0) return;

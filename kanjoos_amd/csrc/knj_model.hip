@@ -259,13 +259,13 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
   KNJ_HIP(launch_gemv(o, s));
   RouterArgs ra{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
                 reinterpret_cast<const float*>(img + lo.router), H, c.n_expert, c.n_expert_used,
-                m->hx, m->router_logits + (uint64_t)il * c.n_expert,
-                m->topk_idx + (uint64_t)il * c.n_expert_used, m->topk_w + (uint64_t)il * c.n_expert_used,
-                m->counter};
+                m->hx, m->router_logits + (uint64_t)il * c.n_expert, nullptr, nullptr, m->counter};
   KNJ_HIP(launch_router(ra, s));
+  // the gate/up launch routes from the logits (softmax + top-k per wave)
   int32_t* ti = m->topk_idx + (uint64_t)il * c.n_expert_used;
   float* tw = m->topk_w + (uint64_t)il * c.n_expert_used;
-  ExpertArgs ea{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps, ti, tw,
+  ExpertArgs ea{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
+                m->router_logits + (uint64_t)il * c.n_expert, ti, tw,
                 img + lo.gate, img + lo.up, img + lo.down,
                 c.type_gate_up, c.type_down, H, c.n_ff, c.n_expert, c.n_expert_used, m->act, m->x,
                 m->x, m->hidden + (uint64_t)il * H};
@@ -530,7 +530,9 @@ int knj_model_time_experts(knj_model* m, int iters, float* us_gateup, float* us_
     for (int i = 0; i < iters; ++i) {
       const int il = i % c.n_layer;  // rotate so repeats come from HBM
       const knj_layer_offsets& lo = m->lo[il];
-      ExpertArgs ea{m->hx, nullptr, 0.0f, m->topk_idx + (uint64_t)il * c.n_expert_used,
+      // as in the decode step: gate/up routes from the layer's logits
+      ExpertArgs ea{m->hx, nullptr, 0.0f, m->router_logits + (uint64_t)il * c.n_expert,
+                    m->topk_idx + (uint64_t)il * c.n_expert_used,
                     m->topk_w + (uint64_t)il * c.n_expert_used, m->image + lo.gate, m->image + lo.up,
                     m->image + lo.down, c.type_gate_up, c.type_down, c.n_embd, c.n_ff, c.n_expert,
                     c.n_expert_used, m->act, nullptr, m->ctx, nullptr};

@@ -81,6 +81,56 @@ __device__ __forceinline__ void router_topk(const float* __restrict__ logits, in
   __syncthreads();
 }
 
+// The same routing by one wave, with no LDS and no barrier: each lane holds
+// experts lane, lane+64, ..  Probabilities are non-negative, so their bit
+// patterns order like the values; a key is those bits + 1 (0 marks an expert
+// already taken).  Each of the k rounds takes the wave maximum of the keys and,
+// among the experts holding it, the lowest index (the strict-'>' argmax with
+// ties to the lower index, model.cpp:442-451).  Lane q < k returns selection
+// q: its expert and its weight p / sum of the kept p, the sum taken in
+// selection order (model.cpp:452-458).  n_expert <= 256.
+__device__ __forceinline__ void wave_route(const float* __restrict__ logits, int n_expert, int k,
+                                           int& my_idx, float& my_w) {
+  const int lane = threadIdx.x & 63;
+  float lg[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lg[j] = lane + 64 * j < n_expert ? logits[lane + 64 * j] : -INFINITY;
+  float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
+  mx = group_max<64>(mx);
+  float ex[4], s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ex[j] = lane + 64 * j < n_expert ? expf(lg[j] - mx) : 0.0f;
+    s += ex[j];
+  }
+  const float sum = group_sum<64>(s);
+  uint32_t key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    key[j] = lane + 64 * j < n_expert ? __float_as_uint(ex[j] / sum) + 1u : 0u;
+  my_idx = 0;
+  float my_p = 0.0f, keep = 0.0f;
+  for (int q = 0; q < k; ++q) {
+    uint32_t b = max(max(key[0], key[1]), max(key[2], key[3]));
+    b = wave_max_u32(b);
+    const unsigned long long m0 = __ballot(key[0] == b), m1 = __ballot(key[1] == b);
+    const unsigned long long m2 = __ballot(key[2] == b), m3 = __ballot(key[3] == b);
+    const int e = m0 ? __builtin_ctzll(m0)
+                     : m1 ? 64 + __builtin_ctzll(m1)
+                          : m2 ? 128 + __builtin_ctzll(m2) : 192 + __builtin_ctzll(m3);
+    const float p = __uint_as_float(b - 1u);
+    keep += p;
+    if (lane == q) {
+      my_idx = e;
+      my_p = p;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) key[j] = (lane == (e & 63) && j == (e >> 6)) ? 0u : key[j];
+  }
+  const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
+  my_w = my_p * inv;
+}
+
 // ------------------------------------------------------------------ router
 // One wave per expert row (4 per workgroup).  Each wave normalises x itself
 // (no workgroup barrier before the dot); workgroup 0 writes hx.  The logits
@@ -98,25 +148,27 @@ __global__ __launch_bounds__(kBlock) void k_router(RouterArgs a) {
     for (int j = 0; j < 16; ++j)
       if (j < nj) wv[j] = *reinterpret_cast<const float4*>(wr + 4 * lane + 256 * j);
   }
-  float4 xv[16];
-  float ss = 0.0f;
+  float4 xv[16], nw[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j)
     if (j < nj) {
       xv[j] = *reinterpret_cast<const float4*>(a.x + 4 * lane + 256 * j);
-      ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+      if (a.norm_w) nw[j] = *reinterpret_cast<const float4*>(a.norm_w + 4 * lane + 256 * j);
     }
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j)
+    if (j < nj) ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
   if (a.norm_w) {
     ss = group_sum<64>(ss);
     const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
 #pragma unroll
     for (int j = 0; j < 16; ++j)
       if (j < nj) {
-        const float4 nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * lane + 256 * j);
-        xv[j].x = xv[j].x * scale * nw.x;
-        xv[j].y = xv[j].y * scale * nw.y;
-        xv[j].z = xv[j].z * scale * nw.z;
-        xv[j].w = xv[j].w * scale * nw.w;
+        xv[j].x = xv[j].x * scale * nw[j].x;
+        xv[j].y = xv[j].y * scale * nw[j].y;
+        xv[j].z = xv[j].z * scale * nw[j].z;
+        xv[j].w = xv[j].w * scale * nw[j].w;
       }
   }
   if (blockIdx.x == 0 && wave == 0) {
@@ -174,10 +226,24 @@ template <int RS>
 __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   __shared__ float xs[xpad_size(2048)];
   __shared__ float red[8];
-  __shared__ int sel_idx[16];
-  if (threadIdx.x < a.k) sel_idx[threadIdx.x] = a.topk_idx[threadIdx.x];
-  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  KNJ_STAMP(0);
+  // x and its norm weight are requested with the routing inputs, so only the
+  // weight loads remain outstanding once the experts are known
+  XRegs xr;
+  stage_x_load(a.hx, a.norm_w, a.n_embd, xr);
+  int my_idx;
+  if (a.logits) {
+    float my_w;
+    wave_route(a.logits, a.n_expert, a.k, my_idx, my_w);
+    KNJ_STAMP(1);
+    if (blockIdx.x == 0 && wave == 0 && lane < a.k) {
+      a.topk_idx[lane] = my_idx;
+      a.topk_w[lane] = my_w;
+    }
+  } else {
+    my_idx = lane < a.k ? a.topk_idx[lane] : 0;
+  }
   const int half = lane >> 5, sub = lane & 31;
   const int nslices = a.n_embd >> 6;
   const bool active = sub < nslices;
@@ -193,12 +259,13 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   auto load_pair = [&](int pr, Q4Slice& q) {
     const int prc = min(pr, npairs - 1);  // always a valid row; unused results are dropped
     const int kk = prc / a.n_ff, row = prc - kk * a.n_ff;
-    const int e = sel_idx[kk];
+    const int e = lane_bcast(my_idx, kk);
     q = q4k_load(base + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)(active ? b : 0) * KNJ_Q4K_BLOCK, g);
   };
   load_pair(pair0, q0);
   load_pair(pair0 + 1, q1);
-  stage_x(a.hx, a.norm_w, a.eps, a.n_embd, xs, red);
+  stage_x_store(xr, a.norm_w != nullptr, a.eps, a.n_embd, xs, red);
+  KNJ_STAMP(2);
   XSlice xv;
   xslice_load(xs, active ? sub : 0, xv);
 #pragma unroll
@@ -206,21 +273,31 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
     const int pr = pair0 + st;
     float acc = (active && pr < npairs) ? q4k_dot(st == 0 ? q0 : q1, g, xv) : 0.0f;
     acc = group_sum<32>(acc);
-    const float u = __shfl(acc, 32, 64);
+    const float u = lane_bcast(acc, 32);
     if (lane == 0 && pr < npairs) {
       const float silu = acc / (1.0f + expf(-acc));
       a.act[pr] = silu * u;  // act is [k][n_ff], pr = kk*n_ff + row
     }
+    if (st == 0) KNJ_STAMP(3);
   }
+  KNJ_STAMP(4);
 }
 
 // Reference-shaped fallback for n_embd > 2048: 32 lanes per row, loop.
 __global__ __launch_bounds__(kBlock) void k_expert_gateup_wide(ExpertArgs a) {
   extern __shared__ float xw[];
   __shared__ float red[8];
-  __shared__ int sel_idx[16];
-  if (threadIdx.x < a.k) sel_idx[threadIdx.x] = a.topk_idx[threadIdx.x];
-  __syncthreads();
+  int my_idx;
+  if (a.logits) {
+    float my_w;
+    wave_route(a.logits, a.n_expert, a.k, my_idx, my_w);
+    if (blockIdx.x == 0 && threadIdx.x < a.k) {
+      a.topk_idx[threadIdx.x] = my_idx;
+      a.topk_w[threadIdx.x] = my_w;
+    }
+  } else {
+    my_idx = (threadIdx.x & 63) < a.k ? a.topk_idx[threadIdx.x & 63] : 0;
+  }
   const int H = a.n_embd;
   float ss = 0.0f;
   for (int i = 4 * threadIdx.x; i < H; i += 4 * kBlock) {
@@ -250,7 +327,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup_wide(ExpertArgs a) {
   const int npairs = a.k * a.n_ff;
   for (int pr = blockIdx.x * (kBlock / 64) + wave; pr < npairs; pr += gridDim.x * (kBlock / 64)) {
     const int kk = pr / a.n_ff, row = pr - kk * a.n_ff;
-    const int e = sel_idx[kk];
+    const int e = lane_bcast(my_idx, kk);
     const uint8_t* rp = (half ? a.up : a.gate) + (uint64_t)e * slab + (uint64_t)row * rb;
     float acc = 0.0f;
     for (int s = sub; s < nslices; s += 32) {
@@ -259,7 +336,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup_wide(ExpertArgs a) {
       acc += q4k_dot(q4k_load(rp + (uint64_t)(s >> 2) * KNJ_Q4K_BLOCK, s & 3), s & 3, xv);
     }
     acc = group_sum<32>(acc);
-    const float u = __shfl(acc, 32, 64);
+    const float u = lane_bcast(acc, 32);
     if (lane == 0) a.act[pr] = (acc / (1.0f + expf(-acc))) * u;
   }
 }
@@ -293,6 +370,7 @@ __device__ __forceinline__ float combine_sorted(const float* dots, const int32_t
 template <int KPG>
 __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   extern __shared__ float acts[];  // [k][xpad_size(n_ff)]
+  constexpr int KMAX = 4 * KPG;    // k <= KMAX
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int gi = lane >> 4, sub = lane & 15;
   const int F = a.n_ff, K = a.k;
@@ -300,19 +378,29 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   const bool active = sub < nslices;
   const uint64_t rb = (uint64_t)(F >> 8) * KNJ_Q4K_BLOCK;
   const uint64_t slab = rb * (uint64_t)a.n_embd;
+  KNJ_STAMP(8);
   const int row = min((int)(blockIdx.x * (kBlock / 64) + wave), a.n_embd - 1);
   const bool row_ok = (int)(blockIdx.x * (kBlock / 64) + wave) < a.n_embd;
   const int b = active ? (sub >> 2) : 0, g = sub & 3;
-  int eid[KPG];
+  // the routing (the same for every row) and this row's residual, requested
+  // with the weights so that nothing after the dot products waits on memory
+  int ids[KMAX];
+  float wts[KMAX];
 #pragma unroll
-  for (int j = 0; j < KPG; ++j) {
-    const int kk = min(gi + 4 * j, K - 1);
-    eid[j] = a.topk_idx[kk];
+  for (int kk = 0; kk < KMAX; ++kk) {
+    ids[kk] = kk < K ? a.topk_idx[kk] : 0x7FFFFFFF;
+    wts[kk] = kk < K ? a.topk_w[kk] : 0.0f;
   }
   Q4Slice q[KPG];
 #pragma unroll
-  for (int j = 0; j < KPG; ++j)
-    q[j] = q4k_load(a.down + (uint64_t)eid[j] * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+  for (int j = 0; j < KPG; ++j) {
+    const int kk = min(gi + 4 * j, K - 1);
+    int e = ids[0];
+#pragma unroll
+    for (int t = 1; t < KMAX; ++t) e = kk == t ? ids[t] : e;
+    q[j] = q4k_load(a.down + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
+  }
+  const float resid = a.resid ? a.resid[row] : 0.0f;
   // stage the k activation vectors once per workgroup: 4 loads in flight per
   // thread per round (named registers: an indexed array was placed in scratch)
   const int fpad = xpad_size(F);
@@ -334,7 +422,18 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
     put(i2, v2);
     put(i3, v3);
   }
+  // slot order by ascending expert index (ids are distinct): rank[kk] =
+  // #{t : ids[t] < ids[kk]}; computed while the loads are in flight
+  int rank[KMAX];
+#pragma unroll
+  for (int kk = 0; kk < KMAX; ++kk) {
+    int r = 0;
+#pragma unroll
+    for (int t = 0; t < KMAX; ++t) r += ids[t] < ids[kk] ? 1 : 0;
+    rank[kk] = r;
+  }
   __syncthreads();
+  KNJ_STAMP(9);
   float dot[KPG];
 #pragma unroll
   for (int j = 0; j < KPG; ++j) {
@@ -344,28 +443,30 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
     const float acc = (active && kk < K) ? q4k_dot(q[j], g, xv) : 0.0f;
     dot[j] = group_sum<16>(acc);
   }
-  if (!row_ok) return;
-  // gather the k dots into lane 0 in slot order
-  float dots[16];
-  int32_t ids[16];
-  float wts[16];
+  KNJ_STAMP(10);
+  // every lane folds the k products in ascending expert order:
+  // o = ((w_a d_a + w_b d_b) + ...) with d of slot kk in lane 16 (kk % 4)
+  float dk[KMAX];
 #pragma unroll
-  for (int j = 0; j < KPG; ++j)
+  for (int kk = 0; kk < KMAX; ++kk) dk[kk] = lane_bcast(dot[kk / 4], 16 * (kk % 4));
+  float o = 0.0f;
 #pragma unroll
-    for (int gg = 0; gg < 4; ++gg) {
-      const int kk = gg + 4 * j;
-      const float v = __shfl(dot[j], 16 * gg, 64);
-      if (kk < 16) dots[kk] = v;
+  for (int r = 0; r < KMAX; ++r) {
+    float wr = 0.0f, dr = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KMAX; ++kk) {
+      const bool hit = rank[kk] == r;
+      wr = hit ? wts[kk] : wr;
+      dr = hit ? dk[kk] : dr;
     }
-  if (lane != 0) return;
-  for (int kk = 0; kk < K; ++kk) {
-    ids[kk] = a.topk_idx[kk];
-    wts[kk] = a.topk_w[kk];
+    if (r < K) o = __fadd_rn(o, __fmul_rn(wr, dr));
   }
-  const float o = combine_sorted(dots, ids, wts, K);
-  const float v = a.resid ? __fadd_rn(a.resid[row], o) : o;
+  KNJ_STAMP(11);
+  if (!row_ok || lane != 0) return;
+  const float v = a.resid ? __fadd_rn(resid, o) : o;
   a.out[row] = v;
   if (a.hidden_copy) a.hidden_copy[row] = v;
+  KNJ_STAMP(12);
 }
 
 // ------------------------------------------------------------------ down (Q6_K)
