@@ -211,7 +211,7 @@ __device__ __forceinline__ void stage_x_load(const float* __restrict__ x,
 }
 
 __device__ __forceinline__ void stage_x_store(const XRegs& r, bool norm, float eps, int n,
-                                              float* xs, float* red) {
+                                              float* xs, float* red, float* xsum = nullptr) {
   float ss = 0.0f;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -235,6 +235,10 @@ __device__ __forceinline__ void stage_x_store(const XRegs& r, bool norm, float e
         o.w = r.v[j].w * scale * r.w[j].w;
       }
       *reinterpret_cast<float4*>(xs + xpad(i)) = o;
+      if (xsum) {  // sums of the 32-element sub-blocks: eight consecutive threads hold one
+        const float t = group_sum<8>((o.x + o.y) + (o.z + o.w));
+        if ((threadIdx.x & 7) == 0) xsum[i >> 5] = t;
+      }
     }
   }
   __syncthreads();
@@ -300,6 +304,22 @@ __device__ __forceinline__ void xslice_load(const float* xs_pad, int slice, XSli
   }
   x.s0 = a;
   x.s1 = b;
+}
+
+// The same with the two sub-block sums already known.
+__device__ __forceinline__ void xslice_load_sums(const float* xs_pad, int slice, float s0, float s1,
+                                                 XSlice& x) {
+  const float* p = xs_pad + 68 * slice;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(p + 4 * k);
+    x.v[4 * k] = t.x;
+    x.v[4 * k + 1] = t.y;
+    x.v[4 * k + 2] = t.z;
+    x.v[4 * k + 3] = t.w;
+  }
+  x.s0 = s0;
+  x.s1 = s1;
 }
 
 // The 64 activations of slice `slice` read straight from global memory into

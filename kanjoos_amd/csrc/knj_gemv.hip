@@ -24,6 +24,7 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__
                                                      const float* __restrict__ resid,
                                                      float* __restrict__ y) {
   __shared__ float xs[xpad_size(4096)];
+  __shared__ float xsum[128];
   __shared__ float red[8];
   constexpr int RPW = 64 / LPR;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -33,21 +34,36 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__
   const int row0 = (blockIdx.x * (kBlock / 64) + wave) * (RS * RPW);
   const bool active = sub < nslices;
   const int b = active ? (sub >> 2) : 0, g = sub & 3;
+  // loads in the order they are needed: x (and its norm weight) first, so the
+  // staging waits only for them; then the weights and the residual
+  XRegs xr;
+  stage_x_load(x, nw, n_in, xr);
   Q4Slice q[RS];
+  float rv[RS];
 #pragma unroll
   for (int st = 0; st < RS; ++st) {
     const int row = min(row0 + st * RPW + rsub, n_out - 1);  // valid address; extra rows dropped
     q[st] = q4k_load(w + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
   }
-  stage_x(x, nw, eps, n_in, xs, red);
+#pragma unroll
+  for (int st = 0; st < RS; ++st)
+    rv[st] = resid ? resid[min(row0 + st * RPW + rsub, n_out - 1)] : 0.0f;
+  __builtin_amdgcn_sched_barrier(0);
+  stage_x_store(xr, nw != nullptr, eps, n_in, xs, red, xsum);
   XSlice xv;
-  xslice_load(xs, active ? sub : 0, xv);
+  const int sl = active ? sub : 0;
+  xslice_load_sums(xs, sl, xsum[2 * sl], xsum[2 * sl + 1], xv);
+  float res[RS];
 #pragma unroll
   for (int st = 0; st < RS; ++st) {
     const int row = row0 + st * RPW + rsub;
     float acc = (active && row < n_out) ? q4k_dot(q[st], g, xv) : 0.0f;
-    acc = group_sum<LPR>(acc);
-    if (sub == 0 && row < n_out) y[row] = resid ? resid[row] + acc : acc;
+    res[st] = group_sum<LPR>(acc);
+  }
+#pragma unroll
+  for (int st = 0; st < RS; ++st) {
+    const int row = row0 + st * RPW + rsub;
+    if (sub == 0 && row < n_out) y[row] = resid ? rv[st] + res[st] : res[st];
   }
 }
 

@@ -96,6 +96,7 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, int
 #pragma unroll
   for (int j = 0; j < 4; ++j) lg[j] = lane + 64 * j < n_expert ? logits[lane + 64 * j] : -INFINITY;
   float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
+  KNJ_STAMP(5);
   mx = group_max<64>(mx);
   float ex[4], s = 0.0f;
 #pragma unroll
@@ -110,6 +111,7 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, int
     key[j] = lane + 64 * j < n_expert ? __float_as_uint(ex[j] / sum) + 1u : 0u;
   my_idx = 0;
   float my_p = 0.0f, keep = 0.0f;
+  KNJ_STAMP(6);
   for (int q = 0; q < k; ++q) {
     uint32_t b = max(max(key[0], key[1]), max(key[2], key[3]));
     b = wave_max_u32(b);
@@ -129,6 +131,7 @@ __device__ __forceinline__ void wave_route(const float* __restrict__ logits, int
   }
   const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
   my_w = my_p * inv;
+  KNJ_STAMP(7);
 }
 
 // ------------------------------------------------------------------ router
@@ -224,26 +227,58 @@ __global__ __launch_bounds__(kBlock) void k_topk(const float* __restrict__ logit
 // their weights requested as soon as the expert index is known.
 template <int RS>
 __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
+  static_assert(RS == 1 || RS == 2 || RS == 4, "one, two or four row pairs per wave");
   __shared__ float xs[xpad_size(2048)];
-  __shared__ float red[8];
+  __shared__ float xsum[64];  // sums of the 32-element sub-blocks of the normalised x
+  __shared__ int sel[16];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   KNJ_STAMP(0);
-  // x and its norm weight are requested with the routing inputs, so only the
-  // weight loads remain outstanding once the experts are known
-  XRegs xr;
-  stage_x_load(a.hx, a.norm_w, a.n_embd, xr);
-  int my_idx;
-  if (a.logits) {
-    float my_w;
-    wave_route(a.logits, a.n_expert, a.k, my_idx, my_w);
-    KNJ_STAMP(1);
-    if (blockIdx.x == 0 && wave == 0 && lane < a.k) {
-      a.topk_idx[lane] = my_idx;
-      a.topk_w[lane] = my_w;
+  // 1) wave 0 alone: x, its norm weight and the logits; the routing; x
+  // normalised into LDS.  The other waves have nothing outstanding at the
+  // barrier, so their weight loads issue as soon as the experts are known.
+  int my_idx = 0;
+  float my_w = 0.0f;
+  if (wave == 0) {
+    const int nj = a.n_embd >> 8;  // float4 per lane (n_embd <= 2048)
+    float4 xv[8], wv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < nj) {
+        xv[j] = *reinterpret_cast<const float4*>(a.hx + 4 * lane + 256 * j);
+        if (a.norm_w) wv[j] = *reinterpret_cast<const float4*>(a.norm_w + 4 * lane + 256 * j);
+      }
+    if (a.logits) {
+      wave_route(a.logits, a.n_expert, a.k, my_idx, my_w);
+    } else if (lane < a.k) {
+      my_idx = a.topk_idx[lane];
     }
-  } else {
-    my_idx = lane < a.k ? a.topk_idx[lane] : 0;
+    if (lane < a.k) sel[lane] = my_idx;
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < nj) ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
+    ss = group_sum<64>(ss);
+    const float scale = 1.0f / sqrtf(ss / (float)a.n_embd + a.eps);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j < nj) {
+        float4 o = xv[j];
+        if (a.norm_w) {
+          o.x = xv[j].x * scale * wv[j].x;
+          o.y = xv[j].y * scale * wv[j].y;
+          o.z = xv[j].z * scale * wv[j].z;
+          o.w = xv[j].w * scale * wv[j].w;
+        }
+        *reinterpret_cast<float4*>(xs + xpad(4 * lane + 256 * j)) = o;
+        // eight consecutive lanes hold one sub-block
+        const float t = group_sum<8>((o.x + o.y) + (o.z + o.w));
+        if ((lane & 7) == 0) xsum[(4 * lane + 256 * j) >> 5] = t;
+      }
   }
+  __syncthreads();
+  KNJ_STAMP(1);
+  // 2) the expert rows: wave = RS (slot, row) pairs, lanes [0,32) the gate
+  // row and [32,64) the up row, one 64-weight slice per lane
   const int half = lane >> 5, sub = lane & 31;
   const int nslices = a.n_embd >> 6;
   const bool active = sub < nslices;
@@ -253,32 +288,49 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   const int pair0 = (blockIdx.x * (kBlock / 64) + wave) * RS;
   const int b = sub >> 2, g = sub & 3;
   const uint8_t* base = half ? a.up : a.gate;
-  static_assert(RS == 2, "two row pairs per wave");
   // named registers (an indexed array was placed in scratch memory here)
-  Q4Slice q0, q1;
+  Q4Slice q0, q1, q2, q3;
   auto load_pair = [&](int pr, Q4Slice& q) {
     const int prc = min(pr, npairs - 1);  // always a valid row; unused results are dropped
     const int kk = prc / a.n_ff, row = prc - kk * a.n_ff;
-    const int e = lane_bcast(my_idx, kk);
+    const int e = sel[kk];
     q = q4k_load(base + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)(active ? b : 0) * KNJ_Q4K_BLOCK, g);
   };
   load_pair(pair0, q0);
-  load_pair(pair0 + 1, q1);
-  stage_x_store(xr, a.norm_w != nullptr, a.eps, a.n_embd, xs, red);
-  KNJ_STAMP(2);
+  if constexpr (RS >= 2) load_pair(pair0 + 1, q1);
+  if constexpr (RS == 4) {
+    load_pair(pair0 + 2, q2);
+    load_pair(pair0 + 3, q3);
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before any wait
   XSlice xv;
-  xslice_load(xs, active ? sub : 0, xv);
+  const int sl = active ? sub : 0;
+  xslice_load_sums(xs, sl, xsum[2 * sl], xsum[2 * sl + 1], xv);
+  KNJ_STAMP(2);
+  // all dot products before any store: a store counts in the same in-order
+  // completion counter as the loads, so a wait for a later load would also
+  // wait for the store
+  float res[RS];
 #pragma unroll
   for (int st = 0; st < RS; ++st) {
     const int pr = pair0 + st;
-    float acc = (active && pr < npairs) ? q4k_dot(st == 0 ? q0 : q1, g, xv) : 0.0f;
+    const Q4Slice& q = st == 0 ? q0 : st == 1 ? q1 : st == 2 ? q2 : q3;
+    float acc = (active && pr < npairs) ? q4k_dot(q, g, xv) : 0.0f;
     acc = group_sum<32>(acc);
     const float u = lane_bcast(acc, 32);
-    if (lane == 0 && pr < npairs) {
-      const float silu = acc / (1.0f + expf(-acc));
-      a.act[pr] = silu * u;  // act is [k][n_ff], pr = kk*n_ff + row
-    }
+    res[st] = (acc / (1.0f + expf(-acc))) * u;
     if (st == 0) KNJ_STAMP(3);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int st = 0; st < RS; ++st)
+      if (pair0 + st < npairs) a.act[pair0 + st] = res[st];  // act is [k][n_ff]
+  }
+  // the routing, for the down launch and the caller (kept until now so no
+  // wave waits on these stores before its loads)
+  if (a.logits && blockIdx.x == 0 && wave == 0 && lane < a.k) {
+    a.topk_idx[lane] = my_idx;
+    a.topk_w[lane] = my_w;
   }
   KNJ_STAMP(4);
 }
@@ -369,11 +421,13 @@ __device__ __forceinline__ float combine_sorted(const float* dots, const int32_t
 // into ascending expert order by lane 0.
 template <int KPG>
 __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
-  extern __shared__ float acts[];  // [k][xpad_size(n_ff)]
+  extern __shared__ float acts[];  // [k][xpad_size(n_ff)], then [k * n_ff / 32] sub-block sums
   constexpr int KMAX = 4 * KPG;    // k <= KMAX
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int gi = lane >> 4, sub = lane & 15;
-  const int F = a.n_ff, K = a.k;
+  const int F = a.n_ff, K = a.k, n = K * F;
+  const int fpad = xpad_size(F);
+  float* sums = acts + K * fpad;
   const int nslices = F >> 6;
   const bool active = sub < nslices;
   const uint64_t rb = (uint64_t)(F >> 8) * KNJ_Q4K_BLOCK;
@@ -382,8 +436,9 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   const int row = min((int)(blockIdx.x * (kBlock / 64) + wave), a.n_embd - 1);
   const bool row_ok = (int)(blockIdx.x * (kBlock / 64) + wave) < a.n_embd;
   const int b = active ? (sub >> 2) : 0, g = sub & 3;
-  // the routing (the same for every row) and this row's residual, requested
-  // with the weights so that nothing after the dot products waits on memory
+  // 1) the routing (the same for every row), the first 8192 activations and
+  // this row's residual; the expert weights follow, so staging the
+  // activations waits only for the activations
   int ids[KMAX];
   float wts[KMAX];
 #pragma unroll
@@ -391,6 +446,19 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
     ids[kk] = kk < K ? a.topk_idx[kk] : 0x7FFFFFFF;
     wts[kk] = kk < K ? a.topk_w[kk] : 0.0f;
   }
+  const float resid = a.resid ? a.resid[row] : 0.0f;
+  // (named registers: an indexed array was placed in scratch memory)
+  float4 v0, v1, v2, v3, v4, v5, v6, v7;
+  auto ld = [&](int base, float4& v0, float4& v1, float4& v2, float4& v3, float4& v4, float4& v5,
+                float4& v6, float4& v7) {
+    auto one = [&](int j, float4& v) {
+      const int i = base + 4 * kBlock * j;
+      v = *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
+    };
+    one(0, v0); one(1, v1); one(2, v2); one(3, v3);
+    one(4, v4); one(5, v5); one(6, v6); one(7, v7);
+  };
+  ld(4 * threadIdx.x, v0, v1, v2, v3, v4, v5, v6, v7);
   Q4Slice q[KPG];
 #pragma unroll
   for (int j = 0; j < KPG; ++j) {
@@ -400,30 +468,30 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
     for (int t = 1; t < KMAX; ++t) e = kk == t ? ids[t] : e;
     q[j] = q4k_load(a.down + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q4K_BLOCK, g);
   }
-  const float resid = a.resid ? a.resid[row] : 0.0f;
-  // stage the k activation vectors once per workgroup: 4 loads in flight per
-  // thread per round (named registers: an indexed array was placed in scratch)
-  const int fpad = xpad_size(F);
-  for (int base = 4 * threadIdx.x; base < K * F; base += 16 * kBlock) {
-    const int n = K * F;
-    const int i0 = base, i1 = base + 4 * kBlock, i2 = base + 8 * kBlock, i3 = base + 12 * kBlock;
-    const float4 v0 = *reinterpret_cast<const float4*>(a.act + i0);
-    const float4 v1 = *reinterpret_cast<const float4*>(a.act + (i1 < n ? i1 : i0));
-    const float4 v2 = *reinterpret_cast<const float4*>(a.act + (i2 < n ? i2 : i0));
-    const float4 v3 = *reinterpret_cast<const float4*>(a.act + (i3 < n ? i3 : i0));
-    auto put = [&](int i, const float4& v) {
-      if (i < n) {
+  __builtin_amdgcn_sched_barrier(0);  // every weight load is issued before any wait
+  // 2) activations to LDS, with the sum of every 32-element sub-block (eight
+  // consecutive threads hold one sub-block)
+  auto put = [&](int base, const float4& v0, const float4& v1, const float4& v2, const float4& v3,
+                 const float4& v4, const float4& v5, const float4& v6, const float4& v7) {
+    auto one = [&](int j, const float4& v) {
+      const int i = base + 4 * kBlock * j;
+      if (i < n) {  // uniform over each group of eight lanes (n is a multiple of 32)
         const int kk = i / F, c = i - kk * F;
         *reinterpret_cast<float4*>(acts + kk * fpad + xpad(c)) = v;
+        const float t = group_sum<8>((v.x + v.y) + (v.z + v.w));
+        if ((threadIdx.x & 7) == 0) sums[i >> 5] = t;
       }
     };
-    put(i0, v0);
-    put(i1, v1);
-    put(i2, v2);
-    put(i3, v3);
+    one(0, v0); one(1, v1); one(2, v2); one(3, v3);
+    one(4, v4); one(5, v5); one(6, v6); one(7, v7);
+  };
+  put(4 * threadIdx.x, v0, v1, v2, v3, v4, v5, v6, v7);
+  for (int base = 4 * threadIdx.x + 32 * kBlock; base < n; base += 32 * kBlock) {
+    ld(base, v0, v1, v2, v3, v4, v5, v6, v7);
+    put(base, v0, v1, v2, v3, v4, v5, v6, v7);
   }
   // slot order by ascending expert index (ids are distinct): rank[kk] =
-  // #{t : ids[t] < ids[kk]}; computed while the loads are in flight
+  // #{t : ids[t] < ids[kk]}
   int rank[KMAX];
 #pragma unroll
   for (int kk = 0; kk < KMAX; ++kk) {
@@ -437,10 +505,11 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   float dot[KPG];
 #pragma unroll
   for (int j = 0; j < KPG; ++j) {
-    const int kk = gi + 4 * j;
+    const int kk = min(gi + 4 * j, K - 1);
+    const int sl = active ? sub : 0;
     XSlice xv;
-    xslice_load(acts + min(kk, K - 1) * fpad, active ? sub : 0, xv);
-    const float acc = (active && kk < K) ? q4k_dot(q[j], g, xv) : 0.0f;
+    xslice_load_sums(acts + kk * fpad, sl, sums[(kk * F >> 5) + 2 * sl], sums[(kk * F >> 5) + 2 * sl + 1], xv);
+    const float acc = (active && gi + 4 * j < K) ? q4k_dot(q[j], g, xv) : 0.0f;
     dot[j] = group_sum<16>(acc);
   }
   KNJ_STAMP(10);
@@ -561,11 +630,14 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s) {
   if (a.type_down == KNJ_TYPE_Q4_K && a.n_ff <= 1024) {
     const int kpg = (a.k + 3) / 4;
     const int grid = (a.n_embd + 3) / 4;
-    const size_t lds = (size_t)a.k * xpad_size(a.n_ff) * 4;
-#define GD(J)                                                                       \
-  if (kpg == J) {                                                                   \
-    hipLaunchKernelGGL(k_expert_down<J>, dim3(grid), dim3(kBlock), lds, s, a);      \
-    return hipGetLastError();                                                       \
+    const size_t lds = ((size_t)a.k * xpad_size(a.n_ff) + (size_t)a.k * a.n_ff / 32) * 4;
+#define GD(J)                                                                                \
+  if (kpg == J) {                                                                            \
+    if (lds > 65536)                                                                         \
+      (void)hipFuncSetAttribute((const void*)k_expert_down<J>,                               \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);       \
+    hipLaunchKernelGGL(k_expert_down<J>, dim3(grid), dim3(kBlock), lds, s, a);               \
+    return hipGetLastError();                                                                \
   }
     GD(1) GD(2) GD(3) GD(4)
 #undef GD
