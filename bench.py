@@ -52,6 +52,40 @@ def bytes_per_token(cfg: K.ModelConfig, ctx: int) -> dict:
                 kv_per_layer=kv, head=head)
 
 
+def expert_traffic():
+    """HBM bytes per k_expert_gateup launch from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the counters' reading
+    for a device copy of known size), or None when it is absent."""
+    path = os.path.join(ROOT, "profiles", "k_expert_gateup_traffic.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["hbm_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def calib_probe() -> None:
+    """Two kernels whose HBM traffic is known exactly: k_gemv_bf16 over a
+    2048 x 65536 bf16 matrix (268,435,456 bytes read once; x and y are 8 KiB and
+    256 KiB) and k_dequant of 16,777,216 Q4_K weights (9,437,184 bytes read,
+    67,108,864 bytes written)."""
+    n_in, n_out = 2048, 65536
+    w = K.DeviceBuffer(n_in * n_out * 2)
+    w.zero()
+    x = K.DeviceBuffer(n_in * 4)
+    x.zero()
+    y = K.DeviceBuffer(n_out * 4)
+    n = 1 << 24
+    q = K.DeviceBuffer(n // 256 * 144)
+    q.zero()
+    out = K.DeviceBuffer(n * 4)
+    for _ in range(2):
+        K.gemv(K.TYPE_BF16, w, n_in, n_out, x, y)
+        K.dequant(K.TYPE_Q4_K, q, n, out)
+    K.synchronize()
+    log("calibration probe: 2 x (bf16 GEMV 256 MiB read, Q4_K dequant 64 MiB write)")
+
+
 def cpu_baseline(model: K.Model, cfg: K.ModelConfig, budget_s: float, max_tokens: int) -> dict:
     """The CPU oracle (restating the reference's CPU forward pass) on the host
     cores, continuing from the GPU's weights and KV cache at the same position."""
@@ -95,7 +129,12 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--ctx", type=int, default=4096, help="KV prefill length before timing")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--expert-iters", type=int, default=480)
+    ap.add_argument("--expert-steps", type=int, default=8,
+                    help="decode steps whose expert launches are timed one by one with events")
+    ap.add_argument("--calib-probe", action="store_true",
+                    help="also run two streaming kernels of known traffic (a 256 MiB bf16 GEMV "
+                         "read, a 256 MiB f32 dequant write) to scale rocprofv3 "
+                         "FETCH_SIZE/WRITE_SIZE readings")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -109,7 +148,7 @@ def main() -> int:
 
     caps = K.open_device(0)
     log(f"device {caps.name.decode()} {caps.gcn_arch.decode()} {caps.cu_count} CUs")
-    n_ctx = args.ctx + args.warmup + args.steps + 8
+    n_ctx = args.ctx + args.warmup + args.steps + args.expert_steps + 8
     cfg = K.qwen3_30b_a3b(n_ctx=n_ctx)
     t0 = time.perf_counter()
     model = K.Model.synthetic(cfg, seed=args.seed)
@@ -143,8 +182,10 @@ def main() -> int:
     bpt = bytes_per_token(cfg, int(round(mean_ctx)))
     token_gbps = bpt["total"] / (ms_per_step * 1e-3) / 1e9
 
-    # dominant kernel: expert gate/up GEMV (and down), events on the model stream
-    us_gu, us_dn = model.time_experts(args.expert_iters)
+    # dominant kernel: expert gate/up GEMV (and down) inside decode steps that
+    # continue the timed run; each launch records HIP start/end events of its own
+    # execution on the model stream
+    us_gu, us_dn = model.time_experts(args.expert_steps)
     H, F, k = cfg.n_embd, cfg.n_ff, cfg.n_expert_used
     bytes_gu = k * 2 * K.row_bytes(cfg.type_gate_up, H) * F
     bytes_dn = k * K.row_bytes(cfg.type_down, F) * H
@@ -152,6 +193,9 @@ def main() -> int:
     gbps_dn = bytes_dn / (us_dn * 1e-6) / 1e9
     gbps_ex = (bytes_gu + bytes_dn) / ((us_gu + us_dn) * 1e-6) / 1e9
     log(f"expert gate/up {us_gu:.2f} us ({gbps_gu:.0f} GB/s), down {us_dn:.2f} us ({gbps_dn:.0f} GB/s)")
+    traffic = expert_traffic()
+    if args.calib_probe:
+        calib_probe()
 
     result = {
         "metric": "decode tokens/s at batch 1 + achieved HBM GB/s (% of 8 TB/s) on Q4_K expert GEMV",
@@ -179,7 +223,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps_gu / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
             "bytes_per_launch": bytes_gu,
             "avg_us": round(us_gu, 3),
             "down_kernel": {"bytes_per_launch": bytes_dn, "avg_us": round(us_dn, 3),

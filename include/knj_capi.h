@@ -152,12 +152,14 @@ int knj_model_kv_upload(knj_model* m, const uint16_t* k_host, const uint16_t* v_
 /* Times `iters` greedy steps with HIP events on the model's stream (graph
  * replays), returns total milliseconds. */
 int knj_model_time_decode(knj_model* m, int iters, float* ms_out);
-/* Times the expert GEMV kernels of the decode step with HIP events on the
- * model's stream: `iters` launches of the gate/up kernel, then `iters` of the
- * down kernel, each launch on the next layer's weights (rotating through all
- * layers so repeats come from HBM, not the 256 MB last-level cache).  Returns
- * the average microseconds per launch of each. */
-int knj_model_time_experts(knj_model* m, int iters, float* us_gateup, float* us_down);
+/* Times the expert GEMV kernels inside real decode steps: `steps` (1..64)
+ * greedy tokens from token 0 at the current position, the step's kernels
+ * launched directly (no graph); every layer's gate/up and down launch records
+ * HIP start/end events of its own execution (hipExtLaunchKernel) on the
+ * model's stream.  Returns the mean
+ * microseconds per launch of each over n_layer * steps launches; advances the
+ * position by `steps`. */
+int knj_model_time_experts(knj_model* m, int steps, float* us_gateup, float* us_down);
 
 #ifdef __cplusplus
 }

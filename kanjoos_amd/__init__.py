@@ -365,8 +365,10 @@ class Model:
         check(lib().knj_model_time_decode(self.h, iters, C.byref(ms)))
         return ms.value
 
-    def time_experts(self, iters: int):
-        """(gate/up, down) average microseconds per launch, rotating over layers."""
+    def time_experts(self, steps: int):
+        """(gate/up, down) mean microseconds per launch over `steps` greedy decode
+        steps launched directly, each expert launch recording HIP start/end events
+        (n_layer * steps launches of each); advances the position by `steps`."""
         a, b = C.c_float(), C.c_float()
-        check(lib().knj_model_time_experts(self.h, iters, C.byref(a), C.byref(b)))
+        check(lib().knj_model_time_experts(self.h, steps, C.byref(a), C.byref(b)))
         return a.value, b.value

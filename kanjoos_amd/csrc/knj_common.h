@@ -100,8 +100,12 @@ struct ExpertArgs {
   float* hidden_copy;     // optional second destination of out
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
-hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s);
-hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s);
+// t0/t1, when set, are recorded by the kernel dispatch itself at its start and
+// end (hipExtLaunchKernel): the launch's execution time, as a profiler sees it.
+hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t0 = nullptr,
+                                hipEvent_t t1 = nullptr);
+hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0 = nullptr,
+                              hipEvent_t t1 = nullptr);
 
 // Fused decode attention of one token (QK-norm, RoPE, f16 append, split-KV
 // attention, merge).  q/k/v are the raw projections of this token.

@@ -87,6 +87,8 @@ struct knj_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool use_graph = true;  // KNJ_NO_GRAPH=1 launches the step's kernels directly
+  hipEvent_t* expert_events = nullptr;  // set by knj_model_time_experts: 4 per layer per step
+  int expert_slot = 0;
   std::vector<void*> owned;
 };
 
@@ -269,7 +271,10 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
                 img + lo.gate, img + lo.up, img + lo.down,
                 c.type_gate_up, c.type_down, H, c.n_ff, c.n_expert, c.n_expert_used, m->act, m->x,
                 m->x, m->hidden + (uint64_t)il * H};
-  KNJ_HIP(launch_experts(ea, s));
+  // timing runs: each expert launch records its own start/end events
+  hipEvent_t* ev = m->expert_events ? m->expert_events + 4 * m->expert_slot++ : nullptr;
+  KNJ_HIP(launch_expert_gateup(ea, s, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr));
+  KNJ_HIP(launch_expert_down(ea, s, ev ? ev[2] : nullptr, ev ? ev[3] : nullptr));
   return KNJ_OK;
 }
 
@@ -520,33 +525,41 @@ int knj_model_time_decode(knj_model* m, int iters, float* ms_out) {
   return KNJ_OK;
 }
 
-int knj_model_time_experts(knj_model* m, int iters, float* us_gateup, float* us_down) {
-  KNJ_CHECK_ARG(m && us_gateup && us_down && iters > 0, "bad arguments");
-  const knj_model_config& c = m->c;
-  hipEvent_t ev[3];
-  for (auto& e : ev) KNJ_HIP(hipEventCreate(&e));
-  for (int phase = 0; phase < 2; ++phase) {
-    KNJ_HIP(hipEventRecord(ev[phase], m->stream));
-    for (int i = 0; i < iters; ++i) {
-      const int il = i % c.n_layer;  // rotate so repeats come from HBM
-      const knj_layer_offsets& lo = m->lo[il];
-      // as in the decode step: gate/up routes from the layer's logits
-      ExpertArgs ea{m->hx, nullptr, 0.0f, m->router_logits + (uint64_t)il * c.n_expert,
-                    m->topk_idx + (uint64_t)il * c.n_expert_used,
-                    m->topk_w + (uint64_t)il * c.n_expert_used, m->image + lo.gate, m->image + lo.up,
-                    m->image + lo.down, c.type_gate_up, c.type_down, c.n_embd, c.n_ff, c.n_expert,
-                    c.n_expert_used, m->act, nullptr, m->ctx, nullptr};
-      KNJ_HIP(phase == 0 ? launch_expert_gateup(ea, m->stream) : launch_expert_down(ea, m->stream));
-    }
+int knj_model_time_experts(knj_model* m, int steps, float* us_gateup, float* us_down) {
+  KNJ_CHECK_ARG(m && us_gateup && us_down && steps > 0 && steps <= 64, "bad arguments");
+  if (m->pos + steps > m->c.n_ctx) {
+    set_error("context exhausted");
+    return KNJ_E_ARG;
   }
-  KNJ_HIP(hipEventRecord(ev[2], m->stream));
-  KNJ_HIP(hipEventSynchronize(ev[2]));
-  float a = 0.0f, b = 0.0f;
-  KNJ_HIP(hipEventElapsedTime(&a, ev[0], ev[1]));
-  KNJ_HIP(hipEventElapsedTime(&b, ev[1], ev[2]));
+  const int n = 4 * m->c.n_layer * steps;
+  std::vector<hipEvent_t> ev(n, nullptr);
+  for (auto& e : ev) KNJ_HIP(hipEventCreate(&e));
+  // greedy decode from token 0, the step's kernels launched directly; every
+  // expert launch records start/end events of its own execution
+  int rc = set_state(m, 0, 0);
+  m->expert_events = ev.data();
+  m->expert_slot = 0;
+  for (int i = 0; i < steps && !rc; ++i) rc = enqueue_step(m, m->stream);
+  m->expert_events = nullptr;
+  if (!rc) {
+    const hipError_t e = hipStreamSynchronize(m->stream);
+    if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+  }
+  double gu = 0.0, dn = 0.0;
+  for (int i = 0; i < m->c.n_layer * steps && !rc; ++i) {
+    float a = 0.0f, b = 0.0f;
+    hipError_t e = hipEventElapsedTime(&a, ev[4 * i], ev[4 * i + 1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&b, ev[4 * i + 2], ev[4 * i + 3]);
+    if (e != hipSuccess) rc = hip_fail(e, "hipEventElapsedTime");
+    gu += a;
+    dn += b;
+  }
   for (auto& e : ev) (void)hipEventDestroy(e);
-  *us_gateup = a * 1000.0f / (float)iters;
-  *us_down = b * 1000.0f / (float)iters;
+  if (rc) return rc;
+  m->pos += steps;
+  const double launches = (double)m->c.n_layer * steps;
+  *us_gateup = (float)(gu * 1000.0 / launches);
+  *us_down = (float)(dn * 1000.0 / launches);
   return KNJ_OK;
 }
 

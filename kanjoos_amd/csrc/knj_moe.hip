@@ -9,6 +9,8 @@
 //   down       y_e = W_down[e] . act_e, out = resid + sum_e w_e * y_e with the
 //              experts summed in ascending index (the scatter order of
 //              model.cpp:464-508).
+#include <hip/hip_ext.h>
+
 #include "knj_common.h"
 #include "knj_dev.h"
 
@@ -598,7 +600,18 @@ int pow2_at_least(int v) {
   return p;
 }
 
+// hipLaunchKernelGGL, or the timed launch when start/stop events are given
+template <class F>
+void launch_maybe_timed(F kernel, dim3 grid, size_t lds, hipStream_t s, hipEvent_t t0,
+                        hipEvent_t t1, const ExpertArgs& a) {
+  if (t0)
+    hipExtLaunchKernelGGL(kernel, grid, dim3(kBlock), (uint32_t)lds, s, t0, t1, 0u, a);
+  else
+    hipLaunchKernelGGL(kernel, grid, dim3(kBlock), lds, s, a);
+}
+
 }  // namespace
+
 
 hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
   // four rows (waves) per workgroup; the last workgroup also ranks the experts
@@ -612,21 +625,21 @@ hipError_t launch_topk(const float* logits, int n_expert, int k, int32_t* idx, f
   return hipGetLastError();
 }
 
-hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s) {
+hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
   const int npairs = a.k * a.n_ff;
   if (a.n_embd <= 2048) {
     constexpr int RS = 2;
     const int grid = (npairs + 4 * RS - 1) / (4 * RS);
-    hipLaunchKernelGGL(k_expert_gateup<RS>, dim3(grid), dim3(kBlock), 0, s, a);
+    launch_maybe_timed(k_expert_gateup<RS>, dim3(grid), 0, s, t0, t1, a);
     return hipGetLastError();
   }
   const size_t lds = (size_t)xpad_size(a.n_embd) * 4;
   const int grid = std::min(2048, (npairs + 3) / 4);
-  hipLaunchKernelGGL(k_expert_gateup_wide, dim3(grid), dim3(kBlock), lds, s, a);
+  launch_maybe_timed(k_expert_gateup_wide, dim3(grid), lds, s, t0, t1, a);
   return hipGetLastError();
 }
 
-hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s) {
+hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
   if (a.type_down == KNJ_TYPE_Q4_K && a.n_ff <= 1024) {
     const int kpg = (a.k + 3) / 4;
     const int grid = (a.n_embd + 3) / 4;
@@ -636,7 +649,7 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s) {
     if (lds > 65536)                                                                         \
       (void)hipFuncSetAttribute((const void*)k_expert_down<J>,                               \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);       \
-    hipLaunchKernelGGL(k_expert_down<J>, dim3(grid), dim3(kBlock), lds, s, a);               \
+    launch_maybe_timed(k_expert_down<J>, dim3(grid), lds, s, t0, t1, a);                     \
     return hipGetLastError();                                                                \
   }
     GD(1) GD(2) GD(3) GD(4)
@@ -650,7 +663,11 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s) {
   const int grid = (a.n_embd + rows_per_block - 1) / rows_per_block;
 #define GQ(L)                                                                                   \
   if (lpr == L) {                                                                               \
-    hipLaunchKernelGGL(k_expert_down_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a, rows_per_block); \
+    if (t0)                                                                                     \
+      hipExtLaunchKernelGGL(k_expert_down_q6k<L>, dim3(grid), dim3(kBlock), (uint32_t)lds, s, t0, \
+                            t1, 0u, a, rows_per_block);                                         \
+    else                                                                                        \
+      hipLaunchKernelGGL(k_expert_down_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a, rows_per_block); \
     return hipGetLastError();                                                                   \
   }
   GQ(8) GQ(16) GQ(32) GQ(64)
