@@ -102,6 +102,22 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
                          const float* resid, float* out, float* logits, int32_t* topk_idx,
                          float* topk_w, void* stream);
 
+/* ------------------------------------------------------------ MoE over many tokens (config 2)
+ * knj_moe_batch_layer: Model::moe on n_tokens rows at once (model.cpp:399-510
+ *   with m > 1, the batched matmul of :354-364): per token RMSNorm(x) (norm
+ *   skipped when norm_w is NULL), router logits, softmax and top-k as in
+ *   knj_moe_router; the (token, expert) pairs grouped by expert so every
+ *   expert's weights are read once for all its tokens; gate/up, silu(gate)*up,
+ *   down; out[t] = resid[t] + sum over t's experts in ascending index of
+ *   w * down.  x, resid, out: [n_tokens][n_embd]; logits: [n_tokens][n_expert];
+ *   topk_idx/topk_w: [n_tokens][k].  Q4_K gate/up/down; n_embd and n_ff
+ *   multiples of 256, at most 4096; n_expert <= 256; k <= 16. */
+int knj_moe_batch_layer(const float* x, const float* norm_w, float eps, const float* router_w,
+                        const void* gate, const void* up, const void* down, int type_gate_up,
+                        int type_down, int n_tokens, int n_embd, int n_ff, int n_expert, int k,
+                        const float* resid, float* out, float* logits, int32_t* topk_idx,
+                        float* topk_w, void* stream);
+
 /* ------------------------------------------------------------ attention
  * knj_attention_step: the attention block of one decode token
  *   (/root/reference/src/model/model.cpp:567-616 with an f16 cache): per-head

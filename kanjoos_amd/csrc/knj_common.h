@@ -107,6 +107,28 @@ hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t
 hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0 = nullptr,
                               hipEvent_t t1 = nullptr);
 
+// MoE layer over m tokens at once (prefill chunks, batched decode): RMSNorm,
+// router, per-token top-k, experts grouped on the matrix cores, combine.
+// Q4_K gate/up/down, n_embd and n_ff multiples of 256 and <= 4096,
+// n_expert <= 256, k <= 16.
+struct MoeBatchArgs {
+  const float* x;          // [m][n_embd] residual stream
+  const float* norm_w;     // ffn_norm (null: x is used as is)
+  float eps;
+  const float* router_w;   // [n_expert][n_embd] f32
+  const uint8_t* gate;     // [n_expert] slabs
+  const uint8_t* up;
+  const uint8_t* down;
+  int m, n_embd, n_ff, n_expert, k;
+  const float* resid;      // optional [m][n_embd] added to the output
+  float* out;              // [m][n_embd]
+  float* logits;           // [m][n_expert]
+  int32_t* topk_idx;       // [m][k], selection order
+  float* topk_w;           // [m][k]
+};
+uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int k);
+hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s);
+
 // Fused decode attention of one token (QK-norm, RoPE, f16 append, split-KV
 // attention, merge).  q/k/v are the raw projections of this token.
 struct AttnArgs {

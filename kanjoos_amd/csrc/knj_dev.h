@@ -446,5 +446,56 @@ __device__ __forceinline__ int argmax_index(unsigned long long key) {
   return (int)(0xFFFFFFFFu - (uint32_t)(key & 0xFFFFFFFFull));
 }
 
+// Softmax + top-k routing of one token by one wave, with no LDS and no
+// barrier (Model::moe, /root/reference/src/model/model.cpp:420-460): each lane holds
+// experts lane, lane+64, ..  Probabilities are non-negative, so their bit
+// patterns order like the values; a key is those bits + 1 (0 marks an expert
+// already taken).  Each of the k rounds takes the wave maximum of the keys and,
+// among the experts holding it, the lowest index (the strict-'>' argmax with
+// ties to the lower index, model.cpp:442-451).  Lane q < k returns selection
+// q: its expert and its weight p / sum of the kept p, the sum taken in
+// selection order (model.cpp:452-458).  n_expert <= 256.
+__device__ __forceinline__ void wave_route(const float* __restrict__ logits, int n_expert, int k,
+                                           int& my_idx, float& my_w) {
+  const int lane = threadIdx.x & 63;
+  float lg[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) lg[j] = lane + 64 * j < n_expert ? logits[lane + 64 * j] : -INFINITY;
+  float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
+  mx = group_max<64>(mx);
+  float ex[4], s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ex[j] = lane + 64 * j < n_expert ? expf(lg[j] - mx) : 0.0f;
+    s += ex[j];
+  }
+  const float sum = group_sum<64>(s);
+  uint32_t key[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    key[j] = lane + 64 * j < n_expert ? __float_as_uint(ex[j] / sum) + 1u : 0u;
+  my_idx = 0;
+  float my_p = 0.0f, keep = 0.0f;
+  for (int q = 0; q < k; ++q) {
+    uint32_t b = max(max(key[0], key[1]), max(key[2], key[3]));
+    b = wave_max_u32(b);
+    const unsigned long long m0 = __ballot(key[0] == b), m1 = __ballot(key[1] == b);
+    const unsigned long long m2 = __ballot(key[2] == b), m3 = __ballot(key[3] == b);
+    const int e = m0 ? __builtin_ctzll(m0)
+                     : m1 ? 64 + __builtin_ctzll(m1)
+                          : m2 ? 128 + __builtin_ctzll(m2) : 192 + __builtin_ctzll(m3);
+    const float p = __uint_as_float(b - 1u);
+    keep += p;
+    if (lane == q) {
+      my_idx = e;
+      my_p = p;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) key[j] = (lane == (e & 63) && j == (e >> 6)) ? 0u : key[j];
+  }
+  const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
+  my_w = my_p * inv;
+}
+
 }  // namespace dev
 }  // namespace knj

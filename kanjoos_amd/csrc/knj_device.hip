@@ -293,6 +293,34 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
   return KNJ_OK;
 }
 
+int knj_moe_batch_layer(const float* x, const float* norm_w, float eps, const float* router_w,
+                        const void* gate, const void* up, const void* down, int type_gate_up,
+                        int type_down, int n_tokens, int n_embd, int n_ff, int n_expert, int k,
+                        const float* resid, float* out, float* logits, int32_t* topk_idx,
+                        float* topk_w, void* stream) {
+  int rc = require_open();
+  if (rc) return rc;
+  KNJ_CHECK_ARG(n_tokens > 0 && n_tokens <= 65536, "n_tokens must be in [1, 65536]");
+  KNJ_CHECK_ARG(n_embd > 0 && n_embd % 256 == 0 && n_embd <= 4096,
+                "n_embd must be a positive multiple of 256, at most 4096");
+  KNJ_CHECK_ARG(n_ff > 0 && n_ff % 256 == 0 && n_ff <= 4096,
+                "n_ff must be a positive multiple of 256, at most 4096");
+  KNJ_CHECK_ARG(n_expert > 0 && n_expert <= 256, "n_expert must be in [1, 256]");
+  KNJ_CHECK_ARG(k > 0 && k <= 16 && k <= n_expert, "k must be in [1, min(16, n_expert)]");
+  KNJ_CHECK_ARG(type_gate_up == KNJ_TYPE_Q4_K && type_down == KNJ_TYPE_Q4_K,
+                "the batched expert path takes Q4_K gate/up/down");
+  KNJ_CHECK_ARG(x && router_w && gate && up && down && out && logits && topk_idx && topk_w,
+                "null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  void* scr = device_scratch(moe_batch_scratch_bytes(n_tokens, n_embd, n_ff, n_expert, k), s);
+  if (!scr) return hip_fail(hipErrorOutOfMemory, "scratch");
+  MoeBatchArgs a{x, norm_w, eps, router_w, (const uint8_t*)gate, (const uint8_t*)up,
+                 (const uint8_t*)down, n_tokens, n_embd, n_ff, n_expert, k, resid, out, logits,
+                 topk_idx, topk_w};
+  KNJ_HIP(launch_moe_batch(a, scr, s));
+  return KNJ_OK;
+}
+
 int knj_attention_step(const float* q, const float* k, const float* v, const float* q_norm,
                        const float* k_norm, float eps, float rope_base, int pos, int n_head,
                        int n_head_kv, int head_dim, int n_ctx, uint16_t* k_cache, uint16_t* v_cache,

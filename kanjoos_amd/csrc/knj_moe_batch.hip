@@ -1,0 +1,478 @@
+// kanjoos_amd/csrc/knj_moe_batch.hip -- the MoE layer over many tokens at once
+// (prefill chunks, batched decode).
+//
+// Device side of Model::moe with m > 1 (/root/reference/src/model/model.cpp:399-510):
+// router logits for every token, softmax + top-k per token, the (token, expert)
+// pairs bucketed by expert so each expert's weights are read once for all of
+// its tokens (model.cpp:456-457, 462-477), gate/up + SwiGLU, down, and the
+// weighted sum of each token's k expert outputs in ascending expert order plus
+// the residual.
+//
+// The expert GEMMs run on the matrix cores with f32-equivalent operands.  A
+// Q4_K weight is d*sc*q - dmin*m; per 32-weight sub-block
+//   sum_i w_i x_i = d * sum_i (sc*q_i) x_i - dmin * m * sum_i x_i.
+// sc*q_i (<= 63*15) is an exact f16 integer; x is split into an f16 high part
+// and an f16 remainder, so every product is exact in the f32 accumulator and x
+// keeps ~22 significant bits.  The min term is one more matrix-core step over
+// the per-sub-block sums of x (also split hi/lo) against the 6-bit mins.  d and
+// dmin scale the two accumulators once per 256-weight super-block.
+#include "knj_common.h"
+#include "knj_dev.h"
+
+namespace knj {
+namespace {
+
+using namespace dev;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTok = 32;      // pairs (A rows) per work item
+constexpr int kRowsWG = 128;  // weight rows per workgroup (32 per wave)
+
+// Order of the 8 weights a lane unpacks from 8 code bytes (low halves of bytes
+// 0, 2, then 1, 3, ...): position j holds weight perm8(j).  The A operand (x)
+// is stored in the same order.
+__host__ __device__ constexpr int perm8(int j) { return (j & 4) | ((j & 1) << 1) | ((j & 2) >> 1); }
+
+__device__ __forceinline__ half2v as_h2(uint32_t v) { return __builtin_bit_cast(half2v, v); }
+
+// 8 weights sc*q from two code words (bytes c0..c7), nibble `shift` (0 low, 4
+// high), in perm8 order.  (0x6400 | q) is the f16 1024 + q; fma with sc and
+// -1024*sc leaves q*sc exactly.
+__device__ __forceinline__ half8 q4_unpack(uint32_t w0, uint32_t w1, int shift, half2v sc2,
+                                           half2v nc2) {
+  auto cv = [&](uint32_t w) {
+    return __builtin_elementwise_fma(as_h2((w & 0x000F000Fu) | 0x64006400u), sc2, nc2);
+  };
+  const half2v a = cv(w0 >> shift), b = cv(w0 >> (shift + 8));
+  const half2v c = cv(w1 >> shift), d = cv(w1 >> (shift + 8));
+  return half8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+}
+
+__device__ __forceinline__ half8 ld_h8(const _Float16* p) {
+  return __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(p));
+}
+
+__device__ __forceinline__ f32x16 mfma32(half8 a, half8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ operand prep
+// Row r of src (n floats, n % 256 == 0): optionally RMS-normalised with w
+// (model.cpp:240-271), then written as f32 (dst, optional), as f16 hi/lo in
+// perm8 order, and as per-32 sums split hi/lo.
+template <bool NORM>
+__global__ __launch_bounds__(kBlock) void k_split_rows(const float* __restrict__ src,
+                                                       const float* __restrict__ nw, float eps,
+                                                       int n, float* __restrict__ dst,
+                                                       _Float16* __restrict__ hi,
+                                                       _Float16* __restrict__ lo,
+                                                       _Float16* __restrict__ shi,
+                                                       _Float16* __restrict__ slo) {
+  __shared__ float red[8];
+  const int r = blockIdx.x, t = threadIdx.x;
+  const float* s = src + (uint64_t)r * n;
+  // 8-element groups t and t + 256 (n <= 4096)
+  float v[2][8];
+  float ss = 0.0f;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int g = t + kBlock * q;
+    if (8 * g < n) {
+      const float4 a = *reinterpret_cast<const float4*>(s + 8 * g);
+      const float4 b = *reinterpret_cast<const float4*>(s + 8 * g + 4);
+      v[q][0] = a.x; v[q][1] = a.y; v[q][2] = a.z; v[q][3] = a.w;
+      v[q][4] = b.x; v[q][5] = b.y; v[q][6] = b.z; v[q][7] = b.w;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += v[q][j] * v[q][j];
+    }
+  }
+  float scale = 1.0f;
+  if (NORM) {
+    ss = block_sum(ss, red);
+    scale = 1.0f / sqrtf(ss / (float)n + eps);
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int g = t + kBlock * q;
+    if (8 * g < n) {  // uniform over aligned groups of 4 threads (n % 32 == 0)
+      if (NORM) {
+        const float4 a = *reinterpret_cast<const float4*>(nw + 8 * g);
+        const float4 b = *reinterpret_cast<const float4*>(nw + 8 * g + 4);
+        const float w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[q][j] = v[q][j] * scale * w[j];
+      }
+      if (dst) {
+        float* d = dst + (uint64_t)r * n + 8 * g;
+        *reinterpret_cast<float4*>(d) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
+        *reinterpret_cast<float4*>(d + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
+      }
+      half8 h, l;
+      float sum = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float x = v[q][perm8(j)];
+        h[j] = (_Float16)x;
+        l[j] = (_Float16)(x - (float)h[j]);
+        sum += v[q][j];
+      }
+      *reinterpret_cast<uint4*>(hi + (uint64_t)r * n + 8 * g) = __builtin_bit_cast(uint4, h);
+      *reinterpret_cast<uint4*>(lo + (uint64_t)r * n + 8 * g) = __builtin_bit_cast(uint4, l);
+      // sub-block of 32 = groups 4i .. 4i+3 = four consecutive threads
+      sum = group_sum<4>(sum);
+      if ((t & 3) == 0) {
+        const _Float16 sh = (_Float16)sum;
+        shi[(uint64_t)r * (n / 32) + g / 4] = sh;
+        slo[(uint64_t)r * (n / 32) + g / 4] = (_Float16)(sum - (float)sh);
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------------------ router
+// logits[t][e] = sum_i hx[t][i] W[e][i] on the f32 matrix cores: workgroup =
+// 16 tokens x 16 experts, the four waves each take a quarter of n_embd and
+// their partial tiles are added in wave order.
+__global__ __launch_bounds__(kBlock) void k_router_batch(const float* __restrict__ hx,
+                                                         const float* __restrict__ w, int m,
+                                                         int n, int n_expert,
+                                                         float* __restrict__ logits) {
+  __shared__ float part[4][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, kq = lane >> 4;
+  const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
+  const int tok = min(t0 + r, m - 1), ex = min(e0 + r, n_expert - 1);
+  const int per = n / 16;  // contiguous k per lane
+  const float* ap = hx + (uint64_t)tok * n + wave * (n / 4) + kq * per;
+  const float* bp = w + (uint64_t)ex * n + wave * (n / 4) + kq * per;
+  f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s = 0; s < per; s += 4) {
+    const float4 a = *reinterpret_cast<const float4*>(ap + s);
+    const float4 b = *reinterpret_cast<const float4*>(bp + s);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+  }
+  // c[i] = C[token 4kq+i][expert r]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) part[wave][(4 * kq + i) * 16 + r] = c[i];
+  __syncthreads();
+  const int tt = threadIdx.x >> 4, ee = threadIdx.x & 15;
+  if (t0 + tt < m && e0 + ee < n_expert) {
+    const int q = tt * 16 + ee;
+    logits[(uint64_t)(t0 + tt) * n_expert + e0 + ee] =
+        ((part[0][q] + part[1][q]) + part[2][q]) + part[3][q];
+  }
+}
+
+// Softmax + top-k of every token: one wave per token.
+__global__ __launch_bounds__(kBlock) void k_route_batch(const float* __restrict__ logits, int m,
+                                                        int n_expert, int k,
+                                                        int32_t* __restrict__ topk_idx,
+                                                        float* __restrict__ topk_w) {
+  const int t = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+  if (t >= m) return;
+  int idx;
+  float wt;
+  wave_route(logits + (uint64_t)t * n_expert, n_expert, k, idx, wt);
+  if (lane < k) {
+    topk_idx[(uint64_t)t * k + lane] = idx;
+    topk_w[(uint64_t)t * k + lane] = wt;
+  }
+}
+
+// ------------------------------------------------------------------ bucketing
+// One workgroup: pairs (token, slot) grouped by expert.  offsets[e] is the
+// first pair of expert e (offsets[E] = m*k); pair_tok[q] the token of pair q;
+// pair_of[t*k + s] the pair of token t's slot s; items the (expert, first
+// pair) of every tile of kTok pairs.  The order of pairs within an expert does
+// not change any result: each pair's outputs depend only on its own row.
+__global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ topk_idx, int m,
+                                                   int k, int n_expert, int* __restrict__ offsets,
+                                                   int* __restrict__ pair_tok,
+                                                   int* __restrict__ pair_of,
+                                                   int2* __restrict__ items,
+                                                   int* __restrict__ n_items) {
+  __shared__ int cnt[256], off[257], cur[256], ioff[257];
+  const int t = threadIdx.x, P = m * k;
+  if (t < n_expert) cnt[t] = 0;
+  __syncthreads();
+  for (int p = t; p < P; p += kBlock) atomicAdd(&cnt[topk_idx[p]], 1);
+  __syncthreads();
+  if (t == 0) {
+    off[0] = 0;
+    ioff[0] = 0;
+    for (int e = 0; e < n_expert; ++e) {
+      off[e + 1] = off[e] + cnt[e];
+      ioff[e + 1] = ioff[e] + (cnt[e] + kTok - 1) / kTok;
+    }
+    offsets[n_expert] = off[n_expert];
+    *n_items = ioff[n_expert];
+  }
+  __syncthreads();
+  if (t < n_expert) {
+    offsets[t] = off[t];
+    cur[t] = off[t];
+    for (int i = 0; i < ioff[t + 1] - ioff[t]; ++i) items[ioff[t] + i] = make_int2(t, i * kTok);
+  }
+  __syncthreads();
+  for (int p = t; p < P; p += kBlock) {
+    const int q = atomicAdd(&cur[topk_idx[p]], 1);
+    pair_tok[q] = p / k;
+    pair_of[p] = q;
+  }
+}
+
+// ------------------------------------------------------------------ grouped expert GEMM
+struct GroupArgs {
+  const uint8_t* w0;        // [E] Q4_K slabs of n_out rows x n_in (gate, or down)
+  const uint8_t* w1;        // up slabs (gate/up only)
+  int n_in, n_out;
+  const _Float16* ah;       // A rows [rows][n_in], f16 high parts in perm8 order
+  const _Float16* al;       // f16 remainders
+  const _Float16* sh;       // [rows][n_in / 32] sub-block sums, high parts
+  const _Float16* sl;
+  const int* pair_tok;      // A row of each pair (null: the pair index itself)
+  const int* offsets;       // [E + 1]
+  const int2* items;
+  const int* n_items;
+  float* out;               // [pairs][n_out]
+};
+
+// Workgroup = one tile of kTok pairs of one expert x kRowsWG weight rows; wave
+// = 32 rows.  C[token][row] of the 32x32x16 matrix-core steps: lane l owns
+// weight row l % 32, so its row's d/dmin/scales are its own; A = the pair rows
+// (token l % 32), B = the unpacked weights.  Per 256-weight super-block: one
+// header and four 16-byte code loads per matrix, 16 steps per code group for
+// hi/lo x and the two nibble sub-blocks, one step for the min term.
+template <bool GATEUP>
+__global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
+  const int item = blockIdx.y;
+  if (item >= *a.n_items) return;
+  const int2 it = a.items[item];
+  const int e = it.x;
+  const int p0 = a.offsets[e] + it.y;
+  const int cnt = min(kTok, a.offsets[e + 1] - p0);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rbase = blockIdx.x * kRowsWG + wave * 32;
+  if (rbase >= a.n_out) return;
+  const int row = rbase + (lane & 31), kh = lane >> 5;
+  const int j = lane & 31;  // A row (token of the tile) this lane loads
+  const int pj = p0 + min(j, cnt - 1);
+  const int arow = a.pair_tok ? a.pair_tok[pj] : pj;
+  const int nsb = a.n_in >> 8;
+  const _Float16* ahp = a.ah + (uint64_t)arow * a.n_in + 16 * kh;
+  const _Float16* alp = a.al + (uint64_t)arow * a.n_in + 16 * kh;
+  const _Float16* shp = (kh ? a.sl : a.sh) + (uint64_t)arow * (a.n_in >> 5);
+  const uint64_t rb = (uint64_t)nsb * KNJ_Q4K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_out;
+  const uint8_t* wr0 = a.w0 + (uint64_t)e * slab + (uint64_t)row * rb;
+  const uint8_t* wr1 = GATEUP ? a.w1 + (uint64_t)e * slab + (uint64_t)row * rb : nullptr;
+  f32x16 acc0 = {}, acc1 = {};
+  for (int sb = 0; sb < nsb; ++sb) {
+    const uint8_t* b0 = wr0 + (uint64_t)sb * KNJ_Q4K_BLOCK;
+    const uint4 h0 = *reinterpret_cast<const uint4*>(b0);
+    uint4 c0[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      c0[g] = *reinterpret_cast<const uint4*>(b0 + KNJ_Q4K_QS + 32 * g + 16 * kh);
+    uint4 h1 = h0;
+    uint4 c1[4] = {c0[0], c0[1], c0[2], c0[3]};
+    if constexpr (GATEUP) {
+      const uint8_t* b1 = wr1 + (uint64_t)sb * KNJ_Q4K_BLOCK;
+      h1 = *reinterpret_cast<const uint4*>(b1);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        c1[g] = *reinterpret_cast<const uint4*>(b1 + KNJ_Q4K_QS + 32 * g + 16 * kh);
+    }
+    const half8 am = ld_h8(shp + 8 * sb);
+    // scales and mins of this lane's row, and the min-term step
+    auto mins_step = [&](const uint4& h, half2v* sc2, half2v* nc2, f32x16& cm) {
+      half8 bm;
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        uint32_t sc, mn;
+        q4k_scale_min(h.y, h.z, h.w, s, sc, mn);
+        const _Float16 f = (_Float16)(float)sc;
+        sc2[s] = half2v{f, f};
+        nc2[s] = half2v{(_Float16)(-1024.0f * (float)sc), (_Float16)(-1024.0f * (float)sc)};
+        bm[s] = (_Float16)(float)mn;
+      }
+      cm = mfma32(am, bm, f32x16{});
+    };
+    half2v sc0[8], nc0[8], sc1[8], nc1[8];
+    f32x16 cm0, cm1 = {};
+    mins_step(h0, sc0, nc0, cm0);
+    if constexpr (GATEUP) mins_step(h1, sc1, nc1, cm1);
+    f32x16 cq0 = {}, cq1 = {};
+    const _Float16* xh = ahp + 256 * sb;
+    const _Float16* xl = alp + 256 * sb;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const uint32_t w0a = kk ? c0[g].z : c0[g].x, w0b = kk ? c0[g].w : c0[g].y;
+        // x of sub-blocks 2g and 2g+1 at this lane's 8 positions
+        const int o = 64 * g + 8 * kk;
+        const half8 xh0 = ld_h8(xh + o), xl0 = ld_h8(xl + o);
+        const half8 xh1 = ld_h8(xh + o + 32), xl1 = ld_h8(xl + o + 32);
+        const half8 blo = q4_unpack(w0a, w0b, 0, sc0[2 * g], nc0[2 * g]);
+        const half8 bhi = q4_unpack(w0a, w0b, 4, sc0[2 * g + 1], nc0[2 * g + 1]);
+        cq0 = mfma32(xh0, blo, cq0);
+        cq0 = mfma32(xl0, blo, cq0);
+        cq0 = mfma32(xh1, bhi, cq0);
+        cq0 = mfma32(xl1, bhi, cq0);
+        if constexpr (GATEUP) {
+          const uint32_t w1a = kk ? c1[g].z : c1[g].x, w1b = kk ? c1[g].w : c1[g].y;
+          const half8 ulo = q4_unpack(w1a, w1b, 0, sc1[2 * g], nc1[2 * g]);
+          const half8 uhi = q4_unpack(w1a, w1b, 4, sc1[2 * g + 1], nc1[2 * g + 1]);
+          cq1 = mfma32(xh0, ulo, cq1);
+          cq1 = mfma32(xl0, ulo, cq1);
+          cq1 = mfma32(xh1, uhi, cq1);
+          cq1 = mfma32(xl1, uhi, cq1);
+        }
+      }
+    }
+    const float d0 = h2f(h0.x), m0 = h2f(h0.x >> 16);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc0[i] += d0 * cq0[i] - m0 * cm0[i];
+    if constexpr (GATEUP) {
+      const float d1 = h2f(h1.x), m1 = h2f(h1.x >> 16);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc1[i] += d1 * cq1[i] - m1 * cm1[i];
+    }
+  }
+  // acc[i] = C[token 8*(i/4) + 4*kh + i%4][row]
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tj = 8 * (i / 4) + 4 * kh + (i % 4);
+    if (tj < cnt) {
+      float v = acc0[i];
+      if constexpr (GATEUP) v = (v / (1.0f + expf(-v))) * acc1[i];
+      a.out[(uint64_t)(p0 + tj) * a.n_out + row] = v;
+    }
+  }
+}
+
+// ------------------------------------------------------------------ combine
+// out[t] = resid[t] + sum over token t's k slots, in ascending expert order,
+// of w * y[pair] (the scatter order of model.cpp:499-507).
+__global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
+                                                    const int* __restrict__ pair_of,
+                                                    const int32_t* __restrict__ topk_idx,
+                                                    const float* __restrict__ topk_w, int k,
+                                                    int n, const float* __restrict__ resid,
+                                                    float* __restrict__ out) {
+  const int t = blockIdx.x;
+  int ids[16], pr[16], rank[16];
+  float wt[16];
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    ids[s] = s < k ? topk_idx[(uint64_t)t * k + s] : 0x7FFFFFFF;
+    wt[s] = s < k ? topk_w[(uint64_t)t * k + s] : 0.0f;
+    pr[s] = s < k ? pair_of[(uint64_t)t * k + s] : 0;
+  }
+#pragma unroll
+  for (int s = 0; s < 16; ++s) {
+    int r = 0;
+#pragma unroll
+    for (int q = 0; q < 16; ++q) r += ids[q] < ids[s] ? 1 : 0;
+    rank[s] = r;
+  }
+  for (int i = threadIdx.x; i < n; i += kBlock) {
+    float o = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      if (r >= k) break;
+      int ps = 0;
+      float ws = 0.0f;
+#pragma unroll
+      for (int s = 0; s < 16; ++s)
+        if (rank[s] == r) {
+          ps = pr[s];
+          ws = wt[s];
+        }
+      o = __fadd_rn(o, __fmul_rn(ws, y[(uint64_t)ps * n + i]));
+    }
+    out[(uint64_t)t * n + i] = resid ? __fadd_rn(resid[(uint64_t)t * n + i], o) : o;
+  }
+}
+
+}  // namespace
+
+uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int k) {
+  const uint64_t P = (uint64_t)m * k, H = n_embd, F = n_ff;
+  const uint64_t items = (uint64_t)n_expert + (P + kTok - 1) / kTok;
+  uint64_t b = 0;
+  auto add = [&](uint64_t bytes) { b += (bytes + 255) & ~255ull; };
+  add(m * H * 4);                       // hx
+  add(m * H * 2); add(m * H * 2);       // x hi/lo
+  add(m * H / 16); add(m * H / 16);     // x sums hi/lo
+  add((n_expert + 1) * 4);              // offsets
+  add(P * 4); add(P * 4);               // pair_tok, pair_of
+  add(items * 8); add(256);             // items, n_items
+  add(P * F * 4);                       // act
+  add(P * F * 2); add(P * F * 2);       // act hi/lo
+  add(P * F / 16); add(P * F / 16);     // act sums hi/lo
+  add(P * H * 4);                       // y
+  return b;
+}
+
+hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s) {
+  const int m = a.m, H = a.n_embd, F = a.n_ff, E = a.n_expert, K = a.k;
+  const uint64_t P = (uint64_t)m * K;
+  const int max_items = E + (int)((P + kTok - 1) / kTok);
+  uint8_t* p = (uint8_t*)scratch;
+  auto take = [&](uint64_t bytes) {
+    uint8_t* q = p;
+    p += (bytes + 255) & ~255ull;
+    return q;
+  };
+  float* hx = (float*)take((uint64_t)m * H * 4);
+  _Float16* xh = (_Float16*)take((uint64_t)m * H * 2);
+  _Float16* xl = (_Float16*)take((uint64_t)m * H * 2);
+  _Float16* sxh = (_Float16*)take((uint64_t)m * H / 16);
+  _Float16* sxl = (_Float16*)take((uint64_t)m * H / 16);
+  int* offsets = (int*)take((uint64_t)(E + 1) * 4);
+  int* pair_tok = (int*)take(P * 4);
+  int* pair_of = (int*)take(P * 4);
+  int2* items = (int2*)take((uint64_t)max_items * 8);
+  int* n_items = (int*)take(256);
+  float* act = (float*)take(P * F * 4);
+  _Float16* ah = (_Float16*)take(P * F * 2);
+  _Float16* al = (_Float16*)take(P * F * 2);
+  _Float16* sah = (_Float16*)take(P * F / 16);
+  _Float16* sal = (_Float16*)take(P * F / 16);
+  float* y = (float*)take(P * H * 4);
+
+  if (a.norm_w)
+    hipLaunchKernelGGL(k_split_rows<true>, dim3(m), dim3(kBlock), 0, s, a.x, a.norm_w, a.eps, H,
+                       hx, xh, xl, sxh, sxl);
+  else
+    hipLaunchKernelGGL(k_split_rows<false>, dim3(m), dim3(kBlock), 0, s, a.x, nullptr, 0.0f, H,
+                       hx, xh, xl, sxh, sxl);
+  hipLaunchKernelGGL(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(kBlock), 0, s, hx,
+                     a.router_w, m, H, E, a.logits);
+  hipLaunchKernelGGL(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, a.logits, m, E, K,
+                     a.topk_idx, a.topk_w);
+  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
+                     pair_of, items, n_items);
+  GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, pair_tok, offsets, items, n_items, act};
+  hipLaunchKernelGGL(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+                     0, s, gu);
+  hipLaunchKernelGGL(k_split_rows<false>, dim3((unsigned)P), dim3(kBlock), 0, s, act, nullptr,
+                     0.0f, F, nullptr, ah, al, sah, sal);
+  GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, nullptr, offsets, items, n_items, y};
+  hipLaunchKernelGGL(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+                     0, s, dn);
+  hipLaunchKernelGGL(k_combine, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
+                     H, a.resid, a.out);
+  return hipGetLastError();
+}
+
+}  // namespace knj

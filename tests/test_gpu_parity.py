@@ -110,6 +110,43 @@ def test_moe_decode_layer_config1(device, type_down):
     assert rel_rmse(out.download(np.float32), out_w[0]) <= 1e-5
 
 
+@pytest.fixture(scope="module")
+def config1_weights():
+    return moe_layer_inputs()
+
+
+@pytest.mark.parametrize("m", [1, 7, 64, 512])
+def test_moe_batch_layer(device, config1_weights, m):
+    """Config 2 (m = 512) and smaller batches: the batched MoE layer against the
+    oracle's Model::moe on the same m rows (top-k bit-exact, out <= 1e-5)."""
+    n_embd, n_ff, n_expert, k = 2048, 768, 128, 8
+    say(f"moe batch layer m={m}")
+    _, router, gate, up, down = config1_weights
+    rng = np.random.default_rng(100 + m)
+    x = rng.standard_normal((m, n_embd)).astype(np.float32)
+    resid = rng.standard_normal((m, n_embd)).astype(np.float32)
+    ones = np.ones(n_embd, np.float32)
+    hx = np.stack([O.rmsnorm(x[t], ones, 1e-6) for t in range(m)])
+    out_w, logits_w, ti_w, tw_w = O.moe(hx, router, gate, up, down, n_embd, n_ff, n_expert, k)
+    d = {nm: K.DeviceBuffer.from_array(a) for nm, a in
+         dict(x=x, resid=resid, router=router, gate=gate, up=up, down=down, ones=ones).items()}
+    out = K.DeviceBuffer(4 * m * n_embd)
+    logits = K.DeviceBuffer(4 * m * n_expert)
+    ti = K.DeviceBuffer(4 * m * k)
+    tw = K.DeviceBuffer(4 * m * k)
+    K.moe_batch_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], m, n_embd, n_ff, n_expert,
+                      k, out, logits, ti, tw, norm_w=d["ones"], eps=1e-6, resid=d["resid"])
+    got_ti = ti.download(np.int32).reshape(m, k)
+    bad = np.flatnonzero((got_ti != ti_w).any(axis=1))
+    assert bad.size == 0, f"top-k differs for tokens {bad[:8]}"
+    assert rel_rmse(logits.download(np.float32), logits_w.reshape(-1)) <= 1e-5
+    assert np.allclose(tw.download(np.float32).reshape(m, k), tw_w, rtol=1e-5, atol=1e-7)
+    got = out.download(np.float32).reshape(m, n_embd) - resid
+    worst = max(rel_rmse(got[t], out_w[t]) for t in range(m))
+    say(f"  worst per-token rel-RMSE {worst:.3g}")
+    assert worst <= 1e-5
+
+
 def small_config(**kw):
     base = dict(n_layer=3, n_embd=512, n_head=8, n_head_kv=2, head_dim=64, n_ff=256,
                 n_expert=16, n_expert_used=4, n_vocab=4096, n_ctx=160)
