@@ -64,6 +64,48 @@ def expert_traffic():
         return None
 
 
+def moe_batch_leg(model: K.Model, cfg: K.ModelConfig, m: int, iters: int) -> dict:
+    """one MoE layer (the model's layer 0: router, 128 Q4_K
+    experts) over m tokens at once, x ~ N(0,1) with ffn_norm, timed with HIP
+    events over `iters` calls of knj_moe_batch_layer on the default stream."""
+    import ctypes as C
+
+    H, F, E, k = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used
+    lo = model.layer_offsets(0)
+    base = model.image_device()
+    rng = np.random.default_rng(2)
+    x = K.DeviceBuffer.from_array(rng.standard_normal((m, H)).astype(np.float32))
+    out = K.DeviceBuffer(4 * m * H)
+    logits = K.DeviceBuffer(4 * m * E)
+    ti = K.DeviceBuffer(4 * m * k)
+    tw = K.DeviceBuffer(4 * m * k)
+    ptr = lambda off: C.c_void_p(base + off)  # noqa: E731
+
+    def call():
+        K.moe_batch_layer(x, ptr(lo.router), ptr(lo.gate), ptr(lo.up), ptr(lo.down), m, H, F, E, k,
+                          out, logits, ti, tw, norm_w=ptr(lo.ffn_norm), eps=cfg.rms_eps, resid=x)
+
+    for _ in range(3):
+        call()
+    K.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        call()
+    K.synchronize()
+    us = (time.perf_counter() - t0) / iters * 1e6
+    # algorithmic work: router + 3 expert GEMMs per (token, expert) pair
+    flops = 2.0 * m * H * E + 2.0 * m * k * 3 * H * F
+    wbytes = 4 * H * E + E * (2 * K.row_bytes(cfg.type_gate_up, H) * F + K.row_bytes(cfg.type_down, F) * H)
+    log(f"config 2: MoE layer over {m} tokens in {us:.1f} us ({m / us * 1e6:.0f} tokens/s, "
+        f"{flops / us / 1e6:.1f} TFLOP/s)")
+    return {"workload": f"config 2: one MoE layer (128 Q4_K experts, top-8) over {m} tokens at once",
+            "us_per_layer": round(us, 2), "tokens_per_s": round(m / us * 1e6, 1),
+            "algorithmic_tflops": round(flops / us / 1e6, 2), "weight_bytes": wbytes,
+            "weight_GBps": round(wbytes / us / 1e3, 1),
+            "note": "expert GEMMs on f16 matrix cores with split (hi + lo) activations, two "
+                    "matrix-core steps per algorithmic product"}
+
+
 def calib_probe() -> None:
     """Two kernels whose HBM traffic is known exactly: k_gemv_bf16 over a
     2048 x 65536 bf16 matrix (268,435,456 bytes read once; x and y are 8 KiB and
@@ -135,6 +177,8 @@ def main() -> int:
                     help="also run two streaming kernels of known traffic (a 256 MiB bf16 GEMV "
                          "read, a 256 MiB f32 dequant write) to scale rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE readings")
+    ap.add_argument("--prefill-tokens", type=int, default=512,
+                    help="tokens of the config-2 batched MoE layer leg (0 skips it)")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -197,6 +241,8 @@ def main() -> int:
     if args.calib_probe:
         calib_probe()
 
+    moe_batch = moe_batch_leg(model, cfg, args.prefill_tokens, 20) if args.prefill_tokens else None
+
     result = {
         "metric": "decode tokens/s at batch 1 + achieved HBM GB/s (% of 8 TB/s) on Q4_K expert GEMV",
         "value": round(tok_s, 3),
@@ -235,6 +281,7 @@ def main() -> int:
             "frac": round(token_gbps / HBM_PEAK_GBPS, 4),
         },
         "cpu_baseline": None,
+        "moe_batch": moe_batch,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, cfg, args.cpu_budget, args.cpu_tokens)

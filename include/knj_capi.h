@@ -146,6 +146,10 @@ int knj_model_create_from_image(const knj_model_config* cfg, const void* image, 
 int knj_model_free(knj_model* m);
 uint64_t knj_model_image_bytes(const knj_model* m);
 const void* knj_model_image_device(const knj_model* m);
+/* Byte offsets of layer `il`'s tensors inside the weight image of a model of
+ * configuration `c` (the layout of knj_model.h); returns the image size, 0 on a
+ * bad argument. */
+uint64_t knj_model_layer_offsets(const knj_model_config* c, int il, knj_layer_offsets* out);
 int knj_model_download_image(const knj_model* m, void* host, uint64_t bytes);
 int knj_model_reset(knj_model* m);
 int knj_model_pos(const knj_model* m);

@@ -31,7 +31,7 @@ EXPORTS = (
     "knj_built_arch", "knj_last_error", "knj_malloc", "knj_free", "knj_memcpy_h2d",
     "knj_memcpy_d2h", "knj_memset_zero", "knj_synchronize", "knj_dequant", "knj_gemv",
     "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_moe_batch_layer", "knj_attention_step", "knj_model_create_synthetic", "knj_model_create_from_image",
-    "knj_model_free", "knj_model_image_bytes", "knj_model_image_device",
+    "knj_model_free", "knj_model_image_bytes", "knj_model_image_device", "knj_model_layer_offsets",
     "knj_model_download_image", "knj_model_reset", "knj_model_pos", "knj_model_set_pos",
     "knj_model_forward", "knj_model_decode_greedy", "knj_model_hidden", "knj_model_topk",
     "knj_model_logits", "knj_model_kv_download", "knj_model_kv_upload",
@@ -72,6 +72,12 @@ def qwen3_30b_a3b(**kw) -> ModelConfig:
                 init_std=0.02)
     base.update(kw)
     return ModelConfig(**base)
+
+
+class LayerOffsets(C.Structure):
+    """Byte offsets of one layer's tensors in the weight image (knj_layer_offsets)."""
+    _fields_ = [(n, C.c_uint64) for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm", "wqkv", "wo",
+                                           "router", "gate", "up", "down")]
 
 
 class DeviceCaps(C.Structure):
@@ -115,6 +121,7 @@ _SIGS = {
     "knj_model_free": (_i, [_P]),
     "knj_model_image_bytes": (_u64, [_P]),
     "knj_model_image_device": (_P, [_P]),
+    "knj_model_layer_offsets": (_u64, [C.POINTER(ModelConfig), _i, C.POINTER(LayerOffsets)]),
     "knj_model_download_image": (_i, [_P, _P, _u64]),
     "knj_model_reset": (_i, [_P]),
     "knj_model_pos": (_i, [_P]),
@@ -317,6 +324,16 @@ class Model:
 
     def reset(self) -> None:
         check(lib().knj_model_reset(self.h))
+
+    def image_device(self) -> int:
+        """Device address of the weight image."""
+        return lib().knj_model_image_device(self.h)
+
+    def layer_offsets(self, il: int) -> LayerOffsets:
+        lo = LayerOffsets()
+        if not lib().knj_model_layer_offsets(C.byref(self.cfg), il, C.byref(lo)):
+            raise ValueError(f"layer {il} out of range")
+        return lo
 
     def image_bytes(self) -> int:
         return lib().knj_model_image_bytes(self.h)

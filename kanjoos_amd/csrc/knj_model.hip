@@ -447,6 +447,11 @@ int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_
   return KNJ_OK;
 }
 
+uint64_t knj_model_layer_offsets(const knj_model_config* c, int il, knj_layer_offsets* out) {
+  if (!c || !out || il < 0 || il >= c->n_layer) return 0;
+  return knj_model_layout(c, il, out, nullptr, nullptr, nullptr);
+}
+
 int knj_model_decode_greedy(knj_model* m, int32_t first, int steps, int32_t* out_tokens) {
   KNJ_CHECK_ARG(m && out_tokens, "null pointer");
   KNJ_CHECK_ARG(steps > 0 && steps <= m->max_steps, "steps out of range");

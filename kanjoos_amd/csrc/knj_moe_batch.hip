@@ -61,73 +61,70 @@ __device__ __forceinline__ f32x16 mfma32(half8 a, half8 b, f32x16 c) {
 }
 
 // ------------------------------------------------------------------ operand prep
-// Row r of src (n floats, n % 256 == 0): optionally RMS-normalised with w
-// (model.cpp:240-271), then written as f32 (dst, optional), as f16 hi/lo in
-// perm8 order, and as per-32 sums split hi/lo.
-template <bool NORM>
-__global__ __launch_bounds__(kBlock) void k_split_rows(const float* __restrict__ src,
-                                                       const float* __restrict__ nw, float eps,
-                                                       int n, float* __restrict__ dst,
-                                                       _Float16* __restrict__ hi,
-                                                       _Float16* __restrict__ lo,
-                                                       _Float16* __restrict__ shi,
-                                                       _Float16* __restrict__ slo) {
+// Row r of src (n floats): RMS-normalised with w (model.cpp:240-271) into dst.
+__global__ __launch_bounds__(kBlock) void k_norm_rows(const float* __restrict__ src,
+                                                      const float* __restrict__ nw, float eps,
+                                                      int n, float* __restrict__ dst) {
+  __shared__ float xs[4096];
   __shared__ float red[8];
-  const int r = blockIdx.x, t = threadIdx.x;
-  const float* s = src + (uint64_t)r * n;
-  // 8-element groups t and t + 256 (n <= 4096)
-  float v[2][8];
+  const float* s = src + (uint64_t)blockIdx.x * n;
   float ss = 0.0f;
+  for (int i = 4 * threadIdx.x; i < n; i += 4 * kBlock) {
+    const float4 v = *reinterpret_cast<const float4*>(s + i);
+    *reinterpret_cast<float4*>(xs + i) = v;
+    ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+  }
+  ss = block_sum(ss, red);
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+  float* d = dst + (uint64_t)blockIdx.x * n;
+  for (int i = 4 * threadIdx.x; i < n; i += 4 * kBlock) {
+    const float4 v = *reinterpret_cast<const float4*>(xs + i);
+    const float4 w = *reinterpret_cast<const float4*>(nw + i);
+    *reinterpret_cast<float4*>(d + i) =
+        make_float4(v.x * scale * w.x, v.y * scale * w.y, v.z * scale * w.z, v.w * scale * w.w);
+  }
+}
+
+// The A operand of the grouped GEMM for pair p (one workgroup each): row
+// row_of[p] of src (row p when row_of is null), n floats, as f16 high parts and
+// remainders in perm8 order and as per-32 sums split the same way.  Layouts
+// interleave the pairs so that a wave's 32 pairs read one contiguous run:
+// hi/lo[(q * P + p) * 8 + j] for 8-group q; sums[((b / 8) * P + p) * 8 + b % 8]
+// for 32-sub-block b.
+__global__ __launch_bounds__(kBlock) void k_split_pairs(const float* __restrict__ src,
+                                                        const int* __restrict__ row_of, int n,
+                                                        int P, _Float16* __restrict__ hi,
+                                                        _Float16* __restrict__ lo,
+                                                        _Float16* __restrict__ shi,
+                                                        _Float16* __restrict__ slo) {
+  const int p = blockIdx.x, t = threadIdx.x;
+  const float* s = src + (uint64_t)(row_of ? row_of[p] : p) * n;
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int g = t + kBlock * q;
-    if (8 * g < n) {
+  for (int q2 = 0; q2 < 2; ++q2) {
+    const int g = t + kBlock * q2;  // 8-group (n <= 4096)
+    if (8 * g < n) {                // uniform over aligned groups of 4 threads (n % 32 == 0)
       const float4 a = *reinterpret_cast<const float4*>(s + 8 * g);
       const float4 b = *reinterpret_cast<const float4*>(s + 8 * g + 4);
-      v[q][0] = a.x; v[q][1] = a.y; v[q][2] = a.z; v[q][3] = a.w;
-      v[q][4] = b.x; v[q][5] = b.y; v[q][6] = b.z; v[q][7] = b.w;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += v[q][j] * v[q][j];
-    }
-  }
-  float scale = 1.0f;
-  if (NORM) {
-    ss = block_sum(ss, red);
-    scale = 1.0f / sqrtf(ss / (float)n + eps);
-  }
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int g = t + kBlock * q;
-    if (8 * g < n) {  // uniform over aligned groups of 4 threads (n % 32 == 0)
-      if (NORM) {
-        const float4 a = *reinterpret_cast<const float4*>(nw + 8 * g);
-        const float4 b = *reinterpret_cast<const float4*>(nw + 8 * g + 4);
-        const float w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[q][j] = v[q][j] * scale * w[j];
-      }
-      if (dst) {
-        float* d = dst + (uint64_t)r * n + 8 * g;
-        *reinterpret_cast<float4*>(d) = make_float4(v[q][0], v[q][1], v[q][2], v[q][3]);
-        *reinterpret_cast<float4*>(d + 4) = make_float4(v[q][4], v[q][5], v[q][6], v[q][7]);
-      }
+      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
       half8 h, l;
       float sum = 0.0f;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float x = v[q][perm8(j)];
+        const float x = v[perm8(j)];
         h[j] = (_Float16)x;
         l[j] = (_Float16)(x - (float)h[j]);
-        sum += v[q][j];
+        sum += v[j];
       }
-      *reinterpret_cast<uint4*>(hi + (uint64_t)r * n + 8 * g) = __builtin_bit_cast(uint4, h);
-      *reinterpret_cast<uint4*>(lo + (uint64_t)r * n + 8 * g) = __builtin_bit_cast(uint4, l);
-      // sub-block of 32 = groups 4i .. 4i+3 = four consecutive threads
-      sum = group_sum<4>(sum);
+      const uint64_t o = ((uint64_t)g * P + p) * 8;
+      *reinterpret_cast<uint4*>(hi + o) = __builtin_bit_cast(uint4, h);
+      *reinterpret_cast<uint4*>(lo + o) = __builtin_bit_cast(uint4, l);
+      sum = group_sum<4>(sum);  // sub-block g/4 = four consecutive threads
       if ((t & 3) == 0) {
+        const int sb = g / 4;
+        const uint64_t so = ((uint64_t)(sb / 8) * P + p) * 8 + sb % 8;
         const _Float16 sh = (_Float16)sum;
-        shi[(uint64_t)r * (n / 32) + g / 4] = sh;
-        slo[(uint64_t)r * (n / 32) + g / 4] = (_Float16)(sum - (float)sh);
+        shi[so] = sh;
+        slo[so] = (_Float16)(sum - (float)sh);
       }
     }
   }
@@ -233,11 +230,11 @@ struct GroupArgs {
   const uint8_t* w0;        // [E] Q4_K slabs of n_out rows x n_in (gate, or down)
   const uint8_t* w1;        // up slabs (gate/up only)
   int n_in, n_out;
-  const _Float16* ah;       // A rows [rows][n_in], f16 high parts in perm8 order
+  const _Float16* ah;       // A operand of every pair (k_split_pairs layout), high parts
   const _Float16* al;       // f16 remainders
-  const _Float16* sh;       // [rows][n_in / 32] sub-block sums, high parts
+  const _Float16* sh;       // sub-block sums, high parts
   const _Float16* sl;
-  const int* pair_tok;      // A row of each pair (null: the pair index itself)
+  int P;                    // pairs
   const int* offsets;       // [E + 1]
   const int2* items;
   const int* n_items;
@@ -262,13 +259,13 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
   const int rbase = blockIdx.x * kRowsWG + wave * 32;
   if (rbase >= a.n_out) return;
   const int row = rbase + (lane & 31), kh = lane >> 5;
-  const int j = lane & 31;  // A row (token of the tile) this lane loads
+  const int j = lane & 31;  // pair of the tile this lane loads the A operand of
   const int pj = p0 + min(j, cnt - 1);
-  const int arow = a.pair_tok ? a.pair_tok[pj] : pj;
   const int nsb = a.n_in >> 8;
-  const _Float16* ahp = a.ah + (uint64_t)arow * a.n_in + 16 * kh;
-  const _Float16* alp = a.al + (uint64_t)arow * a.n_in + 16 * kh;
-  const _Float16* shp = (kh ? a.sl : a.sh) + (uint64_t)arow * (a.n_in >> 5);
+  const uint64_t qs = (uint64_t)a.P * 8;  // halves between consecutive 8-groups
+  const _Float16* ahp = a.ah + (uint64_t)pj * 8 + 2 * kh * qs;
+  const _Float16* alp = a.al + (uint64_t)pj * 8 + 2 * kh * qs;
+  const _Float16* shp = (kh ? a.sl : a.sh) + (uint64_t)pj * 8;
   const uint64_t rb = (uint64_t)nsb * KNJ_Q4K_BLOCK;
   const uint64_t slab = rb * (uint64_t)a.n_out;
   const uint8_t* wr0 = a.w0 + (uint64_t)e * slab + (uint64_t)row * rb;
@@ -290,7 +287,7 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
       for (int g = 0; g < 4; ++g)
         c1[g] = *reinterpret_cast<const uint4*>(b1 + KNJ_Q4K_QS + 32 * g + 16 * kh);
     }
-    const half8 am = ld_h8(shp + 8 * sb);
+    const half8 am = ld_h8(shp + (uint64_t)sb * qs);
     // scales and mins of this lane's row, and the min-term step
     auto mins_step = [&](const uint4& h, half2v* sc2, half2v* nc2, f32x16& cm) {
       half8 bm;
@@ -310,17 +307,18 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
     mins_step(h0, sc0, nc0, cm0);
     if constexpr (GATEUP) mins_step(h1, sc1, nc1, cm1);
     f32x16 cq0 = {}, cq1 = {};
-    const _Float16* xh = ahp + 256 * sb;
-    const _Float16* xl = alp + 256 * sb;
+    const _Float16* xh = ahp + 32 * sb * qs;
+    const _Float16* xl = alp + 32 * sb * qs;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const uint32_t w0a = kk ? c0[g].z : c0[g].x, w0b = kk ? c0[g].w : c0[g].y;
-        // x of sub-blocks 2g and 2g+1 at this lane's 8 positions
-        const int o = 64 * g + 8 * kk;
+        // x of sub-blocks 2g and 2g+1 at this lane's 8 positions: 8-groups
+        // 32 sb + 8 g + 2 kh + kk and 4 further
+        const uint64_t o = (uint64_t)(8 * g + kk) * qs;
         const half8 xh0 = ld_h8(xh + o), xl0 = ld_h8(xl + o);
-        const half8 xh1 = ld_h8(xh + o + 32), xl1 = ld_h8(xl + o + 32);
+        const half8 xh1 = ld_h8(xh + o + 4 * qs), xl1 = ld_h8(xl + o + 4 * qs);
         const half8 blo = q4_unpack(w0a, w0b, 0, sc0[2 * g], nc0[2 * g]);
         const half8 bhi = q4_unpack(w0a, w0b, 4, sc0[2 * g + 1], nc0[2 * g + 1]);
         cq0 = mfma32(xh0, blo, cq0);
@@ -411,8 +409,8 @@ uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int 
   uint64_t b = 0;
   auto add = [&](uint64_t bytes) { b += (bytes + 255) & ~255ull; };
   add(m * H * 4);                       // hx
-  add(m * H * 2); add(m * H * 2);       // x hi/lo
-  add(m * H / 16); add(m * H / 16);     // x sums hi/lo
+  add(P * H * 2); add(P * H * 2);       // x hi/lo per pair
+  add(P * H / 16); add(P * H / 16);     // x sums hi/lo
   add((n_expert + 1) * 4);              // offsets
   add(P * 4); add(P * 4);               // pair_tok, pair_of
   add(items * 8); add(256);             // items, n_items
@@ -434,10 +432,10 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
     return q;
   };
   float* hx = (float*)take((uint64_t)m * H * 4);
-  _Float16* xh = (_Float16*)take((uint64_t)m * H * 2);
-  _Float16* xl = (_Float16*)take((uint64_t)m * H * 2);
-  _Float16* sxh = (_Float16*)take((uint64_t)m * H / 16);
-  _Float16* sxl = (_Float16*)take((uint64_t)m * H / 16);
+  _Float16* xh = (_Float16*)take(P * H * 2);
+  _Float16* xl = (_Float16*)take(P * H * 2);
+  _Float16* sxh = (_Float16*)take(P * H / 16);
+  _Float16* sxl = (_Float16*)take(P * H / 16);
   int* offsets = (int*)take((uint64_t)(E + 1) * 4);
   int* pair_tok = (int*)take(P * 4);
   int* pair_of = (int*)take(P * 4);
@@ -450,24 +448,25 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   _Float16* sal = (_Float16*)take(P * F / 16);
   float* y = (float*)take(P * H * 4);
 
-  if (a.norm_w)
-    hipLaunchKernelGGL(k_split_rows<true>, dim3(m), dim3(kBlock), 0, s, a.x, a.norm_w, a.eps, H,
-                       hx, xh, xl, sxh, sxl);
-  else
-    hipLaunchKernelGGL(k_split_rows<false>, dim3(m), dim3(kBlock), 0, s, a.x, nullptr, 0.0f, H,
-                       hx, xh, xl, sxh, sxl);
-  hipLaunchKernelGGL(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(kBlock), 0, s, hx,
+  const float* xin = a.x;
+  if (a.norm_w) {
+    hipLaunchKernelGGL(k_norm_rows, dim3(m), dim3(kBlock), 0, s, a.x, a.norm_w, a.eps, H, hx);
+    xin = hx;
+  }
+  hipLaunchKernelGGL(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(kBlock), 0, s, xin,
                      a.router_w, m, H, E, a.logits);
   hipLaunchKernelGGL(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, a.logits, m, E, K,
                      a.topk_idx, a.topk_w);
   hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
                      pair_of, items, n_items);
-  GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, pair_tok, offsets, items, n_items, act};
+  hipLaunchKernelGGL(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, xin, pair_tok, H,
+                     (int)P, xh, xl, sxh, sxl);
+  GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, (int)P, offsets, items, n_items, act};
   hipLaunchKernelGGL(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      0, s, gu);
-  hipLaunchKernelGGL(k_split_rows<false>, dim3((unsigned)P), dim3(kBlock), 0, s, act, nullptr,
-                     0.0f, F, nullptr, ah, al, sah, sal);
-  GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, nullptr, offsets, items, n_items, y};
+  hipLaunchKernelGGL(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, act, nullptr, F, (int)P,
+                     ah, al, sah, sal);
+  GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
   hipLaunchKernelGGL(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      0, s, dn);
   hipLaunchKernelGGL(k_combine, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
