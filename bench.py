@@ -106,6 +106,30 @@ def moe_batch_leg(model: K.Model, cfg: K.ModelConfig, m: int, iters: int) -> dic
                     "matrix-core steps per algorithmic product"}
 
 
+def long_ctx_leg(seed: int, ctx: int, steps: int) -> dict:
+    """the Q4_K_M-style mix (Q6_K expert down and LM head),
+    batch 1, f16 KV cache at `ctx` tokens, greedy decode timed over `steps`.  The
+    cache is filled with seeded f16 values instead of running the prefill."""
+    cfg = K.qwen3_30b_a3b(n_ctx=ctx + steps + 8, type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)
+    model = K.Model.synthetic(cfg, seed=seed)
+    model.fill_kv(ctx, seed)
+    first = int(model.decode_greedy(1, 2)[-1])
+    K.synchronize()
+    start = model.pos
+    t0 = time.perf_counter()
+    model.decode_greedy(first, steps)
+    K.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    bpt = bytes_per_token(cfg, start + (steps + 1) // 2)
+    model.close()
+    log(f"config 5: decode at context {start}: {ms:.3f} ms/token, {1e3 / ms:.1f} tok/s")
+    return {"workload": f"config 5: 48 layers, Q6_K expert down + LM head, batch 1, f16 KV at {start} "
+                        "tokens (filled with seeded values, no prefill)",
+            "tokens_per_s": round(1e3 / ms, 2), "ms_per_step": round(ms, 4), "steps": steps,
+            "bytes_per_token": bpt["total"],
+            "token_GBps": round(bpt["total"] / (ms * 1e-3) / 1e9, 1)}
+
+
 def calib_probe() -> None:
     """Two kernels whose HBM traffic is known exactly: k_gemv_bf16 over a
     2048 x 65536 bf16 matrix (268,435,456 bytes read once; x and y are 8 KiB and
@@ -179,6 +203,9 @@ def main() -> int:
                          "FETCH_SIZE/WRITE_SIZE readings")
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="tokens of the config-2 batched MoE layer leg (0 skips it)")
+    ap.add_argument("--long-ctx", type=int, default=32768,
+                    help="context of the config-5 leg (0 skips it)")
+    ap.add_argument("--long-steps", type=int, default=32)
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     ap.add_argument("--cpu-tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -285,8 +312,10 @@ def main() -> int:
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, cfg, args.cpu_budget, args.cpu_tokens)
-    print(json.dumps(result), flush=True)
     model.close()
+    if args.long_ctx:
+        result["long_context"] = long_ctx_leg(args.seed, args.long_ctx, args.long_steps)
+    print(json.dumps(result), flush=True)
     return 0
 
 

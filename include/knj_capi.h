@@ -146,6 +146,10 @@ int knj_model_create_from_image(const knj_model_config* cfg, const void* image, 
 int knj_model_free(knj_model* m);
 uint64_t knj_model_image_bytes(const knj_model* m);
 const void* knj_model_image_device(const knj_model* m);
+/* Fills cache slots [0, n_pos) of every layer with seeded f16 values ~N(0,1)
+ * and sets the position to n_pos: a long context without running its prefill
+ * (for throughput runs; the decode step's work is the same). */
+int knj_model_fill_kv(knj_model* m, int n_pos, uint64_t seed);
 /* Byte offsets of layer `il`'s tensors inside the weight image of a model of
  * configuration `c` (the layout of knj_model.h); returns the image size, 0 on a
  * bad argument. */

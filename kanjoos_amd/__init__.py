@@ -31,7 +31,7 @@ EXPORTS = (
     "knj_built_arch", "knj_last_error", "knj_malloc", "knj_free", "knj_memcpy_h2d",
     "knj_memcpy_d2h", "knj_memset_zero", "knj_synchronize", "knj_dequant", "knj_gemv",
     "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_moe_batch_layer", "knj_attention_step", "knj_model_create_synthetic", "knj_model_create_from_image",
-    "knj_model_free", "knj_model_image_bytes", "knj_model_image_device", "knj_model_layer_offsets",
+    "knj_model_free", "knj_model_image_bytes", "knj_model_image_device", "knj_model_layer_offsets", "knj_model_fill_kv",
     "knj_model_download_image", "knj_model_reset", "knj_model_pos", "knj_model_set_pos",
     "knj_model_forward", "knj_model_decode_greedy", "knj_model_hidden", "knj_model_topk",
     "knj_model_logits", "knj_model_kv_download", "knj_model_kv_upload",
@@ -122,6 +122,7 @@ _SIGS = {
     "knj_model_image_bytes": (_u64, [_P]),
     "knj_model_image_device": (_P, [_P]),
     "knj_model_layer_offsets": (_u64, [C.POINTER(ModelConfig), _i, C.POINTER(LayerOffsets)]),
+    "knj_model_fill_kv": (_i, [_P, _i, _u64]),
     "knj_model_download_image": (_i, [_P, _P, _u64]),
     "knj_model_reset": (_i, [_P]),
     "knj_model_pos": (_i, [_P]),
@@ -324,6 +325,10 @@ class Model:
 
     def reset(self) -> None:
         check(lib().knj_model_reset(self.h))
+
+    def fill_kv(self, n_pos: int, seed: int = 0) -> None:
+        """Seeded f16 values in cache slots [0, n_pos) of every layer; position = n_pos."""
+        check(lib().knj_model_fill_kv(self.h, n_pos, seed))
 
     def image_device(self) -> int:
         """Device address of the weight image."""

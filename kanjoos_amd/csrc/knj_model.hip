@@ -55,6 +55,19 @@ __global__ void k_synth_plain(uint64_t key, int type, uint64_t n, float stddev,
   else reinterpret_cast<uint16_t*>(out)[i] = knj_f32_to_f16(v);
 }
 
+// Cache slots [0, n_pos) of every (layer, kv head) row of length n_ctx * D,
+// f16 values of N(0, 1) from the seeded generator (a stand-in for a prefill's
+// keys and values; the decode step's work does not depend on them).
+__global__ void k_fill_kv(uint16_t* __restrict__ k, uint16_t* __restrict__ v, uint64_t rows,
+                          uint64_t row_elems, uint64_t n_elems, uint64_t key) {
+  const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * n_elems) return;
+  const uint64_t r = i / n_elems, c = i - r * n_elems;
+  const uint64_t o = r * row_elems + c;
+  k[o] = knj_f32_to_f16(knj_normal(key, 2 * i));
+  v[o] = knj_f32_to_f16(knj_normal(key, 2 * i + 1));
+}
+
 __global__ void k_fill_ones(float* p, uint64_t n) {
   const uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) p[i] = 1.0f;
@@ -444,6 +457,22 @@ int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_
                            m->stream));
   }
   KNJ_HIP(hipStreamSynchronize(m->stream));
+  return KNJ_OK;
+}
+
+int knj_model_fill_kv(knj_model* m, int n_pos, uint64_t seed) {
+  KNJ_CHECK_ARG(m && n_pos >= 0 && n_pos <= m->c.n_ctx, "bad arguments");
+  const knj_model_config& c = m->c;
+  const uint64_t rows = (uint64_t)c.n_layer * c.n_head_kv;
+  const uint64_t row_elems = (uint64_t)c.n_ctx * c.head_dim, n = (uint64_t)n_pos * c.head_dim;
+  const uint64_t total = rows * n;
+  if (total) {
+    hipLaunchKernelGGL(k_fill_kv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, m->stream,
+                       m->kv_k, m->kv_v, rows, row_elems, n, knj_mix64(seed ^ 0x4B56ull));
+    KNJ_HIP(hipGetLastError());
+  }
+  KNJ_HIP(hipStreamSynchronize(m->stream));
+  m->pos = n_pos;
   return KNJ_OK;
 }
 

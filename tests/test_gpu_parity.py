@@ -322,12 +322,14 @@ def _attn_ref(q, k, v, qn, kn, eps, base, pos, n_head, n_kv, D, kc, vc):
     return out, kr
 
 
-@pytest.mark.parametrize("n_head,n_kv,D", [(32, 4, 128), (16, 2, 64), (12, 4, 128), (8, 8, 64)])
-@pytest.mark.parametrize("pos", [0, 63, 64, 130, 199])
-def test_attention_step(device, n_head, n_kv, D, pos):
-    """knj_attention_step against a float64 reference: cache append and output."""
-    say(f"attention n_head={n_head} n_kv={n_kv} D={D} pos={pos}")
-    n_ctx, eps, base = 200, 1e-6, 1e6
+@pytest.mark.parametrize("n_head,n_kv,D,pos,n_ctx", [
+    (nh, nkv, d, p, 200) for (nh, nkv, d) in [(32, 4, 128), (16, 2, 64), (12, 4, 128), (8, 8, 64)]
+    for p in [0, 63, 64, 130, 199]] + [(32, 4, 128, 20000, 32768), (32, 4, 128, 32767, 32768)])
+def test_attention_step(device, n_head, n_kv, D, pos, n_ctx):
+    """knj_attention_step against a float64 reference: cache append and output
+    (the last two cases are config 5's 32K context)."""
+    say(f"attention n_head={n_head} n_kv={n_kv} D={D} pos={pos} n_ctx={n_ctx}")
+    eps, base = 1e-6, 1e6
     rng = np.random.default_rng(1000 * pos + D + n_head)
     q = rng.standard_normal(n_head * D).astype(np.float32)
     k = rng.standard_normal(n_kv * D).astype(np.float32)
