@@ -150,6 +150,29 @@ const void* knj_model_image_device(const knj_model* m);
  * and sets the position to n_pos: a long context without running its prefill
  * (for throughput runs; the decode step's work is the same). */
 int knj_model_fill_kv(knj_model* m, int n_pos, uint64_t seed);
+/* ------------------------------------------------------------ batched decode (config 4)
+ * A knj_batch decodes n_seq sequences in lockstep on one model's weights (the
+ * model must outlive it): one step is Model::forward's per-token work
+ * (model.cpp:512-672) for n_seq tokens at once, each sequence with its own f16
+ * KV cache of n_ctx slots (n_ctx <= the model's) and its own position.  Every
+ * weight matrix is read once per step for all sequences (matrix-core GEMMs;
+ * the MoE pairs grouped by expert).  Q4_K attention and experts, bf16 head.
+ * knj_batch_forward: one step on tokens[n_seq]; logits_out [n_seq][n_vocab]
+ *   (may be NULL).  knj_batch_decode_greedy: `steps` greedy steps from
+ *   first[n_seq]; out_tokens [steps][n_seq].  Hidden states, top-k and caches
+ *   of the last step per sequence as for knj_model_*.  No counterpart in the
+ *   reference, which decodes one sequence. */
+typedef struct knj_batch knj_batch;
+int knj_batch_create(knj_model* m, int n_seq, int n_ctx, knj_batch** out);
+int knj_batch_free(knj_batch* b);
+int knj_batch_pos(const knj_batch* b);
+int knj_batch_forward(knj_batch* b, const int32_t* tokens, float* logits_out);
+int knj_batch_decode_greedy(knj_batch* b, const int32_t* first, int steps, int32_t* out_tokens);
+int knj_batch_fill_kv(knj_batch* b, int n_pos, uint64_t seed);
+int knj_batch_hidden(const knj_batch* b, int il, int seq, float* out);
+int knj_batch_topk(const knj_batch* b, int il, int seq, int32_t* idx, float* w);
+int knj_batch_kv_download(const knj_batch* b, int seq, uint16_t* k, uint16_t* v);
+
 /* Byte offsets of layer `il`'s tensors inside the weight image of a model of
  * configuration `c` (the layout of knj_model.h); returns the image size, 0 on a
  * bad argument. */

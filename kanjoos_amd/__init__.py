@@ -36,6 +36,9 @@ EXPORTS = (
     "knj_model_forward", "knj_model_decode_greedy", "knj_model_hidden", "knj_model_topk",
     "knj_model_logits", "knj_model_kv_download", "knj_model_kv_upload",
     "knj_model_time_decode", "knj_model_time_experts",
+    "knj_batch_create", "knj_batch_free", "knj_batch_pos", "knj_batch_forward",
+    "knj_batch_decode_greedy", "knj_batch_fill_kv", "knj_batch_hidden", "knj_batch_topk",
+    "knj_batch_kv_download",
 )
 
 
@@ -136,6 +139,15 @@ _SIGS = {
     "knj_model_kv_upload": (_i, [_P, _P, _P]),
     "knj_model_time_decode": (_i, [_P, _i, C.POINTER(_f)]),
     "knj_model_time_experts": (_i, [_P, _i, C.POINTER(_f), C.POINTER(_f)]),
+    "knj_batch_create": (_i, [_P, _i, _i, C.POINTER(_P)]),
+    "knj_batch_free": (_i, [_P]),
+    "knj_batch_pos": (_i, [_P]),
+    "knj_batch_forward": (_i, [_P, _P, _P]),
+    "knj_batch_decode_greedy": (_i, [_P, _P, _i, _P]),
+    "knj_batch_fill_kv": (_i, [_P, _i, _u64]),
+    "knj_batch_hidden": (_i, [_P, _i, _i, _P]),
+    "knj_batch_topk": (_i, [_P, _i, _i, _P, _P]),
+    "knj_batch_kv_download": (_i, [_P, _i, _P, _P]),
 }
 
 _lib = None
@@ -405,3 +417,66 @@ class Model:
         a, b = C.c_float(), C.c_float()
         check(lib().knj_model_time_experts(self.h, steps, C.byref(a), C.byref(b)))
         return a.value, b.value
+
+
+class Batch:
+    """n_seq sequences decoded in lockstep on a Model's weights (knj_batch_*);
+    the model must stay open while the batch is used."""
+
+    def __init__(self, model: "Model", n_seq: int, n_ctx: int):
+        self.model = model
+        self.cfg = model.cfg
+        self.n_seq = n_seq
+        self.n_ctx = n_ctx
+        h = _P()
+        check(lib().knj_batch_create(model.h, n_seq, n_ctx, C.byref(h)))
+        self.h = h.value
+
+    def close(self) -> None:
+        if self.h:
+            lib().knj_batch_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def pos(self) -> int:
+        return lib().knj_batch_pos(self.h)
+
+    def forward(self, tokens) -> np.ndarray:
+        t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(self.n_seq))
+        out = np.empty((self.n_seq, self.cfg.n_vocab), dtype=np.float32)
+        check(lib().knj_batch_forward(self.h, _ptr(t), _ptr(out)))
+        return out
+
+    def decode_greedy(self, first, steps: int) -> np.ndarray:
+        f = np.ascontiguousarray(np.asarray(first, dtype=np.int32).reshape(self.n_seq))
+        out = np.empty((steps, self.n_seq), dtype=np.int32)
+        check(lib().knj_batch_decode_greedy(self.h, _ptr(f), steps, _ptr(out)))
+        return out
+
+    def fill_kv(self, n_pos: int, seed: int = 0) -> None:
+        check(lib().knj_batch_fill_kv(self.h, n_pos, seed))
+
+    def hidden(self, il: int, seq: int) -> np.ndarray:
+        out = np.empty(self.cfg.n_embd, dtype=np.float32)
+        check(lib().knj_batch_hidden(self.h, il, seq, _ptr(out)))
+        return out
+
+    def topk(self, il: int, seq: int):
+        k = self.cfg.n_expert_used
+        i = np.empty(k, dtype=np.int32)
+        w = np.empty(k, dtype=np.float32)
+        check(lib().knj_batch_topk(self.h, il, seq, _ptr(i), _ptr(w)))
+        return i, w
+
+    def kv_download(self, seq: int):
+        shape = (self.cfg.n_layer, self.cfg.n_head_kv, self.n_ctx, self.cfg.head_dim)
+        k = np.empty(shape, dtype=np.uint16)
+        v = np.empty(shape, dtype=np.uint16)
+        check(lib().knj_batch_kv_download(self.h, seq, _ptr(k), _ptr(v)))
+        return k, v

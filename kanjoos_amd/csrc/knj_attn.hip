@@ -81,9 +81,16 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   KNJ_STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int p0 = split * kChunk;
-  uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
-  uint16_t* vc = a.v_cache + (uint64_t)kvh * a.n_ctx * D;
-  float* part = a.partial + ((uint64_t)(kvh * G) * n_split + split) * (D + 2);
+  const int z = blockIdx.z;  // sequence
+  uint16_t* kc = a.k_cache + z * a.kv_stride + (uint64_t)kvh * a.n_ctx * D;
+  uint16_t* vc = a.v_cache + z * a.kv_stride + (uint64_t)kvh * a.n_ctx * D;
+  float* part = a.partial + (uint64_t)z * a.n_head * n_split * (D + 2) +
+                ((uint64_t)(kvh * G) * n_split + split) * (D + 2);
+  const float* qz = a.q + z * a.qkv_stride;
+  const float* kz = a.k + z * a.qkv_stride;
+  const float* vz = a.v + z * a.qkv_stride;
+  const float* rc = a.rope_cos + (uint64_t)z * a.rope_stride;
+  const float* rs = a.rope_sin + (uint64_t)z * a.rope_stride;
   const uint64_t hstride = (uint64_t)n_split * (D + 2);
   // 1) every load that does not depend on the position first: this chunk's
   // cache slots (16 bytes per load; rows past the valid length are dropped
@@ -106,15 +113,15 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
     ld(3, k3, v3);
   }
   const int qh = min(tid / T, G - 1), qc = tid % T;
-  const float4 qraw = *reinterpret_cast<const float4*>(a.q + (uint64_t)(kvh * G + qh) * D + 4 * qc);
+  const float4 qraw = *reinterpret_cast<const float4*>(qz + (uint64_t)(kvh * G + qh) * D + 4 * qc);
   const float4 qnw = *reinterpret_cast<const float4*>(a.q_norm + 4 * qc);
-  const float4 kraw = *reinterpret_cast<const float4*>(a.k + (uint64_t)kvh * D + 4 * qc);
-  const float4 vraw = *reinterpret_cast<const float4*>(a.v + (uint64_t)kvh * D + 4 * qc);
+  const float4 kraw = *reinterpret_cast<const float4*>(kz + (uint64_t)kvh * D + 4 * qc);
+  const float4 vraw = *reinterpret_cast<const float4*>(vz + (uint64_t)kvh * D + 4 * qc);
   const float4 knw = *reinterpret_cast<const float4*>(a.k_norm + 4 * qc);
   const int ri = (qc < T / 2) ? 4 * qc : 4 * qc - D / 2;  // rotation index of element 4qc
-  const float4 cs = *reinterpret_cast<const float4*>(a.rope_cos + ri);
-  const float4 sn = *reinterpret_cast<const float4*>(a.rope_sin + ri);
-  const int pos = *a.pos;
+  const float4 cs = *reinterpret_cast<const float4*>(rc + ri);
+  const float4 sn = *reinterpret_cast<const float4*>(rs + ri);
+  const int pos = a.pos[z];
   const int n_kv = pos + 1;
   const int cnt = min(kChunk, n_kv - p0);
   KNJ_STAMP(1);
@@ -262,8 +269,8 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
   __shared__ float fs[1024];
   __shared__ float red[8];
   __shared__ float parts[kBlock];
-  const int h = blockIdx.x, tid = threadIdx.x;
-  const float* ph = a.partial + (uint64_t)h * n_split * (D + 2);
+  const int h = blockIdx.x, tid = threadIdx.x, z = blockIdx.y;
+  const float* ph = a.partial + ((uint64_t)z * a.n_head + h) * n_split * (D + 2);
   const int d = tid % D, pt = tid / D;
   const int per = (n_split + NP - 1) / NP;
   const int s0 = pt * per, s1 = min(n_split, s0 + per);
@@ -312,7 +319,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
   if (tid < D) {
     float o = parts[tid];
     for (int q = 1; q < NP; ++q) o += parts[tid + q * D];
-    a.out[(uint64_t)h * D + tid] = o / L;
+    a.out[z * a.out_stride + (uint64_t)h * D + tid] = o / L;
   }
 }
 
@@ -323,12 +330,13 @@ int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   const int n_split = attn_splits(a.n_ctx);
   if (n_split > 1024) return hipErrorInvalidValue;
+  const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
-    hipLaunchKernelGGL(k_attention<128>, dim3(a.n_head_kv, n_split), dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_head), dim3(kBlock), 0, s, a, n_split);
+    hipLaunchKernelGGL(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
-    hipLaunchKernelGGL(k_attention<64>, dim3(a.n_head_kv, n_split), dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(k_attn_merge<64>, dim3(a.n_head), dim3(kBlock), 0, s, a, n_split);
+    hipLaunchKernelGGL(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_attn_merge<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
     return hipErrorInvalidValue;
   }

@@ -125,9 +125,22 @@ struct MoeBatchArgs {
   float* logits;           // [m][n_expert]
   int32_t* topk_idx;       // [m][k], selection order
   float* topk_w;           // [m][k]
+  float* hidden_copy = nullptr;  // optional second destination of out
 };
 uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int k);
 hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s);
+
+// Dense GEMMs over m rows at once (the batched decode step), on the matrix
+// cores with split-f16 (Q4_K) or split-bf16 (bf16 weights) activations:
+// out[r] (+= resid[r]) = W x_r.  Scratch: dense_scratch_bytes(m, n_in).
+uint64_t dense_scratch_bytes(int m, int n_in);
+hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, int n, float* out,
+                            hipStream_t s);
+hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const float* x,
+                            const float* resid, float* out, void* scratch, hipStream_t s);
+hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, const float* x,
+                             float* out, void* scratch, hipStream_t s);
+hipError_t launch_argmax_rows(const float* logits, int m, int n, int32_t* tok, hipStream_t s);
 
 // Fused decode attention of one token (QK-norm, RoPE, f16 append, split-KV
 // attention, merge).  q/k/v are the raw projections of this token.
@@ -145,8 +158,14 @@ struct AttnArgs {
   uint16_t* v_cache;
   int n_head, n_head_kv, head_dim, n_ctx;
   float scale;
-  float* partial;            // [n_head][n_split][D + 2] scratch
+  float* partial;            // [n_seq][n_head][n_split][D + 2] scratch
   float* out;                // [n_head][D]
+  // Several sequences in one launch (grid z = sequence): sequence s reads
+  // q/k/v + s * qkv_stride, rope rows + s * rope_stride, its position pos[s],
+  // the caches + s * kv_stride, and writes out + s * out_stride.
+  int n_seq = 1;
+  uint64_t qkv_stride = 0, kv_stride = 0, out_stride = 0;
+  int rope_stride = 0;
 };
 int attn_splits(int n_ctx);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);

@@ -22,6 +22,7 @@
 
 #include "../../include/knj_synth.h"
 #include "knj_common.h"
+#include "knj_model_impl.h"
 
 namespace knj {
 namespace {
@@ -74,36 +75,21 @@ __global__ void k_fill_ones(float* p, uint64_t n) {
 }
 
 }  // namespace
+
+int fill_kv_rows(uint16_t* k, uint16_t* v, uint64_t rows, uint64_t row_elems, uint64_t n_elems,
+                 uint64_t seed, hipStream_t s) {
+  const uint64_t total = rows * n_elems;
+  if (!total) return KNJ_OK;
+  hipLaunchKernelGGL(k_fill_kv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, k, v, rows,
+                     row_elems, n_elems, knj_mix64(seed ^ 0x4B56ull));
+  KNJ_HIP(hipGetLastError());
+  return KNJ_OK;
+}
+
 }  // namespace knj
 
 using namespace knj;
 
-struct knj_model {
-  knj_model_config c{};
-  uint8_t* image = nullptr;
-  uint64_t image_bytes = 0;
-  std::vector<knj_layer_offsets> lo;
-  uint64_t off_embd = 0, off_onorm = 0, off_head = 0;
-  hipStream_t stream = nullptr;
-  // activations
-  float *x = nullptr, *qkv = nullptr, *ctx = nullptr, *hx = nullptr, *act = nullptr;
-  float *logits = nullptr, *router_logits = nullptr, *hidden = nullptr, *topk_w = nullptr;
-  int32_t* topk_idx = nullptr;
-  float *rope_cos = nullptr, *rope_sin = nullptr, *rope_cur = nullptr, *attn_part = nullptr;
-  uint16_t *kv_k = nullptr, *kv_v = nullptr;
-  StepState* st = nullptr;
-  int32_t* out_tokens = nullptr;
-  unsigned long long* keys = nullptr;  // LM-head per-workgroup argmax keys
-  int max_steps = 0;
-  unsigned int* counter = nullptr;
-  int pos = 0;
-  hipGraph_t graph = nullptr;
-  hipGraphExec_t exec = nullptr;
-  bool use_graph = true;  // KNJ_NO_GRAPH=1 launches the step's kernels directly
-  hipEvent_t* expert_events = nullptr;  // set by knj_model_time_experts: 4 per layer per step
-  int expert_slot = 0;
-  std::vector<void*> owned;
-};
 
 namespace {
 
@@ -463,14 +449,9 @@ int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_
 int knj_model_fill_kv(knj_model* m, int n_pos, uint64_t seed) {
   KNJ_CHECK_ARG(m && n_pos >= 0 && n_pos <= m->c.n_ctx, "bad arguments");
   const knj_model_config& c = m->c;
-  const uint64_t rows = (uint64_t)c.n_layer * c.n_head_kv;
-  const uint64_t row_elems = (uint64_t)c.n_ctx * c.head_dim, n = (uint64_t)n_pos * c.head_dim;
-  const uint64_t total = rows * n;
-  if (total) {
-    hipLaunchKernelGGL(k_fill_kv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, m->stream,
-                       m->kv_k, m->kv_v, rows, row_elems, n, knj_mix64(seed ^ 0x4B56ull));
-    KNJ_HIP(hipGetLastError());
-  }
+  int rc = fill_kv_rows(m->kv_k, m->kv_v, (uint64_t)c.n_layer * c.n_head_kv,
+                        (uint64_t)c.n_ctx * c.head_dim, (uint64_t)n_pos * c.head_dim, seed, m->stream);
+  if (rc) return rc;
   KNJ_HIP(hipStreamSynchronize(m->stream));
   m->pos = n_pos;
   return KNJ_OK;

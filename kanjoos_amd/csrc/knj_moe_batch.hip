@@ -225,6 +225,19 @@ __global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ t
   }
 }
 
+// Work list of a dense GEMM over m rows seen as one expert: offsets {0, m} in
+// meta[0..1], the tile count in meta[2], tile t = (0, 32 t) at meta + 64.
+__global__ void k_dense_meta(int m, int* meta) {
+  const int tiles = (m + kTok - 1) / kTok;
+  if (threadIdx.x == 0) {
+    meta[0] = 0;
+    meta[1] = m;
+    meta[2] = tiles;
+  }
+  int2* items = reinterpret_cast<int2*>(meta + 64);
+  for (int t = threadIdx.x; t < tiles; t += blockDim.x) items[t] = make_int2(0, t * kTok);
+}
+
 // ------------------------------------------------------------------ grouped expert GEMM
 struct GroupArgs {
   const uint8_t* w0;        // [E] Q4_K slabs of n_out rows x n_in (gate, or down)
@@ -239,6 +252,7 @@ struct GroupArgs {
   const int2* items;
   const int* n_items;
   float* out;               // [pairs][n_out]
+  const float* resid = nullptr;  // optional [pairs][n_out] added to out (may alias out)
 };
 
 // Workgroup = one tile of kTok pairs of one expert x kRowsWG weight rows; wave
@@ -352,8 +366,106 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
     if (tj < cnt) {
       float v = acc0[i];
       if constexpr (GATEUP) v = (v / (1.0f + expf(-v))) * acc1[i];
-      a.out[(uint64_t)(p0 + tj) * a.n_out + row] = v;
+      const uint64_t o = (uint64_t)(p0 + tj) * a.n_out + row;
+      a.out[o] = a.resid ? a.resid[o] + v : v;
     }
+  }
+}
+
+// ------------------------------------------------------------------ bf16 weights (LM head)
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+// Row p of src (n floats) as three bf16 parts x = hi + mid + lo (24
+// significant bits), natural order, pairs interleaved: part[(q * P + p) * 8 + j].
+__global__ __launch_bounds__(kBlock) void k_split_bf16x3(const float* __restrict__ src, int n,
+                                                         int P, uint16_t* __restrict__ hi,
+                                                         uint16_t* __restrict__ mid,
+                                                         uint16_t* __restrict__ lo) {
+  const int p = blockIdx.x;
+  const float* s = src + (uint64_t)p * n;
+  for (int g = threadIdx.x; 8 * g < n; g += kBlock) {
+    uint16_t h[8], md[8], l[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = s[8 * g + j];
+      h[j] = knj_f32_to_bf16(x);
+      const float r1 = x - knj_bf16_to_f32(h[j]);
+      md[j] = knj_f32_to_bf16(r1);
+      l[j] = knj_f32_to_bf16(r1 - knj_bf16_to_f32(md[j]));
+    }
+    const uint64_t o = ((uint64_t)g * P + p) * 8;
+    *reinterpret_cast<uint4*>(hi + o) = *reinterpret_cast<const uint4*>(h);
+    *reinterpret_cast<uint4*>(mid + o) = *reinterpret_cast<const uint4*>(md);
+    *reinterpret_cast<uint4*>(lo + o) = *reinterpret_cast<const uint4*>(l);
+  }
+}
+
+__device__ __forceinline__ bf16x8 ld_b8(const uint16_t* p) {
+  return __builtin_bit_cast(bf16x8, *reinterpret_cast<const uint4*>(p));
+}
+
+// out[p][row] = W[row] . x_p for bf16 W [n_out][n_in] and tiles of 32 pairs
+// (blockIdx.y = tile): workgroup = 128 rows, wave = 32, lane l owns row l % 32;
+// three 32x32x16 bf16 matrix-core steps per 16 weights (x hi, mid, lo).
+__global__ __launch_bounds__(kBlock) void k_dense_bf16(const uint16_t* __restrict__ w, int n_in,
+                                                       int n_out, int P,
+                                                       const uint16_t* __restrict__ xh,
+                                                       const uint16_t* __restrict__ xm,
+                                                       const uint16_t* __restrict__ xl,
+                                                       float* __restrict__ out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rbase = blockIdx.x * kRowsWG + wave * 32;
+  if (rbase >= n_out) return;
+  const int row = min(rbase + (lane & 31), n_out - 1), kh = lane >> 5;
+  const int p0 = blockIdx.y * kTok, cnt = min(kTok, P - p0);
+  const int pj = p0 + min(lane & 31, cnt - 1);
+  const uint64_t qs = (uint64_t)P * 8;
+  const uint16_t* wr = w + (uint64_t)row * n_in + 8 * kh;
+  const uint64_t xo = (uint64_t)pj * 8 + kh * qs;
+  f32x16 acc = {};
+  for (int k0 = 0; k0 < n_in; k0 += 64) {
+    bf16x8 b[4], ah[4], am[4], al[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      b[u] = ld_b8(wr + k0 + 16 * u);
+      const uint64_t q = (uint64_t)((k0 + 16 * u) / 8) * qs + xo;
+      ah[u] = ld_b8(xh + q);
+      am[u] = ld_b8(xm + q);
+      al[u] = ld_b8(xl + q);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah[u], b[u], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(am[u], b[u], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al[u], b[u], acc, 0, 0, 0);
+    }
+  }
+  if (rbase + (lane & 31) >= n_out) return;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tj = 8 * (i / 4) + 4 * kh + (i % 4);
+    if (tj < cnt) out[(uint64_t)(p0 + tj) * n_out + row] = acc[i];
+  }
+}
+
+// Greedy token of each row of logits [m][n] (first maximum wins): one
+// workgroup per row.
+__global__ __launch_bounds__(kBlock) void k_argmax_rows(const float* __restrict__ logits, int n,
+                                                        int32_t* __restrict__ tok) {
+  const float* r = logits + (uint64_t)blockIdx.x * n;
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < n; i += kBlock) {
+    const unsigned long long k = argmax_key(r[i], i);
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  __shared__ unsigned long long wb[kBlock / 64];
+  if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = best;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int q = 1; q < kBlock / 64; ++q) best = wb[q] > best ? wb[q] : best;
+    best = wb[0] > best ? wb[0] : best;
+    tok[blockIdx.x] = argmax_index(best);
   }
 }
 
@@ -471,6 +583,72 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
                      0, s, dn);
   hipLaunchKernelGGL(k_combine, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
                      H, a.resid, a.out);
+  hipError_t e = hipGetLastError();
+  if (e == hipSuccess && a.hidden_copy)
+    e = hipMemcpyAsync(a.hidden_copy, a.out, (uint64_t)m * H * 4, hipMemcpyDeviceToDevice, s);
+  return e;
+}
+
+// ---- dense batched GEMMs of the batched decode step
+uint64_t dense_scratch_bytes(int m, int n_in) {
+  const uint64_t P = (uint64_t)m;
+  return 4 * ((P * n_in * 2 + 255) & ~255ull) + 2 * ((P * n_in / 16 + 255) & ~255ull) + 1024;
+}
+
+hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, int n, float* out,
+                            hipStream_t s) {
+  if (n > 4096 || n % 256) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_norm_rows, dim3(m), dim3(kBlock), 0, s, x, nw, eps, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const float* x,
+                            const float* resid, float* out, void* scratch, hipStream_t s) {
+  if (n_in > 4096 || n_in % 256 || n_out % 32 || m > 1024) return hipErrorInvalidValue;
+  const uint64_t P = (uint64_t)m;
+  uint8_t* p = (uint8_t*)scratch;
+  auto take = [&](uint64_t bytes) {
+    uint8_t* q = p;
+    p += (bytes + 255) & ~255ull;
+    return q;
+  };
+  _Float16* xh = (_Float16*)take(P * n_in * 2);
+  _Float16* xl = (_Float16*)take(P * n_in * 2);
+  _Float16* sh = (_Float16*)take(P * n_in / 16);
+  _Float16* sl = (_Float16*)take(P * n_in / 16);
+  int* meta = (int*)take(1024);  // offsets {0, m}, n_items, items
+  hipLaunchKernelGGL(k_split_pairs, dim3(m), dim3(kBlock), 0, s, x, nullptr, n_in, m, xh, xl, sh,
+                     sl);
+  hipLaunchKernelGGL(k_dense_meta, dim3(1), dim3(64), 0, s, m, meta);
+  GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, meta, (const int2*)(meta + 64), meta + 2,
+              out, resid};
+  const int tiles = (m + kTok - 1) / kTok;
+  hipLaunchKernelGGL(k_group_q4k<false>, dim3((n_out + kRowsWG - 1) / kRowsWG, tiles),
+                     dim3(kBlock), 0, s, g);
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, const float* x,
+                             float* out, void* scratch, hipStream_t s) {
+  if (n_in % 64) return hipErrorInvalidValue;
+  const uint64_t P = (uint64_t)m;
+  uint8_t* p = (uint8_t*)scratch;
+  auto take = [&](uint64_t bytes) {
+    uint8_t* q = p;
+    p += (bytes + 255) & ~255ull;
+    return q;
+  };
+  uint16_t* xh = (uint16_t*)take(P * n_in * 2);
+  uint16_t* xm = (uint16_t*)take(P * n_in * 2);
+  uint16_t* xl = (uint16_t*)take(P * n_in * 2);
+  hipLaunchKernelGGL(k_split_bf16x3, dim3(m), dim3(kBlock), 0, s, x, n_in, m, xh, xm, xl);
+  hipLaunchKernelGGL(k_dense_bf16, dim3((n_out + kRowsWG - 1) / kRowsWG, (m + kTok - 1) / kTok),
+                     dim3(kBlock), 0, s, w, n_in, n_out, m, xh, xm, xl, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_argmax_rows(const float* logits, int m, int n, int32_t* tok, hipStream_t s) {
+  hipLaunchKernelGGL(k_argmax_rows, dim3(m), dim3(kBlock), 0, s, logits, n, tok);
   return hipGetLastError();
 }
 

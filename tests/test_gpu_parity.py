@@ -358,3 +358,61 @@ def test_attention_step(device, n_head, n_kv, D, pos, n_ctx):
     # output against the reference over the cache as the device wrote it
     ref_out, _ = _attn_ref(q, k, v, qn, kn, eps, base, pos, n_head, n_kv, D, got_kc, got_vc)
     assert rel_rmse(out, ref_out) <= 1e-5
+
+
+def test_batch_decode_parity(device):
+    """Config 4's batched step on a small model: three sequences with different
+    prompts stepped together; every step, every sequence against its own oracle
+    model (per-layer hidden <= 1e-5, top-k exact, logits <= 1e-5), with the same
+    f16 KV adoption as the single-sequence parity test."""
+    cfg = small_config()
+    n_ctx = cfg["n_ctx"]
+    gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    img = gm.download_image()
+    B = 3
+    batch = K.Batch(gm, B, n_ctx)
+    oms = [O.OracleModel(O.make_config(**cfg), seed=SEED, image=img) for _ in range(B)]
+    prompts = np.array([[1, 2, 3, 4], [7, 5, 3, 1], [100, 200, 300, 400]], dtype=np.int32)
+    toks = prompts
+    for step in range(prompts.shape[1] + 3):
+        col = toks[:, step] if step < prompts.shape[1] else nxt
+        lg = batch.forward(col)
+        for s_ in range(B):
+            kg, vg = batch.kv_download(s_)
+            oms[s_].set_kv_source(kg, vg)
+            lw = oms[s_].forward([int(col[s_])])
+            st = oms[s_].kv_stats()
+            assert st["max_mid_dist"] <= 1e-5, (step, s_, st)
+            for il in range(cfg["n_layer"]):
+                e = rel_rmse(batch.hidden(il, s_), oms[s_].hidden(il))
+                assert e <= 1e-5, (step, s_, il, e)
+                assert list(batch.topk(il, s_)[0]) == list(oms[s_].topk(il)[0]), (step, s_, il)
+            assert rel_rmse(lg[s_], lw) <= 1e-5, (step, s_)
+        nxt = lg.argmax(axis=1).astype(np.int32)
+    say(f"batched step parity over {B} sequences, {prompts.shape[1] + 3} steps")
+    for om in oms:
+        om.close()
+    batch.close()
+    gm.close()
+
+
+def test_batch_greedy_matches_single(device):
+    """The batched greedy loop and the single-sequence loop give the same tokens
+    for every sequence (small model, 24 steps)."""
+    cfg = small_config()
+    gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    B, steps = 4, 24
+    prompts = np.array([[1, 2, 3], [9, 8, 7], [11, 12, 13], [3, 2, 1]], dtype=np.int32)
+    batch = K.Batch(gm, B, cfg["n_ctx"])
+    for j in range(prompts.shape[1]):
+        lg = batch.forward(prompts[:, j])
+    first = lg.argmax(axis=1).astype(np.int32)
+    got = batch.decode_greedy(first, steps - 1)
+    batch.close()
+    for s_ in range(B):
+        gm.reset()
+        f = int(np.argmax(gm.forward(prompts[s_])))
+        want = [f] + list(gm.decode_greedy(f, steps - 1))
+        have = [int(first[s_])] + [int(t) for t in got[:, s_]]
+        assert have == want, (s_, have, want)
+    gm.close()
