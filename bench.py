@@ -130,6 +130,27 @@ def long_ctx_leg(seed: int, ctx: int, steps: int) -> dict:
             "token_GBps": round(bpt["total"] / (ms * 1e-3) / 1e9, 1)}
 
 
+def batch_leg(model: K.Model, seed: int, n_seq: int, ctx: int, steps: int) -> dict:
+    """n_seq concurrent greedy sequences on the same weights,
+    each with its own f16 KV cache at `ctx` tokens (filled with seeded values
+    instead of a prefill), `steps` lockstep decode steps timed."""
+    batch = K.Batch(model, n_seq, ctx + steps + 8)
+    batch.fill_kv(ctx, seed)
+    first = np.arange(1, n_seq + 1, dtype=np.int32)
+    first = batch.decode_greedy(first, 2)[-1]
+    K.synchronize()
+    t0 = time.perf_counter()
+    batch.decode_greedy(first, steps)
+    K.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    batch.close()
+    log(f"config 4: {n_seq} sequences at context {ctx}: {ms:.3f} ms/step, "
+        f"{n_seq * 1e3 / ms:.0f} tokens/s")
+    return {"workload": f"config 4: {n_seq} concurrent greedy sequences, f16 KV at {ctx} tokens each "
+                        "(filled with seeded values, no prefill), lockstep decode",
+            "tokens_per_s": round(n_seq * 1e3 / ms, 1), "ms_per_step": round(ms, 4), "steps": steps}
+
+
 def calib_probe() -> None:
     """Two kernels whose HBM traffic is known exactly: k_gemv_bf16 over a
     2048 x 65536 bf16 matrix (268,435,456 bytes read once; x and y are 8 KiB and
@@ -203,6 +224,10 @@ def main() -> int:
                          "FETCH_SIZE/WRITE_SIZE readings")
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="tokens of the config-2 batched MoE layer leg (0 skips it)")
+    ap.add_argument("--batch-seqs", type=int, default=32,
+                    help="sequences of the config-4 leg (0 skips it)")
+    ap.add_argument("--batch-ctx", type=int, default=2048)
+    ap.add_argument("--batch-steps", type=int, default=16)
     ap.add_argument("--long-ctx", type=int, default=32768,
                     help="context of the config-5 leg (0 skips it)")
     ap.add_argument("--long-steps", type=int, default=32)
@@ -269,6 +294,9 @@ def main() -> int:
         calib_probe()
 
     moe_batch = moe_batch_leg(model, cfg, args.prefill_tokens, 20) if args.prefill_tokens else None
+    batched = None
+    if args.batch_seqs and args.batch_ctx + args.batch_steps + 8 <= n_ctx:
+        batched = batch_leg(model, args.seed, args.batch_seqs, args.batch_ctx, args.batch_steps)
 
     result = {
         "metric": "decode tokens/s at batch 1 + achieved HBM GB/s (% of 8 TB/s) on Q4_K expert GEMV",
@@ -309,6 +337,7 @@ def main() -> int:
         },
         "cpu_baseline": None,
         "moe_batch": moe_batch,
+        "batched_decode": batched,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, cfg, args.cpu_budget, args.cpu_tokens)
