@@ -258,107 +258,161 @@ struct GroupArgs {
 // Workgroup = one tile of kTok pairs of one expert x kRowsWG weight rows; wave
 // = 32 rows.  C[token][row] of the 32x32x16 matrix-core steps: lane l owns
 // weight row l % 32, so its row's d/dmin/scales are its own; A = the pair rows
-// (token l % 32), B = the unpacked weights.  Per 256-weight super-block: one
-// header and four 16-byte code loads per matrix, 16 steps per code group for
-// hi/lo x and the two nibble sub-blocks, one step for the min term.
+// (token l % 32), B = the unpacked weights.  Per 256-weight super-block the
+// workgroup stages the tile's A operand (32 pairs x 256 x hi/lo, and the
+// sub-block sums) in LDS once for its four waves; the next super-block's A and
+// this lane's next weight block are loaded while the current one is computed
+// (double-buffered LDS, one barrier per super-block).  Per code group: 8 steps
+// per matrix (hi/lo x and the two nibble sub-blocks x 2); one min-term step
+// per matrix per super-block.
+constexpr int kQStride = 33;                   // uint4 per 8-group row of 32 pairs (+1 pad)
+constexpr int kPart = 32 * kQStride;           // uint4 per hi (or lo) part of a super-block
+constexpr int kBuf = 2 * kPart + 64;           // + the sums (hi 32, lo 32)
+constexpr size_t kGroupLds = 2 * kBuf * 16;    // double-buffered bytes
+
+struct WBlock {
+  uint4 h, c[4];
+};
+
 template <bool GATEUP>
 __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
+  extern __shared__ uint4 lds[];
   const int item = blockIdx.y;
-  if (item >= *a.n_items) return;
+  if (item >= *a.n_items) return;  // uniform over the workgroup
   const int2 it = a.items[item];
   const int e = it.x;
   const int p0 = a.offsets[e] + it.y;
   const int cnt = min(kTok, a.offsets[e + 1] - p0);
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int rbase = blockIdx.x * kRowsWG + wave * 32;
-  if (rbase >= a.n_out) return;
-  const int row = rbase + (lane & 31), kh = lane >> 5;
-  const int j = lane & 31;  // pair of the tile this lane loads the A operand of
-  const int pj = p0 + min(j, cnt - 1);
+  const bool rows_ok = rbase < a.n_out;  // waves past the last row still stage and sync
+  const int row = min(rbase + (lane & 31), a.n_out - 1), kh = lane >> 5;
+  const int j = lane & 31;
   const int nsb = a.n_in >> 8;
-  const uint64_t qs = (uint64_t)a.P * 8;  // halves between consecutive 8-groups
-  const _Float16* ahp = a.ah + (uint64_t)pj * 8 + 2 * kh * qs;
-  const _Float16* alp = a.al + (uint64_t)pj * 8 + 2 * kh * qs;
-  const _Float16* shp = (kh ? a.sl : a.sh) + (uint64_t)pj * 8;
+  const uint64_t P = (uint64_t)a.P;
   const uint64_t rb = (uint64_t)nsb * KNJ_Q4K_BLOCK;
   const uint64_t slab = rb * (uint64_t)a.n_out;
   const uint8_t* wr0 = a.w0 + (uint64_t)e * slab + (uint64_t)row * rb;
-  const uint8_t* wr1 = GATEUP ? a.w1 + (uint64_t)e * slab + (uint64_t)row * rb : nullptr;
+  const uint8_t* wr1 = GATEUP ? a.w1 + (uint64_t)e * slab + (uint64_t)row * rb : wr0;
+  // staging: thread t copies uint4 idx = t + 256 u (u < 8) of the hi/lo parts
+  // and, for t < 64, one sums uint4
+  auto a_src = [&](int sb, int u) -> const uint4* {
+    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
+    const _Float16* base = part ? a.al : a.ah;
+    return reinterpret_cast<const uint4*>(base + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8);
+  };
+  auto a_dst = [&](int buf, int u) -> uint4* {
+    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
+    return lds + buf * kBuf + part * kPart + q * kQStride + jj;
+  };
+  auto s_src = [&](int sb) -> const uint4* {  // threads >= 64 read a copy they do not store
+    const _Float16* base = ((t >> 5) & 1) ? a.sl : a.sh;
+    return reinterpret_cast<const uint4*>(base + ((uint64_t)sb * P + p0 + min(t & 31, cnt - 1)) * 8);
+  };
+  auto w_load = [&](const uint8_t* wr, int sb, WBlock& w) {
+    const uint8_t* b = wr + (uint64_t)sb * KNJ_Q4K_BLOCK;
+    w.h = *reinterpret_cast<const uint4*>(b);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) w.c[g] = *reinterpret_cast<const uint4*>(b + KNJ_Q4K_QS + 32 * g + 16 * kh);
+  };
+  // (the staging registers are loaded and stored on every iteration, without
+  // branches: an array live across divergent code is placed in scratch)
+  uint4 st[8], ss;
+  WBlock w0c, w1c, w0n, w1n;
+  // prologue: super-block 0
+#pragma unroll
+  for (int u = 0; u < 8; ++u) st[u] = *a_src(0, u);
+  ss = *s_src(0);
+  w_load(wr0, 0, w0c);
+  if constexpr (GATEUP) w_load(wr1, 0, w1c);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) *a_dst(0, u) = st[u];
+  if (t < 64) lds[2 * kPart + t] = ss;
+  __syncthreads();
   f32x16 acc0 = {}, acc1 = {};
   for (int sb = 0; sb < nsb; ++sb) {
-    const uint8_t* b0 = wr0 + (uint64_t)sb * KNJ_Q4K_BLOCK;
-    const uint4 h0 = *reinterpret_cast<const uint4*>(b0);
-    uint4 c0[4];
+    const int buf = sb & 1;
+    const int nx = min(sb + 1, nsb - 1);  // the last iteration reloads its own block, unused
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      c0[g] = *reinterpret_cast<const uint4*>(b0 + KNJ_Q4K_QS + 32 * g + 16 * kh);
-    uint4 h1 = h0;
-    uint4 c1[4] = {c0[0], c0[1], c0[2], c0[3]};
-    if constexpr (GATEUP) {
-      const uint8_t* b1 = wr1 + (uint64_t)sb * KNJ_Q4K_BLOCK;
-      h1 = *reinterpret_cast<const uint4*>(b1);
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        c1[g] = *reinterpret_cast<const uint4*>(b1 + KNJ_Q4K_QS + 32 * g + 16 * kh);
-    }
-    const half8 am = ld_h8(shp + (uint64_t)sb * qs);
+    for (int u = 0; u < 8; ++u) st[u] = *a_src(nx, u);
+    ss = *s_src(nx);
+    w_load(wr0, nx, w0n);
+    if constexpr (GATEUP) w_load(wr1, nx, w1n);
+    const uint4* L = lds + buf * kBuf;
+    const half8 am = __builtin_bit_cast(half8, L[2 * kPart + kh * 32 + j]);
     // scales and mins of this lane's row, and the min-term step
-    auto mins_step = [&](const uint4& h, half2v* sc2, half2v* nc2, f32x16& cm) {
+    auto prep = [&](const uint4& h, half2v* sc2, half2v* nc2, f32x16& cm) {
       half8 bm;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
+      for (int s2 = 0; s2 < 8; ++s2) {
         uint32_t sc, mn;
-        q4k_scale_min(h.y, h.z, h.w, s, sc, mn);
+        q4k_scale_min(h.y, h.z, h.w, s2, sc, mn);
         const _Float16 f = (_Float16)(float)sc;
-        sc2[s] = half2v{f, f};
-        nc2[s] = half2v{(_Float16)(-1024.0f * (float)sc), (_Float16)(-1024.0f * (float)sc)};
-        bm[s] = (_Float16)(float)mn;
+        const _Float16 nf = (_Float16)(-1024.0f * (float)sc);
+        sc2[s2] = half2v{f, f};
+        nc2[s2] = half2v{nf, nf};
+        bm[s2] = (_Float16)(float)mn;
       }
       cm = mfma32(am, bm, f32x16{});
     };
     half2v sc0[8], nc0[8], sc1[8], nc1[8];
     f32x16 cm0, cm1 = {};
-    mins_step(h0, sc0, nc0, cm0);
-    if constexpr (GATEUP) mins_step(h1, sc1, nc1, cm1);
-    f32x16 cq0 = {}, cq1 = {};
-    const _Float16* xh = ahp + 32 * sb * qs;
-    const _Float16* xl = alp + 32 * sb * qs;
+    prep(w0c.h, sc0, nc0, cm0);
+    if constexpr (GATEUP) prep(w1c.h, sc1, nc1, cm1);
+    f32x16 cqa = {}, cqb = {};  // gate (or even groups), up (or odd groups)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const uint32_t w0a = kk ? c0[g].z : c0[g].x, w0b = kk ? c0[g].w : c0[g].y;
-        // x of sub-blocks 2g and 2g+1 at this lane's 8 positions: 8-groups
-        // 32 sb + 8 g + 2 kh + kk and 4 further
-        const uint64_t o = (uint64_t)(8 * g + kk) * qs;
-        const half8 xh0 = ld_h8(xh + o), xl0 = ld_h8(xl + o);
-        const half8 xh1 = ld_h8(xh + o + 4 * qs), xl1 = ld_h8(xl + o + 4 * qs);
+        const int q = 8 * g + 2 * kh + kk;
+        const half8 xh0 = __builtin_bit_cast(half8, L[q * kQStride + j]);
+        const half8 xl0 = __builtin_bit_cast(half8, L[kPart + q * kQStride + j]);
+        const half8 xh1 = __builtin_bit_cast(half8, L[(q + 4) * kQStride + j]);
+        const half8 xl1 = __builtin_bit_cast(half8, L[kPart + (q + 4) * kQStride + j]);
+        const uint32_t w0a = kk ? w0c.c[g].z : w0c.c[g].x, w0b = kk ? w0c.c[g].w : w0c.c[g].y;
         const half8 blo = q4_unpack(w0a, w0b, 0, sc0[2 * g], nc0[2 * g]);
         const half8 bhi = q4_unpack(w0a, w0b, 4, sc0[2 * g + 1], nc0[2 * g + 1]);
-        cq0 = mfma32(xh0, blo, cq0);
-        cq0 = mfma32(xl0, blo, cq0);
-        cq0 = mfma32(xh1, bhi, cq0);
-        cq0 = mfma32(xl1, bhi, cq0);
         if constexpr (GATEUP) {
-          const uint32_t w1a = kk ? c1[g].z : c1[g].x, w1b = kk ? c1[g].w : c1[g].y;
+          cqa = mfma32(xh0, blo, cqa);
+          cqa = mfma32(xl0, blo, cqa);
+          cqa = mfma32(xh1, bhi, cqa);
+          cqa = mfma32(xl1, bhi, cqa);
+          const uint32_t w1a = kk ? w1c.c[g].z : w1c.c[g].x, w1b = kk ? w1c.c[g].w : w1c.c[g].y;
           const half8 ulo = q4_unpack(w1a, w1b, 0, sc1[2 * g], nc1[2 * g]);
           const half8 uhi = q4_unpack(w1a, w1b, 4, sc1[2 * g + 1], nc1[2 * g + 1]);
-          cq1 = mfma32(xh0, ulo, cq1);
-          cq1 = mfma32(xl0, ulo, cq1);
-          cq1 = mfma32(xh1, uhi, cq1);
-          cq1 = mfma32(xl1, uhi, cq1);
+          cqb = mfma32(xh0, ulo, cqb);
+          cqb = mfma32(xl0, ulo, cqb);
+          cqb = mfma32(xh1, uhi, cqb);
+          cqb = mfma32(xl1, uhi, cqb);
+        } else {
+          // one matrix: two accumulation chains (low and high nibble sub-blocks)
+          cqa = mfma32(xh0, blo, cqa);
+          cqb = mfma32(xh1, bhi, cqb);
+          cqa = mfma32(xl0, blo, cqa);
+          cqb = mfma32(xl1, bhi, cqb);
         }
       }
     }
-    const float d0 = h2f(h0.x), m0 = h2f(h0.x >> 16);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) acc0[i] += d0 * cq0[i] - m0 * cm0[i];
+    const float d0 = h2f(w0c.h.x), m0 = h2f(w0c.h.x >> 16);
     if constexpr (GATEUP) {
-      const float d1 = h2f(h1.x), m1 = h2f(h1.x >> 16);
+      const float d1 = h2f(w1c.h.x), m1 = h2f(w1c.h.x >> 16);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc1[i] += d1 * cq1[i] - m1 * cm1[i];
+      for (int i = 0; i < 16; ++i) {
+        acc0[i] += d0 * cqa[i] - m0 * cm0[i];
+        acc1[i] += d1 * cqb[i] - m1 * cm1[i];
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) acc0[i] += d0 * (cqa[i] + cqb[i]) - m0 * cm0[i];
     }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) *a_dst(buf ^ 1, u) = st[u];
+    if (t < 64) lds[(buf ^ 1) * kBuf + 2 * kPart + t] = ss;
+    w0c = w0n;
+    if constexpr (GATEUP) w1c = w1n;
+    __syncthreads();
   }
+  if (!rows_ok || rbase + (lane & 31) >= a.n_out) return;
   // acc[i] = C[token 8*(i/4) + 4*kh + i%4][row]
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -533,7 +587,21 @@ uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int 
   return b;
 }
 
+// The grouped kernels use more than the default 64 KB of dynamic LDS.
+hipError_t group_lds_attr() {
+  static hipError_t e = [] {
+    hipError_t r = hipFuncSetAttribute((const void*)k_group_q4k<true>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGroupLds);
+    if (r == hipSuccess)
+      r = hipFuncSetAttribute((const void*)k_group_q4k<false>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGroupLds);
+    return r;
+  }();
+  return e;
+}
+
 hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s) {
+  if (hipError_t e = group_lds_attr()) return e;
   const int m = a.m, H = a.n_embd, F = a.n_ff, E = a.n_expert, K = a.k;
   const uint64_t P = (uint64_t)m * K;
   const int max_items = E + (int)((P + kTok - 1) / kTok);
@@ -575,12 +643,12 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
                      (int)P, xh, xl, sxh, sxl);
   GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, (int)P, offsets, items, n_items, act};
   hipLaunchKernelGGL(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
-                     0, s, gu);
+                     kGroupLds, s, gu);
   hipLaunchKernelGGL(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, act, nullptr, F, (int)P,
                      ah, al, sah, sal);
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
   hipLaunchKernelGGL(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
-                     0, s, dn);
+                     kGroupLds, s, dn);
   hipLaunchKernelGGL(k_combine, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
                      H, a.resid, a.out);
   hipError_t e = hipGetLastError();
@@ -604,6 +672,7 @@ hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, i
 
 hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const float* x,
                             const float* resid, float* out, void* scratch, hipStream_t s) {
+  if (hipError_t e = group_lds_attr()) return e;
   if (n_in > 4096 || n_in % 256 || n_out % 32 || m > 1024) return hipErrorInvalidValue;
   const uint64_t P = (uint64_t)m;
   uint8_t* p = (uint8_t*)scratch;
@@ -624,7 +693,7 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
               out, resid};
   const int tiles = (m + kTok - 1) / kTok;
   hipLaunchKernelGGL(k_group_q4k<false>, dim3((n_out + kRowsWG - 1) / kRowsWG, tiles),
-                     dim3(kBlock), 0, s, g);
+                     dim3(kBlock), kGroupLds, s, g);
   return hipGetLastError();
 }
 
