@@ -76,6 +76,7 @@ struct knj_batch {
   int32_t *topk_idx = nullptr, *tokens = nullptr, *next = nullptr, *dpos = nullptr;
   int32_t* out_tokens = nullptr;
   int* step = nullptr;
+  unsigned long long* keys = nullptr;  // argmax partial keys
   uint16_t *kv_k = nullptr, *kv_v = nullptr;
   void* scratch = nullptr;
   hipGraph_t graph = nullptr;
@@ -138,7 +139,7 @@ int enqueue_batch_step(knj_batch* b, hipStream_t s) {
                            H, b->hx, s));
   KNJ_HIP(launch_dense_bf16(reinterpret_cast<const uint16_t*>(img + m->off_head), H, c.n_vocab, B,
                             b->hx, b->logits, b->scratch, s));
-  KNJ_HIP(launch_argmax_rows(b->logits, B, c.n_vocab, b->next, s));
+  KNJ_HIP(launch_argmax_rows(b->logits, B, c.n_vocab, b->keys, b->next, s));
   hipLaunchKernelGGL(k_batch_close, dim3(1), dim3(std::max(64, (B + 63) / 64 * 64)), 0, s, B,
                      b->next, b->tokens, b->dpos, b->step, b->out_tokens, b->max_steps);
   KNJ_HIP(hipGetLastError());
@@ -235,6 +236,7 @@ int knj_batch_create(knj_model* m, int n_seq, int n_ctx, knj_batch** out) {
   A((void**)&b->dpos, (uint64_t)B * 4);
   A((void**)&b->out_tokens, (uint64_t)b->max_steps * B * 4);
   A((void**)&b->step, 256);
+  A((void**)&b->keys, (uint64_t)B * argmax_key_count(c.n_vocab) * 8);
   const uint64_t kv = (uint64_t)B * L * c.n_head_kv * n_ctx * D * 2;
   A((void**)&b->kv_k, kv);
   A((void**)&b->kv_v, kv);

@@ -140,7 +140,10 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
                             const float* resid, float* out, void* scratch, hipStream_t s);
 hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, const float* x,
                              float* out, void* scratch, hipStream_t s);
-hipError_t launch_argmax_rows(const float* logits, int m, int n, int32_t* tok, hipStream_t s);
+// Greedy token of every row of logits [m][n]; keys: m * argmax_key_count(n) scratch.
+int argmax_key_count(int n);
+hipError_t launch_argmax_rows(const float* logits, int m, int n, unsigned long long* keys,
+                              int32_t* tok, hipStream_t s);
 
 // Fused decode attention of one token (QK-norm, RoPE, f16 append, split-KV
 // attention, merge).  q/k/v are the raw projections of this token.

@@ -421,6 +421,65 @@ __device__ __forceinline__ float q6k_quarter(const uint8_t* __restrict__ blk, in
   return d * ((float)sc[0] * s0 + (float)sc[1] * s1);
 }
 
+// A Q6_K "unit": quarter-octet o (0..3) of half hf of one block -- weights
+// 128 hf + 32 t + 8 o + i (t, i < 4, 8): ql bytes 64 hf + 8 o (quarters 0, 2)
+// and 64 hf + 32 + 8 o (quarters 1, 3), qh bytes 32 hf + 8 o, the scales of
+// sub-group o/2 of each quarter and d (dequant_q6_k, dequant.cpp:164-191).
+// Q6_K blocks are 210 bytes, so these runs are only 2-byte aligned: each is
+// read as three aligned words and shifted into place.
+struct Q6Unit {
+  uint32_t l0a, l0b, l1a, l1b, ha, hb;  // ql run 0, ql run 1, qh run (8 bytes each)
+  int32_t sc[4];                        // the quarters' scales
+  uint32_t d;                           // f16 bits of d
+};
+
+__device__ __forceinline__ void ld8_u2(const uint8_t* p, uint32_t& a, uint32_t& b) {
+  const uintptr_t addr = reinterpret_cast<uintptr_t>(p);
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(addr & ~(uintptr_t)3);
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+  const uint32_t sh = (uint32_t)(addr & 3) * 8;
+  a = sh ? __builtin_amdgcn_alignbit(w1, w0, sh) : w0;
+  b = sh ? __builtin_amdgcn_alignbit(w2, w1, sh) : w1;
+}
+
+__device__ __forceinline__ Q6Unit q6_unit_load(const uint8_t* __restrict__ blk, int hf, int o) {
+  Q6Unit u;
+  ld8_u2(blk + KNJ_Q6K_QL + 64 * hf + 8 * o, u.l0a, u.l0b);
+  ld8_u2(blk + KNJ_Q6K_QL + 64 * hf + 32 + 8 * o, u.l1a, u.l1b);
+  ld8_u2(blk + KNJ_Q6K_QH + 32 * hf + 8 * o, u.ha, u.hb);
+  // (scales and d by narrow loads, which stay inside the block)
+  const int8_t* sp = reinterpret_cast<const int8_t*>(blk + KNJ_Q6K_SC + 8 * hf + (o >> 1));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) u.sc[t] = sp[2 * t];
+  u.d = *reinterpret_cast<const uint16_t*>(blk + KNJ_Q6K_D);
+  return u;
+}
+
+// sum over the unit's 32 weights of w*x = d * sum_t sc_t * (sum_i q x - 32 sum_i x),
+// with x8[t] the unit's 8 x of quarter t and sx[t] their sum.
+__device__ __forceinline__ float q6_unit_dot(const Q6Unit& u, const float4 (&x8)[4][2],
+                                             const float (&sx)[4]) {
+  float r = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const uint32_t la = (t & 1) ? u.l1a : u.l0a, lb = (t & 1) ? u.l1b : u.l0b;
+    const int ns = (t >> 1) * 4;
+    const uint32_t qa = ((la >> ns) & 0x0F0F0F0Fu) | (((u.ha >> (2 * t)) & 0x03030303u) << 4);
+    const uint32_t qb = ((lb >> ns) & 0x0F0F0F0Fu) | (((u.hb >> (2 * t)) & 0x03030303u) << 4);
+    float acc = 0.0f;
+    acc += (float)((qa >> 0) & 0xFFu) * x8[t][0].x;
+    acc += (float)((qa >> 8) & 0xFFu) * x8[t][0].y;
+    acc += (float)((qa >> 16) & 0xFFu) * x8[t][0].z;
+    acc += (float)(qa >> 24) * x8[t][0].w;
+    acc += (float)((qb >> 0) & 0xFFu) * x8[t][1].x;
+    acc += (float)((qb >> 8) & 0xFFu) * x8[t][1].y;
+    acc += (float)((qb >> 16) & 0xFFu) * x8[t][1].z;
+    acc += (float)(qb >> 24) * x8[t][1].w;
+    r += (float)u.sc[t] * (acc - 32.0f * sx[t]);
+  }
+  return h2f(u.d) * r;
+}
+
 __device__ __forceinline__ unsigned long long argmax_key(float v, int idx) {
   uint32_t u = __float_as_uint(v);
   u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);

@@ -114,6 +114,69 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4k_wide(const uint8_t* __restr
   }
 }
 
+// Q6_K rows of n_in <= 2048 (at most 64 units of 32 weights): lane = unit, so
+// every lane's x (32 values and 4 run sums) is the same for every row and
+// stays in registers; RS rows per wave step, all their loads issued first;
+// rows walked grid-stride (the argmax variant keeps the grid <= kMaxKeys).
+template <int RS>
+__global__ __launch_bounds__(kBlock) void k_gemv_q6k_u(const uint8_t* __restrict__ w, int n_in,
+                                                       int n_out, const float* __restrict__ x,
+                                                       const float* __restrict__ nw, float eps,
+                                                       const float* __restrict__ resid,
+                                                       float* __restrict__ y,
+                                                       unsigned long long* argmax) {
+  __shared__ float xs[xpad_size(2048)];
+  __shared__ float xs8[256];
+  __shared__ float red[8];
+  stage_x(x, nw, eps, n_in, xs, red);
+  for (int g = threadIdx.x; 8 * g < n_in; g += kBlock) {
+    const float4 a = *reinterpret_cast<const float4*>(xs + xpad(8 * g));
+    const float4 b = *reinterpret_cast<const float4*>(xs + xpad(8 * g) + 4);
+    xs8[g] = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+  }
+  __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nb = n_in / KNJ_QK, nunits = 8 * nb;
+  const bool active = lane < nunits;
+  const int u = active ? lane : 0;
+  const int b = u >> 3, hf = (u >> 2) & 1, o = u & 3;
+  float4 x8[4][2];
+  float sx[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int i = 256 * b + 128 * hf + 32 * t + 8 * o;
+    x8[t][0] = *reinterpret_cast<const float4*>(xs + xpad(i));
+    x8[t][1] = *reinterpret_cast<const float4*>(xs + xpad(i) + 4);
+    sx[t] = xs8[i >> 3];
+  }
+  const uint64_t rb = (uint64_t)nb * KNJ_Q6K_BLOCK;
+  const uint8_t* wu = w + (uint64_t)b * KNJ_Q6K_BLOCK;
+  unsigned long long best = 0;
+  const int stride = gridDim.x * (kBlock / 64) * RS;
+  for (int r0 = (blockIdx.x * (kBlock / 64) + wave) * RS; r0 < n_out; r0 += stride) {
+    Q6Unit q[RS];
+#pragma unroll
+    for (int st = 0; st < RS; ++st) q[st] = q6_unit_load(wu + (uint64_t)min(r0 + st, n_out - 1) * rb, hf, o);
+    float rv[RS];
+#pragma unroll
+    for (int st = 0; st < RS; ++st) rv[st] = resid ? resid[min(r0 + st, n_out - 1)] : 0.0f;
+#pragma unroll
+    for (int st = 0; st < RS; ++st) {
+      const float acc = group_sum<64>(active ? q6_unit_dot(q[st], x8, sx) : 0.0f);
+      const int row = r0 + st;
+      if (lane == 0 && row < n_out) {
+        const float v = resid ? rv[st] + acc : acc;
+        y[row] = v;
+        if (argmax) {
+          const unsigned long long k = argmax_key(v, row);
+          best = k > best ? k : best;
+        }
+      }
+    }
+  }
+  if (argmax) block_argmax_store(best, argmax);
+}
+
 // Q6_K rows: 8 quarters per block, LPR lanes per row, activations in LDS.
 template <int LPR>
 __global__ __launch_bounds__(kBlock) void k_gemv_q6k(const uint8_t* __restrict__ w, int n_in,
@@ -376,6 +439,10 @@ int pow2_at_least(int v) {
 
 // Grids of the argmax-capable GEMVs (Q6_K, BF16, F32); one key per workgroup.
 int gemv_grid(int type, int n_in, int n_out) {
+  if (type == KNJ_TYPE_Q6_K && n_in <= 2048) {
+    constexpr int RS = 4;
+    return std::max(1, std::min(2048, (n_out + 4 * RS - 1) / (4 * RS)));
+  }
   if (type == KNJ_TYPE_Q6_K) {
     const int lpr = std::min(64, pow2_at_least(8 * (n_in / KNJ_QK)));
     const int rows_per_block = 4 * (64 / lpr);
@@ -413,6 +480,11 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
     const int grid = std::max(1, std::min(2048, (a.n_out + 3) / 4));
     hipLaunchKernelGGL(k_gemv_q4k_wide, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, a.x,
                        a.norm_w, a.eps, a.resid, a.y);
+    return hipGetLastError();
+  }
+  if (a.type == KNJ_TYPE_Q6_K && a.n_in <= 2048) {
+    hipLaunchKernelGGL(k_gemv_q6k_u<4>, dim3(gemv_grid(a.type, a.n_in, a.n_out)), dim3(kBlock), 0, s,
+                       a.w, a.n_in, a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
     return hipGetLastError();
   }
   if (a.type == KNJ_TYPE_Q6_K) {

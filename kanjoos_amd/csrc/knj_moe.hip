@@ -487,6 +487,115 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   KNJ_STAMP(12);
 }
 
+// ------------------------------------------------------------------ down (Q6_K, n_ff <= 1024)
+// Wave = one output row for all k experts: 32-lane group gi takes expert slots
+// gi, gi+2, ..; lane = one 32-weight Q6_K unit of the row (n_ff / 32 <= 32
+// units).  The k activation vectors and their 8-run sums are staged in LDS once
+// per workgroup; slots are folded in ascending expert order as in the Q4_K
+// kernel.
+template <int KPG>
+__global__ __launch_bounds__(kBlock) void k_expert_down_q6u(ExpertArgs a) {
+  extern __shared__ float acts[];  // [k][n_ff], then [k * n_ff / 8] run sums
+  constexpr int KMAX = 2 * KPG;    // k <= KMAX
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int gi = lane >> 5, u = lane & 31;
+  const int F = a.n_ff, K = a.k, n = K * F;
+  float* s8 = acts + n;
+  const int nunits = F / 32;
+  const bool active = u < nunits;
+  const int uu = active ? u : 0;
+  const int b = uu >> 3, hf = (uu >> 2) & 1, o = uu & 3;
+  const uint64_t rb = (uint64_t)(F / KNJ_QK) * KNJ_Q6K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_embd;
+  const int row = min((int)(blockIdx.x * (kBlock / 64) + wave), a.n_embd - 1);
+  const bool row_ok = (int)(blockIdx.x * (kBlock / 64) + wave) < a.n_embd;
+  int ids[KMAX];
+  float wts[KMAX];
+#pragma unroll
+  for (int kk = 0; kk < KMAX; ++kk) {
+    ids[kk] = kk < K ? a.topk_idx[kk] : 0x7FFFFFFF;
+    wts[kk] = kk < K ? a.topk_w[kk] : 0.0f;
+  }
+  const float resid = a.resid ? a.resid[row] : 0.0f;
+  // activations first (their staging waits only for them), 8 loads in flight
+  // per thread per round; then the weights
+  for (int base = 4 * threadIdx.x; base < n; base += 32 * kBlock) {
+    float4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = base + 4 * kBlock * j;
+      v[j] = *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = base + 4 * kBlock * j;
+      if (i < n) *reinterpret_cast<float4*>(acts + i) = v[j];
+    }
+  }
+  Q6Unit q[KPG];
+#pragma unroll
+  for (int j = 0; j < KPG; ++j) {
+    const int kk = min(gi + 2 * j, K - 1);
+    int e = ids[0];
+#pragma unroll
+    for (int t = 1; t < KMAX; ++t) e = kk == t ? ids[t] : e;
+    q[j] = q6_unit_load(a.down + (uint64_t)e * slab + (uint64_t)row * rb + (uint64_t)b * KNJ_Q6K_BLOCK,
+                        hf, o);
+  }
+  __syncthreads();
+  for (int g = threadIdx.x; 8 * g < n; g += kBlock) {
+    const float4 x0 = *reinterpret_cast<const float4*>(acts + 8 * g);
+    const float4 x1 = *reinterpret_cast<const float4*>(acts + 8 * g + 4);
+    s8[g] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
+  }
+  int rank[KMAX];
+#pragma unroll
+  for (int kk = 0; kk < KMAX; ++kk) {
+    int r = 0;
+#pragma unroll
+    for (int t = 0; t < KMAX; ++t) r += ids[t] < ids[kk] ? 1 : 0;
+    rank[kk] = r;
+  }
+  __syncthreads();
+  float dot[KPG];
+#pragma unroll
+  for (int j = 0; j < KPG; ++j) {
+    const int kk = min(gi + 2 * j, K - 1);
+    float4 x8[4][2];
+    float sx[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int i = kk * F + 256 * b + 128 * hf + 32 * t + 8 * o;
+      x8[t][0] = *reinterpret_cast<const float4*>(acts + i);
+      x8[t][1] = *reinterpret_cast<const float4*>(acts + i + 4);
+      sx[t] = s8[i >> 3];
+    }
+    const float acc = (active && gi + 2 * j < K) ? q6_unit_dot(q[j], x8, sx) : 0.0f;
+    dot[j] = group_sum<32>(acc);
+  }
+  // every lane folds the k products in ascending expert order (slot kk's
+  // product is in lane 32 (kk % 2), register kk / 2)
+  float dk[KMAX];
+#pragma unroll
+  for (int kk = 0; kk < KMAX; ++kk) dk[kk] = lane_bcast(dot[kk / 2], 32 * (kk % 2));
+  float o_ = 0.0f;
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    float wr = 0.0f, dr = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < KMAX; ++kk) {
+      const bool hit = rank[kk] == r;
+      wr = hit ? wts[kk] : wr;
+      dr = hit ? dk[kk] : dr;
+    }
+    if (r < K) o_ = __fadd_rn(o_, __fmul_rn(wr, dr));
+  }
+  if (!row_ok || lane != 0) return;
+  const float v = a.resid ? __fadd_rn(resid, o_) : o_;
+  a.out[row] = v;
+  if (a.hidden_copy) a.hidden_copy[row] = v;
+}
+
 // ------------------------------------------------------------------ down (Q6_K)
 // Tasks (expert slot, row), LPR lanes each over the 8 quarters per block.
 template <int LPR>
@@ -604,6 +713,21 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
     return hipErrorInvalidValue;
   }
   if (a.type_down != KNJ_TYPE_Q6_K) return hipErrorInvalidValue;
+  if (a.n_ff <= 1024 && a.k <= 16) {
+    const int kpg = (a.k + 1) / 2;
+    const int grid = (a.n_embd + 3) / 4;
+    const size_t lds = ((size_t)a.k * a.n_ff + (size_t)a.k * a.n_ff / 8) * 4;
+#define GU(J)                                                                                 \
+  if (kpg <= J) {                                                                             \
+    if (lds > 65536)                                                                          \
+      (void)hipFuncSetAttribute((const void*)k_expert_down_q6u<J>,                            \
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);        \
+    launch_maybe_timed(k_expert_down_q6u<J>, dim3(grid), lds, s, t0, t1, a);                  \
+    return hipGetLastError();                                                                 \
+  }
+    GU(2) GU(4) GU(8)
+#undef GU
+  }
   const int lpr = std::min(64, pow2_at_least(8 * (a.n_ff / KNJ_QK)));
   const int rows_per_block = 8;
   const size_t lds = ((size_t)a.k * a.n_ff + (size_t)a.k * rows_per_block) * 4;

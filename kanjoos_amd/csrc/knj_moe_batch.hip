@@ -502,14 +502,19 @@ __global__ __launch_bounds__(kBlock) void k_dense_bf16(const uint16_t* __restric
   }
 }
 
-// Greedy token of each row of logits [m][n] (first maximum wins): one
-// workgroup per row.
-__global__ __launch_bounds__(kBlock) void k_argmax_rows(const float* __restrict__ logits, int n,
-                                                        int32_t* __restrict__ tok) {
-  const float* r = logits + (uint64_t)blockIdx.x * n;
+// Greedy token of each row of logits [m][n] (first maximum wins), in two
+// passes: workgroup (c, r) reduces chunk c of 8192 entries of row r to one
+// packed (value, index) key; then one workgroup per row reduces its keys.
+constexpr int kArgChunk = 8192;
+
+__global__ __launch_bounds__(kBlock) void k_argmax_part(const float* __restrict__ logits, int n,
+                                                        unsigned long long* __restrict__ keys) {
+  const int r = blockIdx.y, c = blockIdx.x;
+  const float* row = logits + (uint64_t)r * n;
+  const int i0 = c * kArgChunk, i1 = min(n, i0 + kArgChunk);
   unsigned long long best = 0;
-  for (int i = threadIdx.x; i < n; i += kBlock) {
-    const unsigned long long k = argmax_key(r[i], i);
+  for (int i = i0 + threadIdx.x; i < i1; i += kBlock) {
+    const unsigned long long k = argmax_key(row[i], i);
     best = k > best ? k : best;
   }
   best = wave_max_u64(best);
@@ -519,8 +524,20 @@ __global__ __launch_bounds__(kBlock) void k_argmax_rows(const float* __restrict_
   if (threadIdx.x == 0) {
     for (int q = 1; q < kBlock / 64; ++q) best = wb[q] > best ? wb[q] : best;
     best = wb[0] > best ? wb[0] : best;
-    tok[blockIdx.x] = argmax_index(best);
+    keys[(uint64_t)r * gridDim.x + c] = best;
   }
+}
+
+__global__ void k_argmax_final(const unsigned long long* __restrict__ keys, int nk,
+                               int32_t* __restrict__ tok) {
+  const int r = blockIdx.x;
+  unsigned long long best = 0;
+  for (int i = threadIdx.x; i < nk; i += 64) {
+    const unsigned long long k = keys[(uint64_t)r * nk + i];
+    best = k > best ? k : best;
+  }
+  best = wave_max_u64(best);
+  if (threadIdx.x == 0) tok[r] = argmax_index(best);
 }
 
 // ------------------------------------------------------------------ combine
@@ -548,21 +565,25 @@ __global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
     for (int q = 0; q < 16; ++q) r += ids[q] < ids[s] ? 1 : 0;
     rank[s] = r;
   }
+  // the slots in ascending expert order, once for all columns
+  int ps[16];
+  float ws[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    ps[r] = 0;
+    ws[r] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 16; ++s)
+      if (rank[s] == r) {
+        ps[r] = pr[s];
+        ws[r] = wt[s];
+      }
+  }
   for (int i = threadIdx.x; i < n; i += kBlock) {
     float o = 0.0f;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      if (r >= k) break;
-      int ps = 0;
-      float ws = 0.0f;
-#pragma unroll
-      for (int s = 0; s < 16; ++s)
-        if (rank[s] == r) {
-          ps = pr[s];
-          ws = wt[s];
-        }
-      o = __fadd_rn(o, __fmul_rn(ws, y[(uint64_t)ps * n + i]));
-    }
+    for (int r = 0; r < 16; ++r)
+      if (r < k) o = __fadd_rn(o, __fmul_rn(ws[r], y[(uint64_t)ps[r] * n + i]));
     out[(uint64_t)t * n + i] = resid ? __fadd_rn(resid[(uint64_t)t * n + i], o) : o;
   }
 }
@@ -716,8 +737,13 @@ hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, cons
   return hipGetLastError();
 }
 
-hipError_t launch_argmax_rows(const float* logits, int m, int n, int32_t* tok, hipStream_t s) {
-  hipLaunchKernelGGL(k_argmax_rows, dim3(m), dim3(kBlock), 0, s, logits, n, tok);
+int argmax_key_count(int n) { return (n + kArgChunk - 1) / kArgChunk; }
+
+hipError_t launch_argmax_rows(const float* logits, int m, int n, unsigned long long* keys,
+                              int32_t* tok, hipStream_t s) {
+  const int nk = argmax_key_count(n);
+  hipLaunchKernelGGL(k_argmax_part, dim3(nk, m), dim3(kBlock), 0, s, logits, n, keys);
+  hipLaunchKernelGGL(k_argmax_final, dim3(m), dim3(64), 0, s, keys, nk, tok);
   return hipGetLastError();
 }
 
