@@ -67,7 +67,7 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 acc) {
 }
 
 template <int D>
-__global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
+__global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   constexpr int ROWH = D + 8;            // f16 elements per K/V LDS row (16-byte pad)
   constexpr int QROW = D + 4;            // floats per query row
   constexpr int EROW = kChunk + 4;       // floats per score row
@@ -75,12 +75,13 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   __shared__ float qs[8 * QROW];         // normalised, rotated queries
   __shared__ uint16_t ks[kChunk * ROWH];
   __shared__ uint16_t vs[kChunk * ROWH];
-  __shared__ float es[8 * EROW];         // scores, then exp(score - max), per head
+  __shared__ float es[8 * EROW];         // scores, then exp(score - running max), per head
+  __shared__ float alpha[16];            // per head: rescale of the running sums this chunk
   const int kvh = blockIdx.x, split = blockIdx.y, n_split = gridDim.y;
   const int G = a.n_head / a.n_head_kv;
   KNJ_STAMP(0);
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int p0 = split * kChunk;
+  const int c0 = split * cpw;            // first chunk of this workgroup
   const int z = blockIdx.z;  // sequence
   uint16_t* kc = a.k_cache + z * a.kv_stride + (uint64_t)kvh * a.n_ctx * D;
   uint16_t* vc = a.v_cache + z * a.kv_stride + (uint64_t)kvh * a.n_ctx * D;
@@ -92,26 +93,29 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   const float* rc = a.rope_cos + (uint64_t)z * a.rope_stride;
   const float* rs = a.rope_sin + (uint64_t)z * a.rope_stride;
   const uint64_t hstride = (uint64_t)n_split * (D + 2);
-  // 1) every load that does not depend on the position first: this chunk's
-  // cache slots (16 bytes per load; rows past the valid length are dropped
-  // later), the raw query/key/value, the norm weights and the RoPE row
+  // 1) every load that does not depend on the position first: the first
+  // chunk's cache slots (16 bytes per load; rows past the valid length are
+  // dropped later), the raw query/key/value, the norm weights and the RoPE row
   constexpr int PER = (kChunk * D * 2) / (16 * kBlock);  // loads per thread per matrix
   static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
   // (named registers rather than an array: an array live across the query
   // pass below was placed in scratch memory)
   uint4 k0, k1, k2, k3, v0, v1, v2, v3;
-  auto ld = [&](int j, uint4& kk, uint4& vv) {
+  auto ld = [&](int p0, int j, uint4& kk, uint4& vv) {
     const int c16 = tid + kBlock * j;
     const int p = min(p0 + (c16 * 8) / D, a.n_ctx - 1), off = (c16 * 8) % D;
     kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)p * D + off);
     vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)p * D + off);
   };
-  ld(0, k0, v0);
-  ld(1, k1, v1);
-  if constexpr (PER > 2) {
-    ld(2, k2, v2);
-    ld(3, k3, v3);
-  }
+  auto ld_chunk = [&](int p0) {
+    ld(p0, 0, k0, v0);
+    ld(p0, 1, k1, v1);
+    if constexpr (PER > 2) {
+      ld(p0, 2, k2, v2);
+      ld(p0, 3, k3, v3);
+    }
+  };
+  ld_chunk(c0 * kChunk);
   const int qh = min(tid / T, G - 1), qc = tid % T;
   const float4 qraw = *reinterpret_cast<const float4*>(qz + (uint64_t)(kvh * G + qh) * D + 4 * qc);
   const float4 qnw = *reinterpret_cast<const float4*>(a.q_norm + 4 * qc);
@@ -123,40 +127,57 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
   const float4 sn = *reinterpret_cast<const float4*>(rs + ri);
   const int pos = a.pos[z];
   const int n_kv = pos + 1;
-  const int cnt = min(kChunk, n_kv - p0);
+  const int nch = min(cpw, (n_kv - c0 * kChunk + kChunk - 1) / kChunk);  // chunks holding slots
   KNJ_STAMP(1);
 
-  if (cnt > 0) {
-    // 2) queries of this kv head: 4 floats per thread, T threads per head
-    if (tid < G * T) {
-      const float4 r = norm_rope4<D>(qraw, qc, qnw, a.eps, cs, sn);
-      *reinterpret_cast<float4*>(qs + qh * QROW + 4 * qc) = r;
+  if (nch <= 0) {
+    for (int i = tid; i < G * (D + 2); i += kBlock) {
+      const int g = i / (D + 2), j = i % (D + 2);
+      *(part + g * hstride + j) = (j == 0) ? -INFINITY : 0.0f;
     }
+    return;
+  }
+  // 2) queries of this kv head: 4 floats per thread, T threads per head
+  if (tid < G * T) {
+    const float4 r = norm_rope4<D>(qraw, qc, qnw, a.eps, cs, sn);
+    *reinterpret_cast<float4*>(qs + qh * QROW + 4 * qc) = r;
+  }
+  // the key of this step (written to its slot below, in the chunk holding it)
+  uint16_t kh[4] = {0, 0, 0, 0}, vh[4] = {0, 0, 0, 0};
+  if (tid < T) {
+    const float4 r = norm_rope4<D>(kraw, tid, knw, a.eps, cs, sn);
+    kh[0] = f2h(r.x); kh[1] = f2h(r.y); kh[2] = f2h(r.z); kh[3] = f2h(r.w);
+    vh[0] = f2h(vraw.x); vh[1] = f2h(vraw.y); vh[2] = f2h(vraw.z); vh[3] = f2h(vraw.w);
+  }
+  const int r = lane & 15, kq = lane >> 4;
+  const bool hv = r < G;
+  const int h0 = 2 * wave, h1 = 2 * wave + 1;
+  float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;  // running max / sum (softmax waves)
+  f32x4 oe = {0.0f, 0.0f, 0.0f, 0.0f}, oo = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < nch; ++j) {
+    const int p0 = (c0 + j) * kChunk;
+    const int cnt = min(kChunk, n_kv - p0);
     // 3) the slot written this step, if it is in this chunk
     if (pos >= p0 && pos < p0 + cnt && tid < T) {
-      const int c = tid;
-      const float4 r = norm_rope4<D>(kraw, c, knw, a.eps, cs, sn);
-      const uint16_t kh[4] = {f2h(r.x), f2h(r.y), f2h(r.z), f2h(r.w)};
-      const uint16_t vh[4] = {f2h(vraw.x), f2h(vraw.y), f2h(vraw.z), f2h(vraw.w)};
       const int lp = pos - p0;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        kc[(uint64_t)pos * D + 4 * c + k] = kh[k];
-        vc[(uint64_t)pos * D + 4 * c + k] = vh[k];
-        ks[lp * ROWH + 4 * c + k] = kh[k];
-        vs[lp * ROWH + 4 * c + k] = vh[k];
+        kc[(uint64_t)pos * D + 4 * tid + k] = kh[k];
+        vc[(uint64_t)pos * D + 4 * tid + k] = vh[k];
+        ks[lp * ROWH + 4 * tid + k] = kh[k];
+        vs[lp * ROWH + 4 * tid + k] = vh[k];
       }
     }
     KNJ_STAMP(2);
     // cache rows past the valid length become zeros: the value product below
     // runs over all 64 rows with weight 0 there
-    auto st = [&](int j, const uint4& kk, const uint4& vv) {
-      const int c16 = tid + kBlock * j;
+    auto st = [&](int jj, const uint4& kk, const uint4& vv) {
+      const int c16 = tid + kBlock * jj;
       const int p = (c16 * 8) / D, off = (c16 * 8) % D;
       if (p >= cnt) {
-        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = z;
-        *reinterpret_cast<uint4*>(vs + p * ROWH + off) = z;
+        const uint4 zz = make_uint4(0u, 0u, 0u, 0u);
+        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = zz;
+        *reinterpret_cast<uint4*>(vs + p * ROWH + off) = zz;
       } else if (p0 + p != pos) {
         *reinterpret_cast<uint4*>(ks + p * ROWH + off) = kk;
         *reinterpret_cast<uint4*>(vs + p * ROWH + off) = vv;
@@ -168,13 +189,13 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       st(2, k2, v2);
       st(3, k3, v3);
     }
+    // the next chunk's slots load while this one is computed
+    if (j + 1 < nch) ld_chunk(p0 + kChunk);
     __syncthreads();
     KNJ_STAMP(3);
     // 4) scores on the matrix cores: wave w computes S[p][h] for the 16 slots
     // 16w..16w+15 (rows) and the query heads (columns, zero past G).  Lane
     // (r = l%16, kq = l/16) contributes dims kq*D/4 .. kq*D/4 + D/4 - 1.
-    const int r = lane & 15, kq = lane >> 4;
-    const bool hv = r < G;
     {
       const uint16_t* krow = ks + (16 * wave + r) * ROWH + kq * (D / 4);
       const float* qrow = qs + min(r, G - 1) * QROW + kq * (D / 4);
@@ -199,24 +220,23 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       }
     }
     __syncthreads();
-    // 5) softmax of the chunk: wave w owns heads 2w, 2w+1; lane = slot
-    const int h0 = 2 * wave, h1 = 2 * wave + 1;
+    // 5) online softmax of the chunk: wave w owns heads 2w, 2w+1; lane = slot
     if (h0 < G) {
       const float s0 = lane < cnt ? es[h0 * EROW + lane] : -INFINITY;
       const float s1 = (lane < cnt && h1 < G) ? es[h1 * EROW + lane] : -INFINITY;
-      const float m0 = group_max<64>(s0), m1 = group_max<64>(s1);
-      const float e0 = lane < cnt ? expf(s0 - m0) : 0.0f;
-      const float e1 = (lane < cnt && h1 < G) ? expf(s1 - m1) : 0.0f;
-      const float l0 = group_sum<64>(e0), l1 = group_sum<64>(e1);
+      const float n0 = fmaxf(m0, group_max<64>(s0)), n1 = fmaxf(m1, group_max<64>(s1));
+      const float a0 = expf(m0 - n0), a1 = h1 < G ? expf(m1 - n1) : 0.0f;  // exp(-inf) = 0 first
+      const float e0 = lane < cnt ? expf(s0 - n0) : 0.0f;
+      const float e1 = (lane < cnt && h1 < G) ? expf(s1 - n1) : 0.0f;
+      l0 = l0 * a0 + group_sum<64>(e0);
+      l1 = l1 * a1 + group_sum<64>(e1);
+      m0 = n0;
+      m1 = n1;
       es[h0 * EROW + lane] = e0;
       if (h1 < G) es[h1 * EROW + lane] = e1;
       if (lane == 0) {
-        *(part + h0 * hstride + 0) = m0;
-        *(part + h0 * hstride + 1) = l0;
-        if (h1 < G) {
-          *(part + h1 * hstride + 0) = m1;
-          *(part + h1 * hstride + 1) = l1;
-        }
+        alpha[h0] = a0;
+        if (h1 < G) alpha[h1] = a1;
       }
     }
     __syncthreads();
@@ -228,7 +248,13 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
       const int d = 32 * wave + 2 * r;
       const float* erow = es + min(r, G - 1) * EROW + kq * 16;
       const uint16_t* vcol = vs + (kq * 16) * ROWH + d;
-      f32x4 oe = {0.0f, 0.0f, 0.0f, 0.0f}, oo = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int h = 4 * kq + i;
+        const float al = h < G ? alpha[h] : 0.0f;
+        oe[i] *= al;
+        oo[i] *= al;
+      }
 #pragma unroll
       for (int t4 = 0; t4 < 16; t4 += 4) {
         const float4 ev = *reinterpret_cast<const float4*>(erow + t4);
@@ -240,19 +266,27 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a) {
           oo = mfma4(e4[i], h2f(vv >> 16), oo);
         }
       }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int h = 4 * kq + i;
-        if (h < G) *reinterpret_cast<float2*>(part + h * hstride + 2 + d) = make_float2(oe[i], oo[i]);
-      }
     }
-    KNJ_STAMP(5);
-  } else {
-    for (int i = tid; i < G * (D + 2); i += kBlock) {
-      const int g = i / (D + 2), j = i % (D + 2);
-      *(part + g * hstride + j) = (j == 0) ? -INFINITY : 0.0f;
+    __syncthreads();  // the next chunk overwrites ks/vs/es
+  }
+  // 7) the partial record {max, sum, sum e*v} of each head
+  if (h0 < G && lane == 0) {
+    *(part + h0 * hstride + 0) = m0;
+    *(part + h0 * hstride + 1) = l0;
+    if (h1 < G) {
+      *(part + h1 * hstride + 0) = m1;
+      *(part + h1 * hstride + 1) = l1;
     }
   }
+  if (32 * wave < D) {
+    const int d = 32 * wave + 2 * r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kq + i;
+      if (h < G) *reinterpret_cast<float2*>(part + h * hstride + 2 + d) = make_float2(oe[i], oo[i]);
+    }
+  }
+  KNJ_STAMP(5);
 }
 
 // Merge of the split partials of one query head (one workgroup per head):
@@ -328,14 +362,18 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
 int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-  const int n_split = attn_splits(a.n_ctx);
+  // one 64-slot chunk per workgroup up to 128 chunks; beyond, several chunks
+  // per workgroup so the merge sees at most 128 partials per head
+  const int chunks = attn_splits(a.n_ctx);
+  const int cpw = (chunks + 127) / 128;
+  const int n_split = (chunks + cpw - 1) / cpw;
   if (n_split > 1024) return hipErrorInvalidValue;
   const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
-    hipLaunchKernelGGL(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
-    hipLaunchKernelGGL(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     hipLaunchKernelGGL(k_attn_merge<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
     return hipErrorInvalidValue;
