@@ -46,6 +46,11 @@ class Model {
     int threads = 0;  // accepted for interface compatibility; the step runs on the GPU
   };
 
+  // A qwen3moe GGUF file (reference src/model/model.cpp:174): geometry and
+  // weights from the file, throws on a missing key or tensor, a shape that
+  // disagrees with the geometry, a weight type the device path lacks, or
+  // opt.n_ctx above the trained context.
+  static std::unique_ptr<Model> open(const std::string& path, const Options& opt);
   // Synthetic weights (seeded, include/knj_synth.h) of the given geometry and
   // quantisation, generated on the GPU.
   static std::unique_ptr<Model> open_synthetic(const knj_model_config& cfg, uint64_t seed,

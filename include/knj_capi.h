@@ -143,6 +143,15 @@ typedef struct knj_model knj_model;
 int knj_model_create_synthetic(const knj_model_config* cfg, uint64_t seed, knj_model** out);
 int knj_model_create_from_image(const knj_model_config* cfg, const void* image, uint64_t bytes,
                                 knj_model** out);
+/* A qwen3moe GGUF file (the reference's Model::open, model.cpp:174-232, and its
+ * geometry/tensor checks, :97-172): knj_gguf_probe reads the geometry and the
+ * weight types into `out` without a device; knj_model_create_from_gguf also
+ * copies every tensor into a device model (Q, K and V rows into one wqkv).
+ * Errors: a missing key or tensor, a wrong shape, an unsupported type, n_ctx
+ * beyond the trained context -- each with its name in knj_last_error(). */
+int knj_gguf_probe(const char* path, int n_ctx, knj_model_config* out);
+int knj_model_create_from_gguf(const char* path, int n_ctx, knj_model** out);
+int knj_model_config_get(const knj_model* m, knj_model_config* out);
 int knj_model_free(knj_model* m);
 uint64_t knj_model_image_bytes(const knj_model* m);
 const void* knj_model_image_device(const knj_model* m);

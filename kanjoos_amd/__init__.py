@@ -31,7 +31,8 @@ EXPORTS = (
     "knj_built_arch", "knj_last_error", "knj_malloc", "knj_free", "knj_memcpy_h2d",
     "knj_memcpy_d2h", "knj_memset_zero", "knj_synchronize", "knj_dequant", "knj_gemv",
     "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_moe_batch_layer", "knj_attention_step", "knj_model_create_synthetic", "knj_model_create_from_image",
-    "knj_model_free", "knj_model_image_bytes", "knj_model_image_device", "knj_model_layer_offsets", "knj_model_fill_kv",
+    "knj_model_free", "knj_model_image_bytes", "knj_model_image_device", "knj_model_layer_offsets", "knj_model_fill_kv", "knj_gguf_probe",
+    "knj_model_create_from_gguf", "knj_model_config_get",
     "knj_model_download_image", "knj_model_reset", "knj_model_pos", "knj_model_set_pos",
     "knj_model_forward", "knj_model_decode_greedy", "knj_model_hidden", "knj_model_topk",
     "knj_model_logits", "knj_model_kv_download", "knj_model_kv_upload",
@@ -126,6 +127,9 @@ _SIGS = {
     "knj_model_image_device": (_P, [_P]),
     "knj_model_layer_offsets": (_u64, [C.POINTER(ModelConfig), _i, C.POINTER(LayerOffsets)]),
     "knj_model_fill_kv": (_i, [_P, _i, _u64]),
+    "knj_gguf_probe": (_i, [C.c_char_p, _i, C.POINTER(ModelConfig)]),
+    "knj_model_create_from_gguf": (_i, [C.c_char_p, _i, C.POINTER(_P)]),
+    "knj_model_config_get": (_i, [_P, C.POINTER(ModelConfig)]),
     "knj_model_download_image": (_i, [_P, _P, _u64]),
     "knj_model_reset": (_i, [_P]),
     "knj_model_pos": (_i, [_P]),
@@ -288,6 +292,13 @@ def moe_batch_layer(x, router_w, gate, up, down, n_tokens, n_embd, n_ff, n_exper
                                     _p(topk_w), stream))
 
 
+def gguf_probe(path: str, n_ctx: int) -> ModelConfig:
+    """Geometry and weight types of a qwen3moe GGUF file (no device needed)."""
+    cfg = ModelConfig()
+    check(lib().knj_gguf_probe(os.fsencode(path), n_ctx, C.byref(cfg)))
+    return cfg
+
+
 def attention_step(q, k, v, q_norm, k_norm, eps, rope_base, pos, n_head, n_head_kv, head_dim,
                    n_ctx, k_cache, v_cache, out) -> None:
     check(lib().knj_attention_step(_p(q), _p(k), _p(v), _p(q_norm), _p(k_norm), eps, rope_base, pos,
@@ -308,6 +319,15 @@ class Model:
     def synthetic(cls, cfg: ModelConfig, seed: int = 0) -> "Model":
         h = _P()
         check(lib().knj_model_create_synthetic(C.byref(cfg), seed, C.byref(h)))
+        return cls(h.value, cfg)
+
+    @classmethod
+    def from_gguf(cls, path: str, n_ctx: int) -> "Model":
+        """A qwen3moe GGUF file (knj_model_create_from_gguf)."""
+        h = _P()
+        check(lib().knj_model_create_from_gguf(os.fsencode(path), n_ctx, C.byref(h)))
+        cfg = ModelConfig()
+        check(lib().knj_model_config_get(h.value, C.byref(cfg)))
         return cls(h.value, cfg)
 
     @classmethod

@@ -22,6 +22,7 @@
 
 #include "../../include/knj_synth.h"
 #include "knj_common.h"
+#include "knj_gguf.h"
 #include "knj_model_impl.h"
 
 namespace knj {
@@ -358,6 +359,205 @@ int knj_model_create_synthetic(const knj_model_config* cfg, uint64_t seed, knj_m
     return rc;
   }
   return finish_create(m, out);
+}
+
+namespace {
+
+// The geometry of a qwen3moe GGUF file (Model::read_geometry and
+// bind_tensors, /root/reference/src/model/model.cpp:97-172): metadata, tensor
+// names, shapes and the types this path runs.  `n_ctx` must not exceed the
+// trained context (model.cpp:180-186).
+int gguf_config(const GgufView& g, int n_ctx, knj_model_config* c) {
+  const std::string arch = g.meta_string("general.architecture");
+  if (arch != "qwen3moe") {
+    set_error("model: architecture is '" + arch + "', this path implements 'qwen3moe'");
+    return KNJ_E_ARG;
+  }
+  const std::string p = arch + ".";
+  int64_t v = 0;
+  double f = 0.0;
+  auto need_i = [&](const char* key, int32_t& dst) {
+    if (!g.meta_int(p + key, v)) {
+      set_error(std::string("model: metadata '") + p + key + "' is missing");
+      return false;
+    }
+    dst = (int32_t)v;
+    return true;
+  };
+  *c = knj_model_config{};
+  int32_t ctx_train = 0;
+  if (!need_i("block_count", c->n_layer) || !need_i("embedding_length", c->n_embd) ||
+      !need_i("attention.head_count", c->n_head) || !need_i("attention.key_length", c->head_dim) ||
+      !need_i("expert_feed_forward_length", c->n_ff) || !need_i("expert_count", c->n_expert) ||
+      !need_i("expert_used_count", c->n_expert_used) || !need_i("context_length", ctx_train))
+    return KNJ_E_ARG;
+  c->n_head_kv = g.meta_int(p + "attention.head_count_kv", v) ? (int32_t)v : c->n_head;
+  if (!g.meta_float(p + "attention.layer_norm_rms_epsilon", f)) {
+    set_error("model: metadata '" + p + "attention.layer_norm_rms_epsilon' is missing");
+    return KNJ_E_ARG;
+  }
+  c->rms_eps = (float)f;
+  if (!g.meta_float(p + "rope.freq_base", f)) {
+    set_error("model: metadata '" + p + "rope.freq_base' is missing");
+    return KNJ_E_ARG;
+  }
+  c->rope_base = (float)f;
+  if (n_ctx <= 0 || n_ctx > ctx_train) {
+    set_error("model: n_ctx " + std::to_string(n_ctx) + " outside [1, the trained context " +
+              std::to_string(ctx_train) + "]");
+    return KNJ_E_ARG;
+  }
+  c->n_ctx = n_ctx;
+  const GgufTensor* te = g.find("token_embd.weight");
+  if (!te || te->n_dims != 2) {
+    set_error("model: tensor 'token_embd.weight' is missing or not 2-D");
+    return KNJ_E_ARG;
+  }
+  c->n_vocab = g.meta_int("vocab_size", v) ? (int32_t)v : (int32_t)te->dims[1];
+  // shapes (dims[0] fastest) and types
+  const int64_t H = c->n_embd, QD = (int64_t)c->n_head * c->head_dim;
+  const int64_t KVD = (int64_t)c->n_head_kv * c->head_dim, F = c->n_ff, E = c->n_expert;
+  auto want = [&](const std::string& name, std::initializer_list<int64_t> dims,
+                  const GgufTensor** out) {
+    const GgufTensor* t = g.find(name);
+    if (!t) {
+      set_error("model: tensor '" + name + "' is missing");
+      return false;
+    }
+    if (t->n_dims != dims.size()) {
+      set_error("model: tensor '" + name + "' has " + std::to_string(t->n_dims) + " dims, expected " +
+                std::to_string(dims.size()));
+      return false;
+    }
+    int i = 0;
+    for (int64_t d : dims) {
+      if ((int64_t)t->dims[i] != d) {
+        set_error("model: tensor '" + name + "' dim " + std::to_string(i) + " is " +
+                  std::to_string(t->dims[i]) + ", expected " + std::to_string(d));
+        return false;
+      }
+      ++i;
+    }
+    if (t->bytes == 0) {
+      set_error("model: tensor '" + name + "' has unsupported type " + std::to_string(t->type));
+      return false;
+    }
+    if (out) *out = t;
+    return true;
+  };
+  const GgufTensor *ow = nullptr, *on = nullptr;
+  if (!want("token_embd.weight", {H, c->n_vocab}, nullptr) ||
+      !want("output_norm.weight", {H}, &on) || !want("output.weight", {H, c->n_vocab}, &ow))
+    return KNJ_E_ARG;
+  c->type_embd = (int32_t)te->type;
+  c->type_head = (int32_t)ow->type;
+  for (int il = 0; il < c->n_layer; ++il) {
+    const std::string b = "blk." + std::to_string(il) + ".";
+    const GgufTensor *q, *k, *vv, *o, *gi, *ge, *ue, *de;
+    const GgufTensor *n1, *n2, *qn, *kn;
+    if (!want(b + "attn_norm.weight", {H}, &n1) || !want(b + "ffn_norm.weight", {H}, &n2) ||
+        !want(b + "attn_q.weight", {H, QD}, &q) || !want(b + "attn_k.weight", {H, KVD}, &k) ||
+        !want(b + "attn_v.weight", {H, KVD}, &vv) || !want(b + "attn_output.weight", {QD, H}, &o) ||
+        !want(b + "attn_q_norm.weight", {c->head_dim}, &qn) ||
+        !want(b + "attn_k_norm.weight", {c->head_dim}, &kn) ||
+        !want(b + "ffn_gate_inp.weight", {H, E}, &gi) ||
+        !want(b + "ffn_gate_exps.weight", {H, F, E}, &ge) ||
+        !want(b + "ffn_up_exps.weight", {H, F, E}, &ue) ||
+        !want(b + "ffn_down_exps.weight", {F, H, E}, &de))
+      return KNJ_E_ARG;
+    for (const GgufTensor* t : {n1, n2, qn, kn, gi, on})
+      if (t->type != KNJ_TYPE_F32) {
+        set_error("model: tensor '" + t->name + "' must be F32 on this path");
+        return KNJ_E_ARG;
+      }
+    if (il == 0) {
+      c->type_attn = (int32_t)q->type;
+      c->type_gate_up = (int32_t)ge->type;
+      c->type_down = (int32_t)de->type;
+    }
+    if ((int32_t)q->type != c->type_attn || (int32_t)k->type != c->type_attn ||
+        (int32_t)vv->type != c->type_attn || (int32_t)o->type != c->type_attn ||
+        (int32_t)ge->type != c->type_gate_up || (int32_t)ue->type != c->type_gate_up ||
+        (int32_t)de->type != c->type_down) {
+      set_error("model: layer " + std::to_string(il) +
+                " mixes weight types; this path needs one type per projection kind");
+      return KNJ_E_ARG;
+    }
+  }
+  c->init_std = 0.0f;
+  return KNJ_OK;
+}
+
+}  // namespace
+
+int knj_gguf_probe(const char* path, int n_ctx, knj_model_config* out) {
+  KNJ_CHECK_ARG(path && out, "null pointer");
+  GgufView g;
+  if (!g.open(path)) {
+    set_error("gguf: " + g.error());
+    return KNJ_E_ARG;
+  }
+  int rc = gguf_config(g, n_ctx, out);
+  if (rc) return rc;
+  return validate(out);
+}
+
+int knj_model_create_from_gguf(const char* path, int n_ctx, knj_model** out) {
+  int rc = require_open();
+  if (rc) return rc;
+  KNJ_CHECK_ARG(path && out, "null pointer");
+  GgufView g;
+  if (!g.open(path)) {
+    set_error("gguf: " + g.error());
+    return KNJ_E_ARG;
+  }
+  knj_model_config c;
+  if ((rc = gguf_config(g, n_ctx, &c)) || (rc = validate(&c))) return rc;
+  knj_model* m = new knj_model();
+  m->c = c;
+  if ((rc = setup(m))) {
+    knj_model_free(m);
+    return rc;
+  }
+  // each tensor straight from the mapping to its place in the image; the
+  // layer's Q, K and V rows back to back form wqkv
+  auto put = [&](const char* name, uint64_t off) -> int {
+    const GgufTensor* t = g.find(name);
+    if (hipMemcpy(m->image + off, g.data(*t), t->bytes, hipMemcpyHostToDevice) != hipSuccess)
+      return hip_fail(hipErrorUnknown, "image upload");
+    return KNJ_OK;
+  };
+  rc = put("token_embd.weight", m->off_embd);
+  if (!rc) rc = put("output_norm.weight", m->off_onorm);
+  if (!rc) rc = put("output.weight", m->off_head);
+  const uint64_t rqkv = knj_row_bytes(c.type_attn, (uint64_t)c.n_embd);
+  const uint64_t QD = (uint64_t)c.n_head * c.head_dim, KVD = (uint64_t)c.n_head_kv * c.head_dim;
+  for (int il = 0; il < c.n_layer && !rc; ++il) {
+    const std::string b = "blk." + std::to_string(il) + ".";
+    const knj_layer_offsets& lo = m->lo[il];
+    const std::pair<const char*, uint64_t> parts[] = {
+        {"attn_norm.weight", lo.attn_norm}, {"ffn_norm.weight", lo.ffn_norm},
+        {"attn_q_norm.weight", lo.q_norm},  {"attn_k_norm.weight", lo.k_norm},
+        {"attn_q.weight", lo.wqkv},         {"attn_k.weight", lo.wqkv + rqkv * QD},
+        {"attn_v.weight", lo.wqkv + rqkv * (QD + KVD)},
+        {"attn_output.weight", lo.wo},      {"ffn_gate_inp.weight", lo.router},
+        {"ffn_gate_exps.weight", lo.gate},  {"ffn_up_exps.weight", lo.up},
+        {"ffn_down_exps.weight", lo.down}};
+    for (const auto& pr : parts) {
+      if ((rc = put((b + pr.first).c_str(), pr.second))) break;
+    }
+  }
+  if (rc) {
+    knj_model_free(m);
+    return rc;
+  }
+  return finish_create(m, out);
+}
+
+int knj_model_config_get(const knj_model* m, knj_model_config* out) {
+  KNJ_CHECK_ARG(m && out, "null pointer");
+  *out = m->c;
+  return KNJ_OK;
 }
 
 int knj_model_create_from_image(const knj_model_config* cfg, const void* image, uint64_t bytes,

@@ -2,11 +2,11 @@
 //
 // The shape of the reference's kanjoos-run prefill -> greedy decode loop and its
 // --bench PP TG mode (/root/reference/src/cli/main.cpp:245-279, 451-568), over
-// the C++ Model class; weights are the seeded synthetic Qwen3-30B-A3B-shaped
-// model (no GGUF loading in this build).
+// the C++ Model class; weights come from a qwen3moe GGUF file (--model) or are
+// the seeded synthetic Qwen3-30B-A3B-shaped model.
 //
 //   kanjoos-run [--layers N] [--ctx N] [--seed S] [--prompt N] [--n-predict N]
-//               [--bench PP TG] [--small]
+//               [--bench PP TG] [--small] [--model PATH.gguf]
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -22,6 +22,7 @@ int main(int argc, char** argv) {
   int layers = 48, ctx = 4352, prompt = 16, n_predict = 32, pp = 0, tg = 0;
   uint64_t seed = 0;
   bool small = false;
+  std::string model_path;  // --model PATH: a qwen3moe GGUF instead of synthetic weights
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     auto next = [&](const char* name) {
@@ -37,12 +38,26 @@ int main(int argc, char** argv) {
     else if (a == "--prompt") prompt = next("--prompt");
     else if (a == "--n-predict") n_predict = next("--n-predict");
     else if (a == "--small") small = true;
+    else if (a == "--model") {
+      if (i + 1 >= argc) {
+        std::fprintf(stderr, "--model needs a value\n");
+        return 2;
+      }
+      model_path = argv[++i];
+    }
     else if (a == "--bench") {
       pp = next("--bench");
       tg = next("--bench");
     } else {
       std::fprintf(stderr, "unknown argument %s\n", a.c_str());
       return 2;
+    }
+  }
+  if (!model_path.empty()) {  // refuse a bad file before touching the device
+    knj_model_config probe{};
+    if (knj_gguf_probe(model_path.c_str(), ctx, &probe) != 0) {
+      std::fprintf(stderr, "model: %s\n", knj_last_error());
+      return 3;
     }
   }
   auto backend = knj::Backend::create(0);
@@ -63,7 +78,9 @@ int main(int argc, char** argv) {
   try {
     knj::Model::Options opt;
     opt.n_ctx = ctx;
-    auto m = knj::Model::open_synthetic(c, seed, opt);
+    auto m = model_path.empty() ? knj::Model::open_synthetic(c, seed, opt)
+                                : knj::Model::open(model_path, opt);
+    c.n_vocab = m->geom().n_vocab;
     std::printf("%s\n", m->geom().describe().c_str());
     std::mt19937 rng((uint32_t)seed);
     auto run_prompt = [&](int n) {

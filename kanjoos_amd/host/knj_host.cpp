@@ -58,6 +58,18 @@ std::unique_ptr<Model> Model::open_synthetic(const knj_model_config& cfg, uint64
   return m;
 }
 
+std::unique_ptr<Model> Model::open(const std::string& path, const Options& opt) {
+  if (opt.n_ctx <= 0) throw std::runtime_error("model: n_ctx must be positive");
+  std::unique_ptr<Model> m(new Model());
+  check(knj_model_create_from_gguf(path.c_str(), opt.n_ctx, &m->m_), "open");
+  knj_model_config c{};
+  check(knj_model_config_get(m->m_, &c), "open");
+  m->g_ = geometry_of(c);
+  m->n_ctx_ = c.n_ctx;
+  m->logits_.assign((size_t)c.n_vocab, 0.0f);
+  return m;
+}
+
 std::unique_ptr<Model> Model::open_image(const knj_model_config& cfg, const void* image,
                                          uint64_t bytes, const Options& opt) {
   if (opt.n_ctx <= 0) throw std::runtime_error("model: n_ctx must be positive");
