@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../knj_capi.h"
+#include "profiler.h"
 
 namespace knj {
 
@@ -71,12 +72,26 @@ class Model {
   // Drops the KV cache and returns to position 0.
   void reset();
 
+  // Fills cache slots [0, n_pos) with seeded f16 values and moves to n_pos:
+  // a long context without running its prefill (knj_model_fill_kv).
+  void fill_kv(int n_pos, uint64_t seed);
+
   // Runs `n` tokens starting at the current position; returns n_vocab logits
   // of the last token, valid until the next call.
   const float* forward(const int32_t* tokens, int n);
 
   // Greedy decode on the device: feeds `first`, returns `steps` argmax tokens.
   std::vector<int32_t> decode_greedy(int32_t first, int steps);
+
+  // The same decode with every kernel launch timed by dispatch-recorded events
+  // (knj_model_profile), one step per call.  Each step's launches go to `prof`
+  // as device spans named "class:layer:kernel" after prof.step_done() has seen
+  // its warmup; steps are laid end to end on one timeline, so the host time
+  // between steps is not counted as device idle.  Same tokens as decode_greedy.
+  std::vector<int32_t> decode_greedy_profiled(int32_t first, int steps, Profiler& prof);
+
+  // Host<->device bytes copied so far (knj_model_transfer_bytes).
+  TransferStats transfer_stats() const;
 
   knj_model* handle() const { return m_; }
 

@@ -217,6 +217,44 @@ int knj_model_time_decode(knj_model* m, int iters, float* ms_out);
  * position by `steps`. */
 int knj_model_time_experts(knj_model* m, int steps, float* us_gateup, float* us_down);
 
+/* ---- device spans for the profiler -------------------------------------------
+ * The device event backend of the reference's profiler
+ * (/root/reference/src/profiler/profiler.h:98-139: device_span() takes offsets
+ * from one epoch event per stream, set_device_floor() a floor measured through
+ * the same event path, set_device_dropped() the spans a full ring lost).  One
+ * record per kernel launch: the op class it belongs to (the reference's scope
+ * names where one kernel does one op -- "embed", "qkv", "attention", "attn-o",
+ * "moe-router", "head" -- and joined names for fused kernels:
+ * "moe-gate+up+act", "moe-down+scatter", "sample"), the layer (-1 outside the
+ * layers), the kernel symbol, and the dispatch's own start/end in nanoseconds
+ * after the epoch event. */
+typedef struct knj_span {
+  char name[32];
+  char kernel[40];
+  int32_t layer;
+  int32_t stream;
+  uint64_t start_ns;
+  uint64_t end_ns;
+} knj_span;
+
+/* Greedy decode exactly as knj_model_decode_greedy (same tokens, same KV
+ * writes, position advanced by `steps`), but with the step's kernels launched
+ * directly, each with dispatch-recorded start/end events.  Up to `cap` spans
+ * are written; *n_dropped counts launches beyond `cap` (a stated loss).
+ * cap <= 1 << 20. */
+int knj_model_profile(knj_model* m, int32_t first, int steps, int32_t* out_tokens, knj_span* spans,
+                      int cap, int* n_spans, uint64_t* n_dropped);
+
+/* Host<->device bytes this model's calls have copied since it was created
+ * (weight upload, per-step token state, logits/tokens/diagnostic downloads):
+ * the profiler's transfer row. */
+int knj_model_transfer_bytes(const knj_model* m, uint64_t* h2d, uint64_t* d2h);
+
+/* The device instrumentation floor: `n` empty kernels (one wave each, after
+ * untimed warm-up launches) timed through the same dispatch-event path;
+ * *ns_out is their median span. */
+int knj_device_floor(int n, uint64_t* ns_out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -36,7 +36,8 @@ EXPORTS = (
     "knj_model_download_image", "knj_model_reset", "knj_model_pos", "knj_model_set_pos",
     "knj_model_forward", "knj_model_decode_greedy", "knj_model_hidden", "knj_model_topk",
     "knj_model_logits", "knj_model_kv_download", "knj_model_kv_upload",
-    "knj_model_time_decode", "knj_model_time_experts",
+    "knj_model_time_decode", "knj_model_time_experts", "knj_model_profile",
+    "knj_model_transfer_bytes", "knj_device_floor",
     "knj_batch_create", "knj_batch_free", "knj_batch_pos", "knj_batch_forward",
     "knj_batch_decode_greedy", "knj_batch_fill_kv", "knj_batch_hidden", "knj_batch_topk",
     "knj_batch_kv_download",
@@ -82,6 +83,12 @@ class LayerOffsets(C.Structure):
     """Byte offsets of one layer's tensors in the weight image (knj_layer_offsets)."""
     _fields_ = [(n, C.c_uint64) for n in ("attn_norm", "ffn_norm", "q_norm", "k_norm", "wqkv", "wo",
                                            "router", "gate", "up", "down")]
+
+
+class Span(C.Structure):
+    """One profiled kernel launch (include/knj_capi.h knj_span)."""
+    _fields_ = [("name", C.c_char * 32), ("kernel", C.c_char * 40), ("layer", C.c_int32),
+                ("stream", C.c_int32), ("start_ns", C.c_uint64), ("end_ns", C.c_uint64)]
 
 
 class DeviceCaps(C.Structure):
@@ -143,6 +150,9 @@ _SIGS = {
     "knj_model_kv_upload": (_i, [_P, _P, _P]),
     "knj_model_time_decode": (_i, [_P, _i, C.POINTER(_f)]),
     "knj_model_time_experts": (_i, [_P, _i, C.POINTER(_f), C.POINTER(_f)]),
+    "knj_model_profile": (_i, [_P, C.c_int32, _i, _P, _P, _i, C.POINTER(_i), C.POINTER(_u64)]),
+    "knj_model_transfer_bytes": (_i, [_P, C.POINTER(_u64), C.POINTER(_u64)]),
+    "knj_device_floor": (_i, [_i, C.POINTER(_u64)]),
     "knj_batch_create": (_i, [_P, _i, _i, C.POINTER(_P)]),
     "knj_batch_free": (_i, [_P]),
     "knj_batch_pos": (_i, [_P]),
@@ -292,6 +302,13 @@ def moe_batch_layer(x, router_w, gate, up, down, n_tokens, n_embd, n_ff, n_exper
                                     _p(topk_w), stream))
 
 
+def device_floor(n: int = 256) -> int:
+    """Mean span of `n` empty kernels timed through the profiling event path, ns."""
+    v = C.c_uint64(0)
+    check(lib().knj_device_floor(n, C.byref(v)))
+    return v.value
+
+
 def gguf_probe(path: str, n_ctx: int) -> ModelConfig:
     """Geometry and weight types of a qwen3moe GGUF file (no device needed)."""
     cfg = ModelConfig()
@@ -429,6 +446,24 @@ class Model:
         ms = C.c_float()
         check(lib().knj_model_time_decode(self.h, iters, C.byref(ms)))
         return ms.value
+
+    def profile(self, first: int, steps: int, cap: int = 4096):
+        """Greedy decode with every launch timed (knj_model_profile): returns
+        (tokens, spans as (name, layer, kernel, start_ns, end_ns), dropped)."""
+        toks = np.zeros(steps, np.int32)
+        sp = (Span * cap)()
+        n = C.c_int(0)
+        dropped = C.c_uint64(0)
+        check(lib().knj_model_profile(self.h, first, steps, _ptr(toks), sp, cap, C.byref(n),
+                                      C.byref(dropped)))
+        spans = [(s.name.decode(), s.layer, s.kernel.decode(), s.start_ns, s.end_ns)
+                 for s in sp[: n.value]]
+        return toks, spans, dropped.value
+
+    def transfer_bytes(self):
+        h, d = C.c_uint64(0), C.c_uint64(0)
+        check(lib().knj_model_transfer_bytes(self.h, C.byref(h), C.byref(d)))
+        return h.value, d.value
 
     def time_experts(self, steps: int):
         """(gate/up, down) mean microseconds per launch over `steps` greedy decode

@@ -36,7 +36,7 @@ def sources():
     """HIP device+host sources, then the plain C++ host classes (compiled by
     hipcc as host code)."""
     hip = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
-    return hip + [os.path.join(HOST, "knj_host.cpp")]
+    return hip + [os.path.join(HOST, f) for f in ("knj_host.cpp", "knj_profiler.cpp", "knj_residency.cpp")]
 
 
 def _compile(src: str) -> str:

@@ -370,11 +370,11 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (n_split > 1024) return hipErrorInvalidValue;
   const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
-    hipLaunchKernelGGL(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    hipLaunchKernelGGL(k_attn_merge<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
+    KNJ_LAUNCH(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
+    KNJ_LAUNCH(k_attn_merge<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
-    hipLaunchKernelGGL(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    hipLaunchKernelGGL(k_attn_merge<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
+    KNJ_LAUNCH(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
+    KNJ_LAUNCH(k_attn_merge<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
     return hipErrorInvalidValue;
   }

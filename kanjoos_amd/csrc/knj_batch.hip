@@ -104,7 +104,7 @@ int enqueue_batch_step(knj_batch* b, hipStream_t s) {
   const int B = b->n_seq, H = c.n_embd, D = c.head_dim, QD = c.n_head * D, KVD = c.n_head_kv * D;
   const int QKV = QD + 2 * KVD, half = D / 2;
   const uint8_t* img = m->image;
-  hipLaunchKernelGGL(k_embed_batch, dim3((H + 255) / 256, B), dim3(256), 0, s, c.type_embd,
+  KNJ_LAUNCH(k_embed_batch, dim3((H + 255) / 256, B), dim3(256), 0, s, c.type_embd,
                      img + m->off_embd, H, b->tokens, b->dpos, m->rope_cos, m->rope_sin, half, b->x,
                      b->rope);
   KNJ_HIP(hipGetLastError());
@@ -140,7 +140,7 @@ int enqueue_batch_step(knj_batch* b, hipStream_t s) {
   KNJ_HIP(launch_dense_bf16(reinterpret_cast<const uint16_t*>(img + m->off_head), H, c.n_vocab, B,
                             b->hx, b->logits, b->scratch, s));
   KNJ_HIP(launch_argmax_rows(b->logits, B, c.n_vocab, b->keys, b->next, s));
-  hipLaunchKernelGGL(k_batch_close, dim3(1), dim3(std::max(64, (B + 63) / 64 * 64)), 0, s, B,
+  KNJ_LAUNCH(k_batch_close, dim3(1), dim3(std::max(64, (B + 63) / 64 * 64)), 0, s, B,
                      b->next, b->tokens, b->dpos, b->step, b->out_tokens, b->max_steps);
   KNJ_HIP(hipGetLastError());
   return KNJ_OK;

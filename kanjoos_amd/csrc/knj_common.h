@@ -3,6 +3,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include "knj_spans.h"
+
 #include <cstdint>
 #include <string>
 

@@ -467,7 +467,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
       const int grid = (steps_total + 4 * rs - 1) / (4 * rs);
 #define GQ(L, R)                                                                            \
   if (lpr == L && rs == R) {                                                                \
-    hipLaunchKernelGGL((k_gemv_q4k<L, R>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,    \
+    KNJ_LAUNCH((k_gemv_q4k<L, R>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,    \
                        a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y);                        \
     return hipGetLastError();                                                               \
   }
@@ -478,12 +478,12 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
     }
     const size_t lds = (size_t)xpad_size(a.n_in) * 4;
     const int grid = std::max(1, std::min(2048, (a.n_out + 3) / 4));
-    hipLaunchKernelGGL(k_gemv_q4k_wide, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, a.x,
+    KNJ_LAUNCH(k_gemv_q4k_wide, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, a.x,
                        a.norm_w, a.eps, a.resid, a.y);
     return hipGetLastError();
   }
   if (a.type == KNJ_TYPE_Q6_K && a.n_in <= 2048) {
-    hipLaunchKernelGGL(k_gemv_q6k_u<4>, dim3(gemv_grid(a.type, a.n_in, a.n_out)), dim3(kBlock), 0, s,
+    KNJ_LAUNCH(k_gemv_q6k_u<4>, dim3(gemv_grid(a.type, a.n_in, a.n_out)), dim3(kBlock), 0, s,
                        a.w, a.n_in, a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
     return hipGetLastError();
   }
@@ -493,7 +493,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
     const int grid = gemv_grid(a.type, a.n_in, a.n_out);
 #define G6(L)                                                                                 \
   if (lpr == L) {                                                                             \
-    hipLaunchKernelGGL(k_gemv_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, \
+    KNJ_LAUNCH(k_gemv_q6k<L>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out, \
                        a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);                     \
     return hipGetLastError();                                                                 \
   }
@@ -507,7 +507,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
     const int grid = gemv_grid(a.type, a.n_in, a.n_out);
 #define GB(J)                                                                                   \
   if (nj == J) {                                                                                \
-    hipLaunchKernelGGL((k_gemv_bf16<J, RS>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,     \
+    KNJ_LAUNCH((k_gemv_bf16<J, RS>), dim3(grid), dim3(kBlock), 0, s, a.w, a.n_in,     \
                        a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);             \
     return hipGetLastError();                                                                   \
   }
@@ -517,10 +517,10 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
   const size_t lds = (size_t)a.n_in * 4;
   const int grid = gemv_grid(KNJ_TYPE_F32, a.n_in, a.n_out);
   if (a.type == KNJ_TYPE_BF16) {
-    hipLaunchKernelGGL(k_gemv_plain<true>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out,
+    KNJ_LAUNCH(k_gemv_plain<true>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in, a.n_out,
                        a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
   } else {
-    hipLaunchKernelGGL(k_gemv_plain<false>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in,
+    KNJ_LAUNCH(k_gemv_plain<false>, dim3(grid), dim3(kBlock), lds, s, a.w, a.n_in,
                        a.n_out, a.x, a.norm_w, a.eps, a.resid, a.y, a.argmax_key);
   }
   return hipGetLastError();
@@ -528,7 +528,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
 
 hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int nkeys,
                              int32_t* out_tokens, int max_steps, hipStream_t s) {
-  hipLaunchKernelGGL(k_step_close, dim3(1), dim3(kBlock), 0, s, st, keys, nkeys, out_tokens,
+  KNJ_LAUNCH(k_step_close, dim3(1), dim3(kBlock), 0, s, st, keys, nkeys, out_tokens,
                      max_steps);
   return hipGetLastError();
 }

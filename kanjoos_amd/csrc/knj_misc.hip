@@ -61,13 +61,13 @@ __global__ void k_embed(int type, const uint8_t* __restrict__ table, int n_embd,
 
 hipError_t launch_dequant(int type, const uint8_t* w, uint64_t n, float* out, hipStream_t s) {
   const uint64_t blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(k_dequant, dim3((unsigned)blocks), dim3(256), 0, s, type, w, n, out);
+  KNJ_LAUNCH(k_dequant, dim3((unsigned)blocks), dim3(256), 0, s, type, w, n, out);
   return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(const float* x, const float* w, int n, float eps, float* out,
                           hipStream_t s) {
-  hipLaunchKernelGGL(k_rmsnorm, dim3(1), dim3(kBlock), 0, s, x, w, n, eps, out);
+  KNJ_LAUNCH(k_rmsnorm, dim3(1), dim3(kBlock), 0, s, x, w, n, eps, out);
   return hipGetLastError();
 }
 
@@ -75,7 +75,7 @@ hipError_t launch_embed(int type, const uint8_t* table, int n_embd, StepState* s
                         const float* rope_cos, const float* rope_sin, int half, float* rope_cur,
                         hipStream_t s) {
   if (2 * half > 256) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_embed, dim3((n_embd + 255) / 256), dim3(256), 0, s, type, table, n_embd, st,
+  KNJ_LAUNCH(k_embed, dim3((n_embd + 255) / 256), dim3(256), 0, s, type, table, n_embd, st,
                      x, rope_cos, rope_sin, half, rope_cur);
   return hipGetLastError();
 }

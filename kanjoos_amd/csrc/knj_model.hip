@@ -16,6 +16,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
+#include <cstdio>
 #include <cstring>
 #include <memory>
 #include <vector>
@@ -84,6 +85,62 @@ int fill_kv_rows(uint16_t* k, uint16_t* v, uint64_t rows, uint64_t row_elems, ui
   hipLaunchKernelGGL(k_fill_kv, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, k, v, rows,
                      row_elems, n_elems, knj_mix64(seed ^ 0x4B56ull));
   KNJ_HIP(hipGetLastError());
+  return KNJ_OK;
+}
+
+thread_local SpanSink* tl_span_sink = nullptr;
+
+namespace {
+__global__ void k_span_floor(int) {}
+}  // namespace
+
+// Installs a span sink of `cap` event pairs on this thread for its lifetime.
+SpanRun::SpanRun(int cap) {
+  sink.cap = cap;
+  events.assign((size_t)2 * cap, nullptr);
+  for (auto& e : events)
+    if ((err = hipEventCreate(&e)) != hipSuccess) return;
+  if ((err = hipEventCreate(&epoch)) != hipSuccess) return;
+  sink.ev = events.data();
+  sink.tags.reserve((size_t)cap);
+  tl_span_sink = &sink;
+}
+
+SpanRun::~SpanRun() {
+  if (tl_span_sink == &sink) tl_span_sink = nullptr;
+  for (auto e : events)
+    if (e) (void)hipEventDestroy(e);
+  if (epoch) (void)hipEventDestroy(epoch);
+}
+
+void SpanRun::stop() {
+  if (tl_span_sink == &sink) tl_span_sink = nullptr;
+}
+
+// Offsets of every recorded span from the epoch event (the events must have
+// completed), written as knj_span records.
+int SpanRun::collect(knj_span* out, int cap, int* n_out, uint64_t* dropped) {
+  const int n = std::min(sink.used, cap);
+  for (int i = 0; i < n; ++i) {
+    float a = 0.0f, b = 0.0f;
+    hipError_t e = hipEventElapsedTime(&a, epoch, events[2 * i]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&b, epoch, events[2 * i + 1]);
+    if (e != hipSuccess) return hip_fail(e, "hipEventElapsedTime");
+    knj_span& r = out[i];
+    std::memset(&r, 0, sizeof(r));
+    const SpanTag& t = sink.tags[(size_t)i];
+    std::snprintf(r.name, sizeof(r.name), "%s", t.cls);
+    // the stringised kernel expression, without wrapping parentheses
+    std::string k(t.kernel);
+    while (!k.empty() && (k.back() == ')' || k.back() == ' ')) k.pop_back();
+    std::snprintf(r.kernel, sizeof(r.kernel), "%s", k.c_str());
+    r.layer = t.layer;
+    r.stream = 0;
+    r.start_ns = (uint64_t)std::llround((double)a * 1e6);
+    r.end_ns = std::max(r.start_ns, (uint64_t)std::llround((double)b * 1e6));
+  }
+  *n_out = n;
+  if (dropped) *dropped = sink.dropped + (uint64_t)(sink.used - n);
   return KNJ_OK;
 }
 
@@ -177,7 +234,9 @@ int setup(knj_model* m) {
       ts[(size_t)p * half + i] = std::sin(th);
     }
   KNJ_HIP(hipMemcpy(m->rope_cos, tc.data(), tc.size() * 4, hipMemcpyHostToDevice));
+  m->h2d_bytes += tc.size() * 4;
   KNJ_HIP(hipMemcpy(m->rope_sin, ts.data(), ts.size() * 4, hipMemcpyHostToDevice));
+  m->h2d_bytes += ts.size() * 4;
   return KNJ_OK;
 }
 
@@ -249,6 +308,7 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
   const uint8_t* img = m->image;
   GemvArgs qkv{c.type_attn, img + lo.wqkv, H, QD + 2 * KVD, m->x,
                reinterpret_cast<const float*>(img + lo.attn_norm), c.rms_eps, nullptr, m->qkv, nullptr};
+  span_scope("qkv", il);
   KNJ_HIP(launch_gemv(qkv, s));
   const uint64_t kv_layer = (uint64_t)il * c.n_head_kv * c.n_ctx * D;
   AttnArgs at{m->qkv, m->qkv + QD, m->qkv + QD + KVD,
@@ -256,12 +316,15 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
               reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cur, m->rope_cur + D / 2,
               &m->st->pos, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head, c.n_head_kv, D, c.n_ctx,
               1.0f / std::sqrt((float)D), m->attn_part, m->ctx};
+  span_class("attention");
   KNJ_HIP(launch_attention(at, s));
   GemvArgs o{c.type_attn, img + lo.wo, QD, H, m->ctx, nullptr, 0.0f, m->x, m->x, nullptr};
+  span_class("attn-o");
   KNJ_HIP(launch_gemv(o, s));
   RouterArgs ra{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
                 reinterpret_cast<const float*>(img + lo.router), H, c.n_expert, c.n_expert_used,
                 m->hx, m->router_logits + (uint64_t)il * c.n_expert, nullptr, nullptr, m->counter};
+  span_class("moe-router");
   KNJ_HIP(launch_router(ra, s));
   // the gate/up launch routes from the logits (softmax + top-k per wave)
   int32_t* ti = m->topk_idx + (uint64_t)il * c.n_expert_used;
@@ -273,13 +336,16 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
                 m->x, m->hidden + (uint64_t)il * H};
   // timing runs: each expert launch records its own start/end events
   hipEvent_t* ev = m->expert_events ? m->expert_events + 4 * m->expert_slot++ : nullptr;
+  span_class("moe-gate+up+act");
   KNJ_HIP(launch_expert_gateup(ea, s, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr));
+  span_class("moe-down+scatter");
   KNJ_HIP(launch_expert_down(ea, s, ev ? ev[2] : nullptr, ev ? ev[3] : nullptr));
   return KNJ_OK;
 }
 
 int enqueue_step(knj_model* m, hipStream_t s) {
   const knj_model_config& c = m->c;
+  span_scope("embed", -1);
   KNJ_HIP(launch_embed(c.type_embd, m->image + m->off_embd, c.n_embd, m->st, m->x, m->rope_cos,
                        m->rope_sin, c.head_dim / 2, m->rope_cur, s));
   for (int il = 0; il < c.n_layer; ++il) {
@@ -293,7 +359,9 @@ int enqueue_step(knj_model* m, hipStream_t s) {
   GemvArgs head{c.type_head, m->image + m->off_head, c.n_embd, c.n_vocab, m->x,
                 reinterpret_cast<const float*>(m->image + m->off_onorm), c.rms_eps, nullptr,
                 m->logits, m->keys};
+  span_scope("head", -1);
   KNJ_HIP(launch_gemv(head, s));
+  span_class("sample");
   KNJ_HIP(launch_step_close(m->st, m->keys, gemv_grid(c.type_head, c.n_embd, c.n_vocab),
                             m->out_tokens, m->max_steps, s));
   return KNJ_OK;
@@ -329,6 +397,7 @@ int set_state(knj_model* m, int32_t token, int step) {
   h.pos = m->pos;
   h.step = step;
   KNJ_HIP(hipMemcpyAsync(m->st, &h, sizeof(h), hipMemcpyHostToDevice, m->stream));
+  m->h2d_bytes += sizeof(h);
   KNJ_HIP(hipStreamSynchronize(m->stream));
   return KNJ_OK;
 }
@@ -525,6 +594,7 @@ int knj_model_create_from_gguf(const char* path, int n_ctx, knj_model** out) {
     const GgufTensor* t = g.find(name);
     if (hipMemcpy(m->image + off, g.data(*t), t->bytes, hipMemcpyHostToDevice) != hipSuccess)
       return hip_fail(hipErrorUnknown, "image upload");
+    m->h2d_bytes += t->bytes;
     return KNJ_OK;
   };
   rc = put("token_embd.weight", m->off_embd);
@@ -577,6 +647,7 @@ int knj_model_create_from_image(const knj_model_config* cfg, const void* image, 
     set_error("image size does not match the configuration's layout");
     return KNJ_E_ARG;
   }
+  m->h2d_bytes += bytes;
   if (hipMemcpy(m->image, image, bytes, hipMemcpyHostToDevice) != hipSuccess) {
     knj_model_free(m);
     return hip_fail(hipErrorUnknown, "image upload");
@@ -601,6 +672,7 @@ const void* knj_model_image_device(const knj_model* m) { return m ? m->image : n
 int knj_model_download_image(const knj_model* m, void* host, uint64_t bytes) {
   KNJ_CHECK_ARG(m && host && bytes == m->image_bytes, "bad image download arguments");
   KNJ_HIP(hipMemcpy(host, m->image, bytes, hipMemcpyDeviceToHost));
+  m->d2h_bytes += bytes;
   return KNJ_OK;
 }
 
@@ -641,6 +713,7 @@ int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_
   if (logits_host) {
     KNJ_HIP(hipMemcpyAsync(logits_host, m->logits, (uint64_t)m->c.n_vocab * 4, hipMemcpyDeviceToHost,
                            m->stream));
+    m->d2h_bytes += (uint64_t)m->c.n_vocab * 4;
   }
   KNJ_HIP(hipStreamSynchronize(m->stream));
   return KNJ_OK;
@@ -676,6 +749,7 @@ int knj_model_decode_greedy(knj_model* m, int32_t first, int steps, int32_t* out
     if ((rc = run_step(m))) return rc;
   m->pos += steps;
   KNJ_HIP(hipMemcpyAsync(out_tokens, m->out_tokens, (uint64_t)steps * 4, hipMemcpyDeviceToHost, m->stream));
+  m->d2h_bytes += (uint64_t)steps * 4;
   KNJ_HIP(hipStreamSynchronize(m->stream));
   return KNJ_OK;
 }
@@ -684,6 +758,7 @@ int knj_model_hidden(const knj_model* m, int il, float* host_out) {
   KNJ_CHECK_ARG(m && host_out && il >= 0 && il < m->c.n_layer, "bad arguments");
   KNJ_HIP(hipMemcpy(host_out, m->hidden + (uint64_t)il * m->c.n_embd, (uint64_t)m->c.n_embd * 4,
                     hipMemcpyDeviceToHost));
+  m->d2h_bytes += (uint64_t)m->c.n_embd * 4;
   return KNJ_OK;
 }
 
@@ -691,13 +766,16 @@ int knj_model_topk(const knj_model* m, int il, int32_t* idx_out, float* w_out) {
   KNJ_CHECK_ARG(m && idx_out && w_out && il >= 0 && il < m->c.n_layer, "bad arguments");
   const uint64_t k = m->c.n_expert_used;
   KNJ_HIP(hipMemcpy(idx_out, m->topk_idx + il * k, k * 4, hipMemcpyDeviceToHost));
+  m->d2h_bytes += k * 4;
   KNJ_HIP(hipMemcpy(w_out, m->topk_w + il * k, k * 4, hipMemcpyDeviceToHost));
+  m->d2h_bytes += k * 4;
   return KNJ_OK;
 }
 
 int knj_model_logits(const knj_model* m, float* host_out) {
   KNJ_CHECK_ARG(m && host_out, "bad arguments");
   KNJ_HIP(hipMemcpy(host_out, m->logits, (uint64_t)m->c.n_vocab * 4, hipMemcpyDeviceToHost));
+  m->d2h_bytes += (uint64_t)m->c.n_vocab * 4;
   return KNJ_OK;
 }
 
@@ -705,7 +783,9 @@ int knj_model_kv_download(const knj_model* m, uint16_t* k_host, uint16_t* v_host
   KNJ_CHECK_ARG(m && k_host && v_host, "bad arguments");
   const uint64_t kv = knj_kv_elems(&m->c) * 2;
   KNJ_HIP(hipMemcpy(k_host, m->kv_k, kv, hipMemcpyDeviceToHost));
+  m->d2h_bytes += kv;
   KNJ_HIP(hipMemcpy(v_host, m->kv_v, kv, hipMemcpyDeviceToHost));
+  m->d2h_bytes += kv;
   return KNJ_OK;
 }
 
@@ -713,7 +793,9 @@ int knj_model_kv_upload(knj_model* m, const uint16_t* k_host, const uint16_t* v_
   KNJ_CHECK_ARG(m && k_host && v_host, "bad arguments");
   const uint64_t kv = knj_kv_elems(&m->c) * 2;
   KNJ_HIP(hipMemcpy(m->kv_k, k_host, kv, hipMemcpyHostToDevice));
+  m->h2d_bytes += kv;
   KNJ_HIP(hipMemcpy(m->kv_v, v_host, kv, hipMemcpyHostToDevice));
+  m->h2d_bytes += kv;
   return KNJ_OK;
 }
 
@@ -775,6 +857,80 @@ int knj_model_time_experts(knj_model* m, int steps, float* us_gateup, float* us_
   const double launches = (double)m->c.n_layer * steps;
   *us_gateup = (float)(gu * 1000.0 / launches);
   *us_down = (float)(dn * 1000.0 / launches);
+  return KNJ_OK;
+}
+
+int knj_model_profile(knj_model* m, int32_t first, int steps, int32_t* out_tokens, knj_span* spans,
+                      int cap, int* n_spans, uint64_t* n_dropped) {
+  KNJ_CHECK_ARG(m && out_tokens && spans && n_spans, "null pointer");
+  KNJ_CHECK_ARG(cap > 0 && cap <= (1 << 20), "span capacity out of range");
+  KNJ_CHECK_ARG(steps > 0 && steps <= m->max_steps, "steps out of range");
+  KNJ_CHECK_ARG(first >= 0 && first < m->c.n_vocab, "token id out of range");
+  if (m->pos + steps > m->c.n_ctx) {
+    set_error("context exhausted");
+    return KNJ_E_ARG;
+  }
+  int rc = set_state(m, first, 0);
+  if (rc) return rc;
+  SpanRun run(cap);
+  if (run.err != hipSuccess) return hip_fail(run.err, "hipEventCreate");
+  KNJ_HIP(hipEventRecord(run.epoch, m->stream));
+  for (int i = 0; i < steps && !rc; ++i) rc = enqueue_step(m, m->stream);
+  run.stop();
+  if (rc) return rc;
+  KNJ_HIP(hipStreamSynchronize(m->stream));
+  m->pos += steps;
+  KNJ_HIP(hipMemcpy(out_tokens, m->out_tokens, (uint64_t)steps * 4, hipMemcpyDeviceToHost));
+  m->d2h_bytes += (uint64_t)steps * 4;
+  return run.collect(spans, cap, n_spans, n_dropped);
+}
+
+int knj_model_transfer_bytes(const knj_model* m, uint64_t* h2d, uint64_t* d2h) {
+  KNJ_CHECK_ARG(m && h2d && d2h, "null pointer");
+  *h2d = m->h2d_bytes;
+  *d2h = m->d2h_bytes;
+  return KNJ_OK;
+}
+
+int knj_device_floor(int n, uint64_t* ns_out) {
+  KNJ_CHECK_ARG(ns_out && n > 0 && n <= 4096, "bad arguments");
+  hipStream_t s = nullptr;
+  KNJ_HIP(hipStreamCreate(&s));
+  std::vector<knj_span> sp((size_t)n);
+  int got = 0, rc = KNJ_OK;
+  // the first launches of a kernel pay for loading its code object; they are
+  // not part of the floor
+  for (int i = 0; i < 8 && !rc; ++i) {
+    hipLaunchKernelGGL(k_span_floor, dim3(1), dim3(64), 0, s, 0);
+    const hipError_t e = hipStreamSynchronize(s);
+    if (e != hipSuccess) rc = hip_fail(e, "k_span_floor");
+  }
+  {
+    SpanRun run(n);
+    if (run.err != hipSuccess) rc = hip_fail(run.err, "hipEventCreate");
+    if (!rc) {
+      const hipError_t e = hipEventRecord(run.epoch, s);
+      if (e != hipSuccess) rc = hip_fail(e, "hipEventRecord");
+    }
+    for (int i = 0; i < n && !rc; ++i) {
+      KNJ_LAUNCH(k_span_floor, dim3(1), dim3(64), 0, s, 0);
+      const hipError_t e = hipGetLastError();
+      if (e != hipSuccess) rc = hip_fail(e, "k_span_floor");
+    }
+    run.stop();
+    if (!rc) {
+      const hipError_t e = hipStreamSynchronize(s);
+      if (e != hipSuccess) rc = hip_fail(e, "hipStreamSynchronize");
+    }
+    if (!rc) rc = run.collect(sp.data(), n, &got, nullptr);
+  }
+  (void)hipStreamDestroy(s);
+  if (rc) return rc;
+  // the median span: robust to the odd launch delayed by the host
+  std::vector<uint64_t> d((size_t)got);
+  for (int i = 0; i < got; ++i) d[(size_t)i] = sp[(size_t)i].end_ns - sp[(size_t)i].start_ns;
+  std::sort(d.begin(), d.end());
+  *ns_out = got ? d[(size_t)got / 2] : 0;
   return KNJ_OK;
 }
 

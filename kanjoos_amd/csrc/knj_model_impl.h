@@ -34,10 +34,28 @@ struct knj_model {
   bool use_graph = true;  // KNJ_NO_GRAPH=1 launches the step's kernels directly
   hipEvent_t* expert_events = nullptr;  // set by knj_model_time_experts: 4 per layer per step
   int expert_slot = 0;
+  // host<->device bytes copied by this model's calls (the profiler's transfer row)
+  mutable uint64_t h2d_bytes = 0, d2h_bytes = 0;
   std::vector<void*> owned;
 };
 
 namespace knj {
+// A profiling run: installs a SpanSink (knj_spans.h) of `cap` event pairs on
+// the calling thread until stop() or destruction; `epoch` is recorded by the
+// caller on the step's stream before the first launch.
+struct SpanRun {
+  explicit SpanRun(int cap);
+  ~SpanRun();
+  SpanRun(const SpanRun&) = delete;
+  SpanRun& operator=(const SpanRun&) = delete;
+  void stop();
+  int collect(knj_span* out, int cap, int* n_out, uint64_t* dropped);
+  SpanSink sink;
+  std::vector<hipEvent_t> events;
+  hipEvent_t epoch = nullptr;
+  hipError_t err = hipSuccess;
+};
+
 // Slots [0, n_elems / D) of `rows` cache rows of row_elems elements: seeded f16
 // values ~N(0, 1) (k_fill_kv).
 int fill_kv_rows(uint16_t* k, uint16_t* v, uint64_t rows, uint64_t row_elems, uint64_t n_elems,

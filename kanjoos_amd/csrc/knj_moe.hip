@@ -656,11 +656,12 @@ int pow2_at_least(int v) {
   return p;
 }
 
-// hipLaunchKernelGGL, or the timed launch when start/stop events are given
+// hipLaunchKernelGGL, or the timed launch when start/stop events are given or
+// a span sink is installed (knj_spans.h)
 template <class F>
-void launch_maybe_timed(F kernel, dim3 grid, size_t lds, hipStream_t s, hipEvent_t t0,
-                        hipEvent_t t1, const ExpertArgs& a) {
-  if (t0)
+void launch_maybe_timed(F kernel, const char* name, dim3 grid, size_t lds, hipStream_t s,
+                        hipEvent_t t0, hipEvent_t t1, const ExpertArgs& a) {
+  if (t0 || span_take(name, &t0, &t1))
     hipExtLaunchKernelGGL(kernel, grid, dim3(kBlock), (uint32_t)lds, s, t0, t1, 0u, a);
   else
     hipLaunchKernelGGL(kernel, grid, dim3(kBlock), lds, s, a);
@@ -671,13 +672,13 @@ void launch_maybe_timed(F kernel, dim3 grid, size_t lds, hipStream_t s, hipEvent
 
 hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
   // four rows (waves) per workgroup; the last workgroup also ranks the experts
-  hipLaunchKernelGGL(k_router, dim3((a.n_expert + 3) / 4), dim3(kBlock), 0, s, a);
+  KNJ_LAUNCH(k_router, dim3((a.n_expert + 3) / 4), dim3(kBlock), 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_topk(const float* logits, int n_expert, int k, int32_t* idx, float* w,
                        hipStream_t s) {
-  hipLaunchKernelGGL(k_topk, dim3(1), dim3(kBlock), 0, s, logits, n_expert, k, idx, w);
+  KNJ_LAUNCH(k_topk, dim3(1), dim3(kBlock), 0, s, logits, n_expert, k, idx, w);
   return hipGetLastError();
 }
 
@@ -686,12 +687,12 @@ hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t
   if (a.n_embd <= 2048) {
     constexpr int RS = 2;
     const int grid = (npairs + 4 * RS - 1) / (4 * RS);
-    launch_maybe_timed(k_expert_gateup<RS>, dim3(grid), 0, s, t0, t1, a);
+    launch_maybe_timed(k_expert_gateup<RS>, "k_expert_gateup", dim3(grid), 0, s, t0, t1, a);
     return hipGetLastError();
   }
   const size_t lds = (size_t)xpad_size(a.n_embd) * 4;
   const int grid = std::min(2048, (npairs + 3) / 4);
-  launch_maybe_timed(k_expert_gateup_wide, dim3(grid), lds, s, t0, t1, a);
+  launch_maybe_timed(k_expert_gateup_wide, "k_expert_gateup_wide", dim3(grid), lds, s, t0, t1, a);
   return hipGetLastError();
 }
 
@@ -705,7 +706,7 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
     if (lds > 65536)                                                                         \
       (void)hipFuncSetAttribute((const void*)k_expert_down<J>,                               \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);       \
-    launch_maybe_timed(k_expert_down<J>, dim3(grid), lds, s, t0, t1, a);                     \
+    launch_maybe_timed(k_expert_down<J>, "k_expert_down", dim3(grid), lds, s, t0, t1, a);                     \
     return hipGetLastError();                                                                \
   }
     GD(1) GD(2) GD(3) GD(4)
@@ -722,7 +723,7 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
     if (lds > 65536)                                                                          \
       (void)hipFuncSetAttribute((const void*)k_expert_down_q6u<J>,                            \
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);        \
-    launch_maybe_timed(k_expert_down_q6u<J>, dim3(grid), lds, s, t0, t1, a);                  \
+    launch_maybe_timed(k_expert_down_q6u<J>, "k_expert_down_q6u", dim3(grid), lds, s, t0, t1, a);                  \
     return hipGetLastError();                                                                 \
   }
     GU(2) GU(4) GU(8)
@@ -734,7 +735,7 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
   const int grid = (a.n_embd + rows_per_block - 1) / rows_per_block;
 #define GQ(L)                                                                                   \
   if (lpr == L) {                                                                               \
-    if (t0)                                                                                     \
+    if (t0 || span_take("k_expert_down_q6k", &t0, &t1))                                         \
       hipExtLaunchKernelGGL(k_expert_down_q6k<L>, dim3(grid), dim3(kBlock), (uint32_t)lds, s, t0, \
                             t1, 0u, a, rows_per_block);                                         \
     else                                                                                        \

@@ -651,26 +651,26 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
 
   const float* xin = a.x;
   if (a.norm_w) {
-    hipLaunchKernelGGL(k_norm_rows, dim3(m), dim3(kBlock), 0, s, a.x, a.norm_w, a.eps, H, hx);
+    KNJ_LAUNCH(k_norm_rows, dim3(m), dim3(kBlock), 0, s, a.x, a.norm_w, a.eps, H, hx);
     xin = hx;
   }
-  hipLaunchKernelGGL(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(kBlock), 0, s, xin,
+  KNJ_LAUNCH(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(kBlock), 0, s, xin,
                      a.router_w, m, H, E, a.logits);
-  hipLaunchKernelGGL(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, a.logits, m, E, K,
+  KNJ_LAUNCH(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, a.logits, m, E, K,
                      a.topk_idx, a.topk_w);
-  hipLaunchKernelGGL(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
+  KNJ_LAUNCH(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
                      pair_of, items, n_items);
-  hipLaunchKernelGGL(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, xin, pair_tok, H,
+  KNJ_LAUNCH(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, xin, pair_tok, H,
                      (int)P, xh, xl, sxh, sxl);
   GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, (int)P, offsets, items, n_items, act};
-  hipLaunchKernelGGL(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+  KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      kGroupLds, s, gu);
-  hipLaunchKernelGGL(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, act, nullptr, F, (int)P,
+  KNJ_LAUNCH(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, act, nullptr, F, (int)P,
                      ah, al, sah, sal);
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
-  hipLaunchKernelGGL(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+  KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      kGroupLds, s, dn);
-  hipLaunchKernelGGL(k_combine, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
+  KNJ_LAUNCH(k_combine, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
                      H, a.resid, a.out);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && a.hidden_copy)
@@ -687,7 +687,7 @@ uint64_t dense_scratch_bytes(int m, int n_in) {
 hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, int n, float* out,
                             hipStream_t s) {
   if (n > 4096 || n % 256) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_norm_rows, dim3(m), dim3(kBlock), 0, s, x, nw, eps, n, out);
+  KNJ_LAUNCH(k_norm_rows, dim3(m), dim3(kBlock), 0, s, x, nw, eps, n, out);
   return hipGetLastError();
 }
 
@@ -707,13 +707,13 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
   _Float16* sh = (_Float16*)take(P * n_in / 16);
   _Float16* sl = (_Float16*)take(P * n_in / 16);
   int* meta = (int*)take(1024);  // offsets {0, m}, n_items, items
-  hipLaunchKernelGGL(k_split_pairs, dim3(m), dim3(kBlock), 0, s, x, nullptr, n_in, m, xh, xl, sh,
+  KNJ_LAUNCH(k_split_pairs, dim3(m), dim3(kBlock), 0, s, x, nullptr, n_in, m, xh, xl, sh,
                      sl);
-  hipLaunchKernelGGL(k_dense_meta, dim3(1), dim3(64), 0, s, m, meta);
+  KNJ_LAUNCH(k_dense_meta, dim3(1), dim3(64), 0, s, m, meta);
   GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, meta, (const int2*)(meta + 64), meta + 2,
               out, resid};
   const int tiles = (m + kTok - 1) / kTok;
-  hipLaunchKernelGGL(k_group_q4k<false>, dim3((n_out + kRowsWG - 1) / kRowsWG, tiles),
+  KNJ_LAUNCH(k_group_q4k<false>, dim3((n_out + kRowsWG - 1) / kRowsWG, tiles),
                      dim3(kBlock), kGroupLds, s, g);
   return hipGetLastError();
 }
@@ -731,8 +731,8 @@ hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, cons
   uint16_t* xh = (uint16_t*)take(P * n_in * 2);
   uint16_t* xm = (uint16_t*)take(P * n_in * 2);
   uint16_t* xl = (uint16_t*)take(P * n_in * 2);
-  hipLaunchKernelGGL(k_split_bf16x3, dim3(m), dim3(kBlock), 0, s, x, n_in, m, xh, xm, xl);
-  hipLaunchKernelGGL(k_dense_bf16, dim3((n_out + kRowsWG - 1) / kRowsWG, (m + kTok - 1) / kTok),
+  KNJ_LAUNCH(k_split_bf16x3, dim3(m), dim3(kBlock), 0, s, x, n_in, m, xh, xm, xl);
+  KNJ_LAUNCH(k_dense_bf16, dim3((n_out + kRowsWG - 1) / kRowsWG, (m + kTok - 1) / kTok),
                      dim3(kBlock), 0, s, w, n_in, n_out, m, xh, xm, xl, out);
   return hipGetLastError();
 }
@@ -742,8 +742,8 @@ int argmax_key_count(int n) { return (n + kArgChunk - 1) / kArgChunk; }
 hipError_t launch_argmax_rows(const float* logits, int m, int n, unsigned long long* keys,
                               int32_t* tok, hipStream_t s) {
   const int nk = argmax_key_count(n);
-  hipLaunchKernelGGL(k_argmax_part, dim3(nk, m), dim3(kBlock), 0, s, logits, n, keys);
-  hipLaunchKernelGGL(k_argmax_final, dim3(m), dim3(64), 0, s, keys, nk, tok);
+  KNJ_LAUNCH(k_argmax_part, dim3(nk, m), dim3(kBlock), 0, s, logits, n, keys);
+  KNJ_LAUNCH(k_argmax_final, dim3(m), dim3(64), 0, s, keys, nk, tok);
   return hipGetLastError();
 }
 

@@ -6,7 +6,15 @@
 // the seeded synthetic Qwen3-30B-A3B-shaped model.
 //
 //   kanjoos-run [--layers N] [--ctx N] [--seed S] [--prompt N] [--n-predict N]
-//               [--bench PP TG] [--small] [--model PATH.gguf]
+//               [--bench PP TG] [--small] [--model PATH.gguf] [--fill-kv N]
+//               [--profiling[=table|json|csv|no-subtract|off]] [--profile-dir DIR]
+//               [--profile-floor N] [--profile-warmup N] [--profile-detail=class|layer|kernel]
+//
+// --profiling (main.cpp:47-56, 94-98, 198-223, 314-318) times the decode with
+// a dispatch event pair around every kernel launch (Model::decode_greedy_profiled)
+// and prints the profiler's report before the token line; the tokens are the
+// same as without it.
+#include <algorithm>
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
@@ -17,12 +25,15 @@
 
 #include "../../include/knj/backend.h"
 #include "../../include/knj/model.h"
+#include "../../include/knj/profiler.h"
+#include "../../include/knj/residency.h"
 
 int main(int argc, char** argv) {
-  int layers = 48, ctx = 4352, prompt = 16, n_predict = 32, pp = 0, tg = 0;
+  int layers = 48, ctx = 4352, prompt = 16, n_predict = 32, pp = 0, tg = 0, fill_kv = 0;
   uint64_t seed = 0;
   bool small = false;
   std::string model_path;  // --model PATH: a qwen3moe GGUF instead of synthetic weights
+  knj::ProfileConfig pc;
   for (int i = 1; i < argc; ++i) {
     const std::string a = argv[i];
     auto next = [&](const char* name) {
@@ -37,6 +48,7 @@ int main(int argc, char** argv) {
     else if (a == "--seed") seed = (uint64_t)next("--seed");
     else if (a == "--prompt") prompt = next("--prompt");
     else if (a == "--n-predict") n_predict = next("--n-predict");
+    else if (a == "--fill-kv") fill_kv = next("--fill-kv");
     else if (a == "--small") small = true;
     else if (a == "--model") {
       if (i + 1 >= argc) {
@@ -45,7 +57,31 @@ int main(int argc, char** argv) {
       }
       model_path = argv[++i];
     }
-    else if (a == "--bench") {
+    else if (a == "--profile-dir") {
+      if (i + 1 >= argc) {
+        std::fprintf(stderr, "--profile-dir needs a value\n");
+        return 2;
+      }
+      pc.dir = argv[++i];
+    } else if (a == "--profile-floor") pc.floor_ops = next("--profile-floor");
+    else if (a == "--profile-warmup") pc.warmup_steps = next("--profile-warmup");
+    else if (a.rfind("--profile-detail=", 0) == 0) {
+      pc.detail = a.substr(17);
+      if (pc.detail != "class" && pc.detail != "layer" && pc.detail != "kernel") {
+        std::fprintf(stderr, "--profile-detail must be class, layer or kernel\n");
+        return 2;
+      }
+    } else if (a == "--profiling" || a.rfind("--profiling=", 0) == 0) {
+      const std::string fmt = a.size() > 12 ? a.substr(12) : "table";
+      pc.on = fmt != "off";
+      pc.format = "table";
+      if (fmt == "no-subtract") pc.subtract_floor = false;
+      else if (fmt == "json" || fmt == "csv") pc.format = fmt;
+      else if (fmt != "table" && fmt != "off") {
+        std::fprintf(stderr, "--profiling=%s: expected off|table|json|csv|no-subtract\n", fmt.c_str());
+        return 2;
+      }
+    } else if (a == "--bench") {
       pp = next("--bench");
       tg = next("--bench");
     } else {
@@ -106,8 +142,39 @@ int main(int argc, char** argv) {
       (void)out;
       return 0;
     }
-    const int first = run_prompt(prompt);
-    const auto out = m->decode_greedy(first, n_predict);
+    // --fill-kv N: start from a seeded N-token context (the decode benchmarks'
+    // long-context state) instead of position 0
+    if (fill_kv > 0) m->fill_kv(fill_kv, seed);
+    knj::Profiler& prof = knj::Profiler::get();
+    prof.configure(pc);
+    if (pc.on) {
+      prof.enable_device_backend();
+      uint64_t floor_ns = 0;
+      const int floor_n = pc.floor_ops > 0 ? std::min(pc.floor_ops, 4096) : 0;
+      if (floor_n > 0 && knj_device_floor(floor_n, &floor_ns) == KNJ_OK)
+        prof.set_device_floor(floor_ns, floor_n);
+      prof.measure_floor();
+    }
+    int first = 0;
+    {
+      KNJ_PROFILE_OP("prefill");
+      first = run_prompt(prompt);
+    }
+    std::vector<int32_t> out;
+    {
+      KNJ_PROFILE_OP("decode");
+      out = pc.on ? m->decode_greedy_profiled(first, n_predict, prof)
+                  : m->decode_greedy(first, n_predict);
+    }
+    if (pc.on) {
+      const knj::ModelGeometry& g = m->geom();
+      knj::ResidencyManager res((uint32_t)g.n_layer, (uint32_t)g.n_expert, (uint32_t)m->n_ctx(), 256);
+      prof.note_residency(res.stats());
+      prof.note_transfer(m->transfer_stats());
+      prof.print_header(stdout, "0.1", "gfx950", g.describe());
+      prof.report(stdout);
+      prof.write_dir();
+    }
     std::printf("tokens:");
     for (int32_t t : out) std::printf(" %d", t);
     std::printf("\n");

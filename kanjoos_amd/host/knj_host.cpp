@@ -1,4 +1,5 @@
 // kanjoos_amd/host/knj_host.cpp -- C++ host classes (Model, Backend) over the C ABI.
+#include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -81,6 +82,55 @@ std::unique_ptr<Model> Model::open_image(const knj_model_config& cfg, const void
   m->n_ctx_ = c.n_ctx;
   m->logits_.assign((size_t)c.n_vocab, 0.0f);
   return m;
+}
+
+std::vector<int32_t> Model::decode_greedy_profiled(int32_t first, int steps, Profiler& prof) {
+  if (steps <= 0) throw std::runtime_error("model: steps must be positive");
+  std::vector<int32_t> out;
+  out.reserve((size_t)steps);
+  // one step's launches: 2 per layer for attention and 5 more per layer, plus
+  // embed, head and sample; the ring is sized with room to spare
+  const int cap = 8 * g_.n_layer + 16;
+  std::vector<knj_span> sp((size_t)cap);
+  uint64_t base = 0;
+  int32_t tok = first;
+  for (int i = 0; i < steps; ++i) {
+    int n = 0;
+    uint64_t dropped = 0;
+    int32_t next = 0;
+    check(knj_model_profile(m_, tok, 1, &next, sp.data(), cap, &n, &dropped), "profile");
+    const bool kept = prof.steps_kept() + prof.steps_discarded() >= (uint64_t)prof.config().warmup_steps;
+    uint64_t last = 0;
+    for (int j = 0; j < n; ++j) {
+      const knj_span& s = sp[(size_t)j];
+      last = std::max(last, s.end_ns);
+      if (!kept) continue;
+      std::string k(s.kernel);
+      const size_t lt = k.find('<');
+      if (lt != std::string::npos) k.resize(lt);
+      char name[128];
+      if (s.layer >= 0)
+        std::snprintf(name, sizeof(name), "%s:%d:%s", s.name, s.layer, k.c_str());
+      else
+        std::snprintf(name, sizeof(name), "%s:-:%s", s.name, k.c_str());
+      prof.device_span(name, base + s.start_ns, base + s.end_ns, s.stream);
+    }
+    if (kept && dropped) prof.set_device_dropped(prof.device_dropped() + dropped);
+    base += last;
+    prof.step_done();
+    out.push_back(next);
+    tok = next;
+  }
+  return out;
+}
+
+void Model::fill_kv(int n_pos, uint64_t seed) { check(knj_model_fill_kv(m_, n_pos, seed), "fill_kv"); }
+
+TransferStats Model::transfer_stats() const {
+  TransferStats t;
+  check(knj_model_transfer_bytes(m_, &t.h2d_bytes, &t.d2h_bytes), "transfer stats");
+  t.measured = true;
+  return t;
 }
 
 Model::~Model() {

@@ -416,3 +416,62 @@ def test_batch_greedy_matches_single(device):
         have = [int(first[s_])] + [int(t) for t in got[:, s_]]
         assert have == want, (s_, have, want)
     gm.close()
+
+
+def test_profile_spans(device):
+    """knj_model_profile: the same greedy tokens as the graph replay, one span
+    per kernel launch, every layer's ops named, spans in stream order without
+    overlap, and the span total inside the wall time of the step."""
+    cfg = small_config()
+    say(f"profile spans {cfg}")
+    a = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    b = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    try:
+        a.forward([3, 4])
+        b.forward([3, 4])
+        want = a.decode_greedy(7, 6)
+        got, spans, dropped = b.profile(7, 6)
+        assert list(got) == list(want)
+        assert dropped == 0
+        per_step = len(spans) // 6
+        assert per_step * 6 == len(spans)
+        step0 = spans[:per_step]
+        assert step0[0][0] == "embed" and step0[-1][0] == "sample" and step0[-2][0] == "head"
+        for il in range(cfg["n_layer"]):
+            names = {s[0] for s in step0 if s[1] == il}
+            assert names == {"qkv", "attention", "attn-o", "moe-router", "moe-gate+up+act",
+                             "moe-down+scatter"}, (il, names)
+        for s0, s1 in zip(spans, spans[1:]):
+            assert s0[3] <= s0[4] <= s1[3] + 1000, (s0, s1)  # 1 us of event rounding
+        busy = sum(s[4] - s[3] for s in spans)
+        assert 0 < busy <= spans[-1][4] - spans[0][3] + 1000 * len(spans)
+        gate = [s[4] - s[3] for s in spans if s[0] == "moe-gate+up+act"]
+        assert all(0 < d < 1_000_000 for d in gate)
+        h2d, d2h = b.transfer_bytes()
+        assert d2h >= 4 * 6 and h2d > 0  # synthetic weights are generated on the device
+        assert 0 < K.device_floor(64) < 50_000
+    finally:
+        a.close()
+        b.close()
+
+
+def test_cpp_driver_profiling(device, tmp_path):
+    """kanjoos-run --profiling prints the device-domain table and writes the
+    profile files; the tokens are the ones of the run without it."""
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(K.LIB_PATH), "kanjoos-run")
+    base = [exe, "--small", "--layers", "2", "--ctx", "64", "--prompt", "8", "--n-predict", "16"]
+    plain = subprocess.run(base, capture_output=True, text=True, timeout=60)
+    prof = subprocess.run(base + ["--profiling", "--profile-warmup", "4", "--profile-dir",
+                                  str(tmp_path)], capture_output=True, text=True, timeout=60)
+    say(prof.stdout + prof.stderr)
+    assert plain.returncode == 0 and prof.returncode == 0
+    assert plain.stdout.strip().splitlines()[-1] == prof.stdout.strip().splitlines()[-1]
+    assert "clock domain: device" in prof.stdout and "moe-gate+up+act" in prof.stdout
+    assert "0 dropped" in prof.stdout
+    data = json.load(open(tmp_path / "profile.json"))
+    assert data["device_backend"] and data["steps_kept"] == 12 and data["steps_discarded"] == 4
+    comps = {c["component"]: c for c in data["components"]}
+    assert comps["qkv"]["dev_ns"] > 0 and comps["decode"]["host_ns"] > 0
+    assert data["residency"]["vram_pct"] == 100.0 and data["transfer"]["h2d_bytes"] > 0
