@@ -180,49 +180,120 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   __shared__ float xs[xpad_size(2048)];
   __shared__ float xsum[64];  // sums of the 32-element sub-blocks of the normalised x
   __shared__ int sel[16];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __shared__ float selp[16];
+  __shared__ unsigned long long ckey[256];  // candidate keys
+  __shared__ uint32_t gmax[32];
+  __shared__ uint32_t gthr;
+  __shared__ int ncand;
+  __shared__ float red[3][4];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   KNJ_STAMP(0);
-  // 1) wave 0 alone: x, its norm weight and the logits; the routing; x
-  // normalised into LDS.  The other waves have nothing outstanding at the
-  // barrier, so their weight loads issue as soon as the experts are known.
-  int my_idx = 0;
-  float my_w = 0.0f;
-  if (wave == 0) {
-    const int nj = a.n_embd >> 8;  // float4 per lane (n_embd <= 2048)
-    float4 xv[8], wv[8];
+  // 1) the whole workgroup routes and stages x before any weight is loaded.
+  // Loads first: thread t holds the logit of expert t and float4s t, t + 256
+  // of x and of its norm weight (n_embd <= 2048, n_expert <= 256).
+  const bool route = a.logits != nullptr;
+  const int H = a.n_embd, E = a.n_expert;
+  float4 x4[2], w4[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j < nj) {
-        xv[j] = *reinterpret_cast<const float4*>(a.hx + 4 * lane + 256 * j);
-        if (a.norm_w) wv[j] = *reinterpret_cast<const float4*>(a.norm_w + 4 * lane + 256 * j);
+  for (int j = 0; j < 2; ++j) {
+    const int i4 = t + kBlock * j;
+    x4[j] = 4 * i4 < H ? *reinterpret_cast<const float4*>(a.hx + 4 * i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    w4[j] = (a.norm_w && 4 * i4 < H) ? *reinterpret_cast<const float4*>(a.norm_w + 4 * i4)
+                                      : make_float4(1.f, 1.f, 1.f, 1.f);
+  }
+  const float lg = (route && t < E) ? a.logits[t] : -INFINITY;
+  if (t == 0) ncand = 0;
+  const int given = (!route && t < a.k) ? a.topk_idx[t] : 0;
+  // softmax max and the sum of squares of x: one reduction round
+  float ss = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) ss += x4[j].x * x4[j].x + x4[j].y * x4[j].y + x4[j].z * x4[j].z + x4[j].w * x4[j].w;
+  ss = group_sum<64>(ss);
+  const float wmax = group_max<64>(lg);
+  if (lane == 0) {
+    red[0][wave] = wmax;
+    red[1][wave] = ss;
+  }
+  __syncthreads();
+  const float mx = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3]));
+  const float ex = (route && t < E) ? expf(lg - mx) : 0.0f;
+  const float wsum = group_sum<64>(ex);
+  if (lane == 0) red[2][wave] = wsum;
+  // x normalised into LDS meanwhile, with the 32-element sub-block sums
+  {
+    const float sst = ((red[1][0] + red[1][1]) + red[1][2]) + red[1][3];
+    const float scale = 1.0f / sqrtf(sst / (float)H + a.eps);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i4 = t + kBlock * j;
+      float4 o = x4[j];
+      if (a.norm_w) {
+        o.x = x4[j].x * scale * w4[j].x;
+        o.y = x4[j].y * scale * w4[j].y;
+        o.z = x4[j].z * scale * w4[j].z;
+        o.w = x4[j].w * scale * w4[j].w;
       }
-    if (a.logits) {
-      wave_route(a.logits, a.n_expert, a.k, my_idx, my_w);
-    } else if (lane < a.k) {
-      my_idx = a.topk_idx[lane];
+      // eight consecutive threads hold one sub-block
+      const float sb = group_sum<8>((o.x + o.y) + (o.z + o.w));
+      if (4 * i4 < H) {
+        *reinterpret_cast<float4*>(xs + xpad(4 * i4)) = o;
+        if ((lane & 7) == 0) xsum[(4 * i4) >> 5] = sb;
+      }
     }
-    if (lane < a.k) sel[lane] = my_idx;
-    float ss = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j < nj) ss += xv[j].x * xv[j].x + xv[j].y * xv[j].y + xv[j].z * xv[j].z + xv[j].w * xv[j].w;
-    ss = group_sum<64>(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)a.n_embd + a.eps);
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (j < nj) {
-        float4 o = xv[j];
-        if (a.norm_w) {
-          o.x = xv[j].x * scale * wv[j].x;
-          o.y = xv[j].y * scale * wv[j].y;
-          o.z = xv[j].z * scale * wv[j].z;
-          o.w = xv[j].w * scale * wv[j].w;
-        }
-        *reinterpret_cast<float4*>(xs + xpad(4 * lane + 256 * j)) = o;
-        // eight consecutive lanes hold one sub-block
-        const float t = group_sum<8>((o.x + o.y) + (o.z + o.w));
-        if ((lane & 7) == 0) xsum[(4 * lane + 256 * j) >> 5] = t;
+  }
+  __syncthreads();
+  // Selection of the k largest probabilities, ties to the lower index
+  // (strict > over ascending experts, model.cpp:442-451).  A key is the bits
+  // of p (non-negative, so they order like the values) above the complement
+  // of the index.  Candidates first: the maxima of the n_group groups of 8
+  // experts are n_group distinct experts, so when n_group >= k the k-th
+  // largest of them is at most the k-th largest probability, and every
+  // selected expert is at or above it.  Only the candidates are ranked.
+  const float sum = ((red[2][0] + red[2][1]) + red[2][2]) + red[2][3];
+  const float p = (route && t < E) ? ex / sum : 0.0f;
+  if (route) {
+    const unsigned long long key =
+        t < E ? ((unsigned long long)__float_as_uint(p) << 32) | (0xFFFFFFFFu - (unsigned)t) : 0ull;
+    const uint32_t pb = t < E ? __float_as_uint(p) + 1u : 0u;  // 0: no expert
+    uint32_t gm = max(pb, dpp_u32<kDppXor1>(pb));
+    gm = max(gm, dpp_u32<kDppXor2>(gm));
+    gm = max(gm, dpp_u32<kDppHalfMirror>(gm));
+    const int n_group = (E + 7) >> 3;
+    if ((t & 7) == 0 && (t >> 3) < n_group) gmax[t >> 3] = gm;
+    __syncthreads();
+    // the k-th largest group maximum (ties by group order), or 0 (everyone)
+    if (t < n_group && n_group >= a.k) {
+      const uint32_t mine = gmax[t];
+      int r = 0;
+      for (int g2 = 0; g2 < n_group; ++g2) {
+        const uint32_t o = gmax[g2];
+        r += (o > mine || (o == mine && g2 < t)) ? 1 : 0;
       }
+      if (r == a.k - 1) gthr = mine;
+    }
+    __syncthreads();
+    const uint32_t thr = n_group >= a.k ? gthr : 0u;
+    if (t < E && pb >= thr) ckey[atomicAdd(&ncand, 1)] = key;
+    __syncthreads();
+    // each candidate counts the larger candidate keys (order of the list is
+    // immaterial), sixteen loads in flight per pass
+    const int n_cand = ncand;
+    if (t < E && pb >= thr) {
+      int rank = 0;
+      for (int b0 = 0; b0 < n_cand; b0 += 16) {
+        unsigned long long kv[16];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) kv[j] = ckey[min(b0 + j, n_cand - 1)];
+#pragma unroll
+        for (int j = 0; j < 16; ++j) rank += (b0 + j < n_cand && kv[j] > key) ? 1 : 0;
+      }
+      if (rank < a.k) {
+        sel[rank] = t;
+        selp[rank] = p;
+      }
+    }
+  } else if (t < a.k) {
+    sel[t] = given;
   }
   __syncthreads();
   KNJ_STAMP(1);
@@ -277,9 +348,14 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   }
   // the routing, for the down launch and the caller (kept until now so no
   // wave waits on these stores before its loads)
-  if (a.logits && blockIdx.x == 0 && wave == 0 && lane < a.k) {
-    a.topk_idx[lane] = my_idx;
-    a.topk_w[lane] = my_w;
+  if (route && blockIdx.x == 0 && t < a.k) {
+    // weights renormalised over the kept probabilities, summed in selection
+    // order (model.cpp:452-458)
+    float keep = 0.0f;
+    for (int q = 0; q < a.k; ++q) keep += selp[q];
+    const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
+    a.topk_idx[t] = sel[t];
+    a.topk_w[t] = selp[t] * inv;
   }
   KNJ_STAMP(4);
 }

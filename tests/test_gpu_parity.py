@@ -475,3 +475,48 @@ def test_cpp_driver_profiling(device, tmp_path):
     comps = {c["component"]: c for c in data["components"]}
     assert comps["qkv"]["dev_ns"] > 0 and comps["decode"]["host_ns"] > 0
     assert data["residency"]["vram_pct"] == 100.0 and data["transfer"]["h2d_bytes"] > 0
+
+
+@pytest.mark.parametrize("case", ["all_equal", "equal_rows", "two_groups"])
+def test_moe_routing_ties(device, config1_weights, case):
+    """Routing on the device when probabilities tie exactly: equal
+    probabilities keep the lower expert first (Model::moe's strict > over
+    ascending experts), here against the oracle, which is pinned to that rule
+    on the CPU.  The candidate filter of the device top-k sees every group
+    maximum equal in the first case and a threshold shared by many experts in
+    the others."""
+    n_embd, n_ff, n_expert, k = 2048, 768, 128, 8
+    x, router, gate, up, down = config1_weights
+    r0 = np.frombuffer(np.ascontiguousarray(router).tobytes(), np.float32).reshape(n_expert, n_embd)
+    ones = np.ones(n_embd, np.float32)
+    hx = O.rmsnorm(x, ones, 1e-6)
+    # rows along the normalised input give the largest logits (about 2 and 1)
+    big = (hx * np.float32(0.001)).astype(np.float32)
+    r = r0 * np.float32(0.01)
+    if case == "all_equal":
+        r[:] = 0.0
+    elif case == "equal_rows":  # five equal leaders, then the ordinary rows
+        for e in (100, 37, 64, 5, 120):
+            r[e] = big
+    else:  # five equal leaders and six equal runners-up straddling eighth place
+        for e in (9, 17, 33, 70, 101):
+            r[e] = big
+        for e in (2, 50, 90, 127, 11, 60):
+            r[e] = big * np.float32(0.5)
+    r = np.ascontiguousarray(r).view(router.dtype).reshape(router.shape)
+    _, _, ti_w, tw_w = O.moe(hx, r, gate, up, down, n_embd, n_ff, n_expert, k)
+    d = {n: K.DeviceBuffer.from_array(a) for n, a in
+         dict(x=x, router=r, gate=gate, up=up, down=down, ones=ones).items()}
+    out = K.DeviceBuffer(4 * n_embd)
+    logits = K.DeviceBuffer(4 * n_expert)
+    ti = K.DeviceBuffer(4 * k)
+    tw = K.DeviceBuffer(4 * k)
+    K.moe_decode_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], n_embd, n_ff, n_expert, k,
+                       out, logits, ti, tw, norm_w=d["ones"], eps=1e-6)
+    got = list(ti.download(np.int32))
+    say(f"{case}: device {got} oracle {list(ti_w[0])}")
+    assert got == list(ti_w[0])
+    want = {"all_equal": list(range(8)), "equal_rows": [5, 37, 64, 100, 120],
+            "two_groups": [9, 17, 33, 70, 101, 2, 11, 50]}[case]
+    assert got[:len(want)] == want
+    assert np.allclose(tw.download(np.float32), tw_w[0], rtol=1e-6, atol=0)
