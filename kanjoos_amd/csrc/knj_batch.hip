@@ -241,7 +241,8 @@ int knj_batch_create(knj_model* m, int n_seq, int n_ctx, knj_batch** out) {
   A((void**)&b->kv_k, kv);
   A((void**)&b->kv_v, kv);
   const uint64_t scr = std::max({moe_batch_scratch_bytes(B, H, c.n_ff, c.n_expert, c.n_expert_used),
-                                 dense_scratch_bytes(B, std::max(H, QD))});
+                                 dense_scratch_bytes(B, H, QKV), dense_scratch_bytes(B, QD, H),
+                                 dense_scratch_bytes(B, H, 0)});
   A(&b->scratch, scr);
   if (!rc && (hipMemset(b->kv_k, 0, kv) != hipSuccess || hipMemset(b->kv_v, 0, kv) != hipSuccess))
     rc = KNJ_E_HIP;

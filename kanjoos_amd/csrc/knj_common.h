@@ -134,8 +134,10 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
 
 // Dense GEMMs over m rows at once (the batched decode step), on the matrix
 // cores with split-f16 (Q4_K) or split-bf16 (bf16 weights) activations:
-// out[r] (+= resid[r]) = W x_r.  Scratch: dense_scratch_bytes(m, n_in).
-uint64_t dense_scratch_bytes(int m, int n_in);
+// out[r] (+= resid[r]) = W x_r.  Scratch: dense_scratch_bytes(m, n_in, n_out)
+// (Q4_K; the split-f16 operands and, when the reduction is split over several
+// workgroups, their partial products), dense_scratch_bytes(m, n_in, 0) for bf16.
+uint64_t dense_scratch_bytes(int m, int n_in, int n_out);
 hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, int n, float* out,
                             hipStream_t s);
 hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const float* x,

@@ -253,6 +253,12 @@ struct GroupArgs {
   const int* n_items;
   float* out;               // [pairs][n_out]
   const float* resid = nullptr;  // optional [pairs][n_out] added to out (may alias out)
+  // Split over the reduction (dense, not gate/up): blockIdx.z = k-range of
+  // super-blocks [z * nsb / ksplit, (z + 1) * nsb / ksplit); with ksplit > 1
+  // the workgroup writes its product to partial[z][pairs][n_out] (no
+  // residual) and k_ksum adds the ranges in order.
+  int ksplit = 1;
+  float* partial = nullptr;
 };
 
 // Workgroup = one tile of kTok pairs of one expert x kRowsWG weight rows; wave
@@ -288,9 +294,11 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
   const bool rows_ok = rbase < a.n_out;  // waves past the last row still stage and sync
   const int row = min(rbase + (lane & 31), a.n_out - 1), kh = lane >> 5;
   const int j = lane & 31;
-  const int nsb = a.n_in >> 8;
+  const int nsb_all = a.n_in >> 8;
+  const int kz = GATEUP ? 0 : (int)blockIdx.z;
+  const int sbb = kz * nsb_all / a.ksplit, nsb = (kz + 1) * nsb_all / a.ksplit;  // [sbb, nsb)
   const uint64_t P = (uint64_t)a.P;
-  const uint64_t rb = (uint64_t)nsb * KNJ_Q4K_BLOCK;
+  const uint64_t rb = (uint64_t)nsb_all * KNJ_Q4K_BLOCK;
   const uint64_t slab = rb * (uint64_t)a.n_out;
   const uint8_t* wr0 = a.w0 + (uint64_t)e * slab + (uint64_t)row * rb;
   const uint8_t* wr1 = GATEUP ? a.w1 + (uint64_t)e * slab + (uint64_t)row * rb : wr0;
@@ -319,19 +327,19 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
   // branches: an array live across divergent code is placed in scratch)
   uint4 st[8], ss;
   WBlock w0c, w1c, w0n, w1n;
-  // prologue: super-block 0
+  // prologue: the first super-block of the range
 #pragma unroll
-  for (int u = 0; u < 8; ++u) st[u] = *a_src(0, u);
-  ss = *s_src(0);
-  w_load(wr0, 0, w0c);
-  if constexpr (GATEUP) w_load(wr1, 0, w1c);
+  for (int u = 0; u < 8; ++u) st[u] = *a_src(sbb, u);
+  ss = *s_src(sbb);
+  w_load(wr0, sbb, w0c);
+  if constexpr (GATEUP) w_load(wr1, sbb, w1c);
 #pragma unroll
   for (int u = 0; u < 8; ++u) *a_dst(0, u) = st[u];
   if (t < 64) lds[2 * kPart + t] = ss;
   __syncthreads();
   f32x16 acc0 = {}, acc1 = {};
-  for (int sb = 0; sb < nsb; ++sb) {
-    const int buf = sb & 1;
+  for (int sb = sbb; sb < nsb; ++sb) {
+    const int buf = (sb - sbb) & 1;
     const int nx = min(sb + 1, nsb - 1);  // the last iteration reloads its own block, unused
 #pragma unroll
     for (int u = 0; u < 8; ++u) st[u] = *a_src(nx, u);
@@ -421,9 +429,34 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
       float v = acc0[i];
       if constexpr (GATEUP) v = (v / (1.0f + expf(-v))) * acc1[i];
       const uint64_t o = (uint64_t)(p0 + tj) * a.n_out + row;
-      a.out[o] = a.resid ? a.resid[o] + v : v;
+      if (!GATEUP && a.ksplit > 1)
+        a.partial[(uint64_t)kz * P * a.n_out + o] = v;
+      else
+        a.out[o] = a.resid ? a.resid[o] + v : v;
     }
   }
+}
+
+// out[i] = resid[i] + sum_z partial[z][i], the ranges added in order (resid
+// may alias out).
+__global__ __launch_bounds__(kBlock) void k_ksum(const float* __restrict__ partial, int ksplit,
+                                                 uint64_t n, const float* resid, float* out) {
+  const uint64_t i4 = ((uint64_t)blockIdx.x * kBlock + threadIdx.x) * 4;
+  if (i4 >= n) return;  // n is a multiple of 4
+  float4 v[16];
+#pragma unroll
+  for (int z = 0; z < 16; ++z)
+    if (z < ksplit) v[z] = *reinterpret_cast<const float4*>(partial + (uint64_t)z * n + i4);
+  float4 r = resid ? *reinterpret_cast<const float4*>(resid + i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int z = 0; z < 16; ++z)
+    if (z < ksplit) {
+      r.x += v[z].x;
+      r.y += v[z].y;
+      r.z += v[z].z;
+      r.w += v[z].w;
+    }
+  *reinterpret_cast<float4*>(out + i4) = r;
 }
 
 // ------------------------------------------------------------------ bf16 weights (LM head)
@@ -679,9 +712,21 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
 }
 
 // ---- dense batched GEMMs of the batched decode step
-uint64_t dense_scratch_bytes(int m, int n_in) {
+// Ranges of the reduction a dense Q4_K product is split into: enough
+// workgroups for the chip (at most 16 ranges, at most one per super-block).
+int dense_ksplit(int m, int n_in, int n_out) {
+  if (m <= 0 || n_out <= 0) return 1;
+  const int tiles = (m + kTok - 1) / kTok, rows = (n_out + kRowsWG - 1) / kRowsWG;
+  const int want = (256 + tiles * rows - 1) / (tiles * rows);
+  return std::max(1, std::min({want, n_in >> 8, 16}));
+}
+
+uint64_t dense_scratch_bytes(int m, int n_in, int n_out) {
   const uint64_t P = (uint64_t)m;
-  return 4 * ((P * n_in * 2 + 255) & ~255ull) + 2 * ((P * n_in / 16 + 255) & ~255ull) + 1024;
+  const int ks = dense_ksplit(m, n_in, n_out);
+  const uint64_t part = ks > 1 ? (uint64_t)ks * P * n_out * 4 : 0;
+  return 4 * ((P * n_in * 2 + 255) & ~255ull) + 2 * ((P * n_in / 16 + 255) & ~255ull) + 1024 +
+         ((part + 255) & ~255ull);
 }
 
 hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, int n, float* out,
@@ -707,14 +752,23 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
   _Float16* sh = (_Float16*)take(P * n_in / 16);
   _Float16* sl = (_Float16*)take(P * n_in / 16);
   int* meta = (int*)take(1024);  // offsets {0, m}, n_items, items
+  const int ks = dense_ksplit(m, n_in, n_out);
+  float* part = ks > 1 ? (float*)take((uint64_t)ks * P * n_out * 4) : nullptr;
   KNJ_LAUNCH(k_split_pairs, dim3(m), dim3(kBlock), 0, s, x, nullptr, n_in, m, xh, xl, sh,
                      sl);
   KNJ_LAUNCH(k_dense_meta, dim3(1), dim3(64), 0, s, m, meta);
   GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, meta, (const int2*)(meta + 64), meta + 2,
               out, resid};
+  g.ksplit = ks;
+  g.partial = part;
   const int tiles = (m + kTok - 1) / kTok;
-  KNJ_LAUNCH(k_group_q4k<false>, dim3((n_out + kRowsWG - 1) / kRowsWG, tiles),
+  KNJ_LAUNCH(k_group_q4k<false>, dim3((n_out + kRowsWG - 1) / kRowsWG, tiles, ks),
                      dim3(kBlock), kGroupLds, s, g);
+  if (ks > 1) {
+    const uint64_t n = P * n_out;
+    KNJ_LAUNCH(k_ksum, dim3((unsigned)((n / 4 + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, part, ks,
+               n, resid, out);
+  }
   return hipGetLastError();
 }
 
