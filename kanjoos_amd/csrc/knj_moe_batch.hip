@@ -612,13 +612,32 @@ __global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
         ws[r] = wt[s];
       }
   }
-  for (int i = threadIdx.x; i < n; i += kBlock) {
-    float o = 0.0f;
+  // one float4 of columns per thread (blockIdx.y picks the 4 * kBlock-column
+  // range): every slot's load is issued before the first use
+  const int i = 4 * (blockIdx.y * kBlock + threadIdx.x);
+  if (i >= n) return;
+  float4 v[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r)
-      if (r < k) o = __fadd_rn(o, __fmul_rn(ws[r], y[(uint64_t)ps[r] * n + i]));
-    out[(uint64_t)t * n + i] = resid ? __fadd_rn(resid[(uint64_t)t * n + i], o) : o;
+  for (int r = 0; r < 16; ++r)
+    if (r < k) v[r] = *reinterpret_cast<const float4*>(y + (uint64_t)ps[r] * n + i);
+  const float4 rs = resid ? *reinterpret_cast<const float4*>(resid + (uint64_t)t * n + i)
+                          : make_float4(0.f, 0.f, 0.f, 0.f);
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    if (r < k) {
+      o.x = __fadd_rn(o.x, __fmul_rn(ws[r], v[r].x));
+      o.y = __fadd_rn(o.y, __fmul_rn(ws[r], v[r].y));
+      o.z = __fadd_rn(o.z, __fmul_rn(ws[r], v[r].z));
+      o.w = __fadd_rn(o.w, __fmul_rn(ws[r], v[r].w));
+    }
+  if (resid) {
+    o.x = __fadd_rn(rs.x, o.x);
+    o.y = __fadd_rn(rs.y, o.y);
+    o.z = __fadd_rn(rs.z, o.z);
+    o.w = __fadd_rn(rs.w, o.w);
   }
+  *reinterpret_cast<float4*>(out + (uint64_t)t * n + i) = o;
 }
 
 }  // namespace
@@ -703,7 +722,7 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
   KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      kGroupLds, s, dn);
-  KNJ_LAUNCH(k_combine, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
+  KNJ_LAUNCH(k_combine, dim3(m, (H + 4 * kBlock - 1) / (4 * kBlock)), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
                      H, a.resid, a.out);
   hipError_t e = hipGetLastError();
   if (e == hipSuccess && a.hidden_copy)
