@@ -345,6 +345,76 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
   }
 }
 
+// Merge of the split partials of one query head (one workgroup per head),
+// used for several sequences at once, where a workgroup per 32 dims would
+// launch four times the workgroups for the same bytes:
+// M = max m_s, f_s = exp(m_s - M), out = sum_s acc_s f_s / sum_s l_s f_s.
+// Every split's record is written on every call (splits past the position
+// hold m = -inf, l = 0, acc = 0), so no load here waits on the position.
+// Threads [0, D), [D, 2D) .. each fold a contiguous range of splits in order
+// (the first CH accumulator loads are issued before the max/sum pass); the
+// ranges are added in split order.
+template <int D>
+__global__ __launch_bounds__(kBlock) void k_attn_merge_head(AttnArgs a, int n_split) {
+  constexpr int NP = kBlock / D;  // 2 for D = 128, 4 for D = 64
+  constexpr int CH = 16;
+  __shared__ float fs[1024];
+  __shared__ float red[8];
+  __shared__ float parts[kBlock];
+  const int h = blockIdx.x, tid = threadIdx.x, z = blockIdx.y;
+  const float* ph = a.partial + ((uint64_t)z * a.n_head + h) * n_split * (D + 2);
+  const int d = tid % D, pt = tid / D;
+  const int per = (n_split + NP - 1) / NP;
+  const int s0 = pt * per, s1 = min(n_split, s0 + per);
+  float r[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) r[j] = s0 + j < s1 ? ph[(uint64_t)(s0 + j) * (D + 2) + 2 + d] : 0.0f;
+  float m_own[4], l_own[4];
+  float M = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s2 = tid + kBlock * j;
+    m_own[j] = s2 < n_split ? ph[(uint64_t)s2 * (D + 2)] : -INFINITY;
+    l_own[j] = s2 < n_split ? ph[(uint64_t)s2 * (D + 2) + 1] : 0.0f;
+    M = fmaxf(M, m_own[j]);
+  }
+  M = group_max<64>(M);
+  if ((tid & 63) == 0) red[tid >> 6] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float lsum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int s2 = tid + kBlock * j;
+    if (s2 < n_split) {
+      const float f = m_own[j] == -INFINITY ? 0.0f : expf(m_own[j] - M);
+      fs[s2] = f;
+      lsum += l_own[j] * f;
+    }
+  }
+  const float L = block_sum(lsum, red);  // includes the barrier that publishes fs
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j)
+    if (s0 + j < s1) acc += r[j] * fs[s0 + j];
+  for (int b = s0 + CH; b < s1; b += CH) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) r[j] = b + j < s1 ? ph[(uint64_t)(b + j) * (D + 2) + 2 + d] : 0.0f;
+#pragma unroll
+    for (int j = 0; j < CH; ++j)
+      if (b + j < s1) acc += r[j] * fs[b + j];
+  }
+  // fold the ranges in order: part 0 + part 1 (+ 2 + 3)
+  parts[tid] = acc;
+  __syncthreads();
+  if (tid < D) {
+    float o = parts[tid];
+    for (int q = 1; q < NP; ++q) o += parts[tid + q * D];
+    a.out[z * a.out_stride + (uint64_t)h * D + tid] = o / L;
+  }
+}
+
 }  // namespace
 
 int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
@@ -359,10 +429,16 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
     KNJ_LAUNCH(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    KNJ_LAUNCH(k_attn_merge<128>, dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+    if (z == 1)
+      KNJ_LAUNCH(k_attn_merge<128>, dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+    else
+      KNJ_LAUNCH(k_attn_merge_head<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
     KNJ_LAUNCH(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    KNJ_LAUNCH(k_attn_merge<64>, dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+    if (z == 1)
+      KNJ_LAUNCH(k_attn_merge<64>, dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+    else
+      KNJ_LAUNCH(k_attn_merge_head<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
     return hipErrorInvalidValue;
   }
