@@ -59,22 +59,40 @@ __device__ __forceinline__ float4 norm_rope4(float4 v, int c, float4 w, float ep
 }
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
-// One 16x16x4 f32 matrix-core step: acc[i] += sum_k A[4*(l/16)+i][k] B[k][l%16]
-// where lane l supplies A[l%16][l/16] in `a` and B[l/16][l%16] in `b`.
-__device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 acc) {
-  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, acc, 0, 0, 0);
+// One 16x16x32 f16 matrix-core step: acc[i] += sum_k A[4*(l/16)+i][k] B[k][l%16]
+// where lane l supplies A[l%16][8*(l/16) + j] and B[8*(l/16) + j][l%16], j < 8.
+__device__ __forceinline__ f32x4 mfma16(h16x8 a, h16x8 b, f32x4 acc) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc, 0, 0, 0);
 }
+
+// f32 values as f16 high parts and f16 remainders (x = hi + lo to ~22 bits):
+// against f16 cache values the two products are exact and summed in f32.
+__device__ __forceinline__ void split_h8(const float4& p, const float4& q, h16x8& hi, h16x8& lo) {
+  const float v[8] = {p.x, p.y, p.z, p.w, q.x, q.y, q.z, q.w};
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    hi[j] = (_Float16)v[j];
+    lo[j] = (_Float16)(v[j] - (float)hi[j]);
+  }
+}
+
 
 template <int D>
 __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   constexpr int ROWH = D + 8;            // f16 elements per K/V LDS row (16-byte pad)
-  constexpr int QROW = D + 4;            // floats per query row
   constexpr int EROW = kChunk + 4;       // floats per score row
   constexpr int T = D / 4;               // threads per head for the q pass
-  __shared__ float qs[8 * QROW];         // normalised, rotated queries
-  __shared__ uint16_t ks[kChunk * ROWH];
-  __shared__ uint16_t vs[kChunk * ROWH];
+  constexpr int VTS = kChunk + 8;         // f16 elements per transposed V row (one dim)
+  // slot p of dim d sits in 8-slot block (p / 8) ^ ((d / 8) % 8) of the row, so
+  // the staging writes of consecutive dims spread over the banks while the
+  // matrix-core reads still take 8 consecutive slots
+  auto vti = [](int d, int p) { return d * VTS + ((((p >> 3) ^ (d >> 3)) & 7) << 3) + (p & 7); };
+  __shared__ __align__(16) _Float16 qh[8 * ROWH];  // normalised, rotated queries: f16 high parts
+  __shared__ __align__(16) _Float16 ql[8 * ROWH];  // and remainders
+  __shared__ __align__(16) uint16_t ks[kChunk * ROWH];
+  __shared__ __align__(16) uint16_t vt[D * VTS];    // V transposed: vt[dim][slot]
   __shared__ float es[8 * EROW];         // scores, then exp(score - running max), per head
   __shared__ float alpha[16];            // per head: rescale of the running sums this chunk
   const int kvh = blockIdx.x, split = blockIdx.y, n_split = gridDim.y;
@@ -116,8 +134,8 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
     }
   };
   ld_chunk(c0 * kChunk);
-  const int qh = min(tid / T, G - 1), qc = tid % T;
-  const float4 qraw = *reinterpret_cast<const float4*>(qz + (uint64_t)(kvh * G + qh) * D + 4 * qc);
+  const int qhd = min(tid / T, G - 1), qc = tid % T;
+  const float4 qraw = *reinterpret_cast<const float4*>(qz + (uint64_t)(kvh * G + qhd) * D + 4 * qc);
   const float4 qnw = *reinterpret_cast<const float4*>(a.q_norm + 4 * qc);
   const float4 kraw = *reinterpret_cast<const float4*>(kz + (uint64_t)kvh * D + 4 * qc);
   const float4 vraw = *reinterpret_cast<const float4*>(vz + (uint64_t)kvh * D + 4 * qc);
@@ -140,7 +158,13 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   // 2) queries of this kv head: 4 floats per thread, T threads per head
   if (tid < G * T) {
     const float4 r = norm_rope4<D>(qraw, qc, qnw, a.eps, cs, sn);
-    *reinterpret_cast<float4*>(qs + qh * QROW + 4 * qc) = r;
+    const float rv[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const _Float16 h = (_Float16)rv[i];
+      qh[qhd * ROWH + 4 * qc + i] = h;
+      ql[qhd * ROWH + 4 * qc + i] = (_Float16)(rv[i] - (float)h);
+    }
   }
   // the key of this step (written to its slot below, in the chunk holding it)
   uint16_t kh[4] = {0, 0, 0, 0}, vh[4] = {0, 0, 0, 0};
@@ -165,7 +189,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
         kc[(uint64_t)pos * D + 4 * tid + k] = kh[k];
         vc[(uint64_t)pos * D + 4 * tid + k] = vh[k];
         ks[lp * ROWH + 4 * tid + k] = kh[k];
-        vs[lp * ROWH + 4 * tid + k] = vh[k];
+        vt[vti(4 * tid + k, lp)] = vh[k];
       }
     }
     KNJ_STAMP(2);
@@ -174,13 +198,17 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
     auto st = [&](int jj, const uint4& kk, const uint4& vv) {
       const int c16 = tid + kBlock * jj;
       const int p = (c16 * 8) / D, off = (c16 * 8) % D;
-      if (p >= cnt) {
-        const uint4 zz = make_uint4(0u, 0u, 0u, 0u);
-        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = zz;
-        *reinterpret_cast<uint4*>(vs + p * ROWH + off) = zz;
-      } else if (p0 + p != pos) {
-        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = kk;
-        *reinterpret_cast<uint4*>(vs + p * ROWH + off) = vv;
+      const bool dead = p >= cnt;
+      if (dead || p0 + p != pos) {
+        const uint4 k4 = dead ? make_uint4(0u, 0u, 0u, 0u) : kk;
+        const uint4 v4 = dead ? make_uint4(0u, 0u, 0u, 0u) : vv;
+        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = k4;
+        const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vt[vti(off + 2 * i, p)] = (uint16_t)(w[i] & 0xFFFFu);
+          vt[vti(off + 2 * i + 1, p)] = (uint16_t)(w[i] >> 16);
+        }
       }
     };
     st(0, k0, v0);
@@ -197,26 +225,22 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
     // 16w..16w+15 (rows) and the query heads (columns, zero past G).  Lane
     // (r = l%16, kq = l/16) contributes dims kq*D/4 .. kq*D/4 + D/4 - 1.
     {
-      const uint16_t* krow = ks + (16 * wave + r) * ROWH + kq * (D / 4);
-      const float* qrow = qs + min(r, G - 1) * QROW + kq * (D / 4);
-      f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f}, sb = {0.0f, 0.0f, 0.0f, 0.0f};
+      // A = K (16 slots x 32 dims per step), B = the queries (hi, then lo)
+      const uint16_t* krow = ks + (16 * wave + r) * ROWH + 8 * kq;
+      const int hq = min(r, G - 1);
+      const h16x8 zero8 = {};
+      f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int t8 = 0; t8 < D / 4; t8 += 8) {
-        const uint4 kk = *reinterpret_cast<const uint4*>(krow + t8);
-        const float4 qa = *reinterpret_cast<const float4*>(qrow + t8);
-        const float4 qb = *reinterpret_cast<const float4*>(qrow + t8 + 4);
-        sa = mfma4(h2f(kk.x), hv ? qa.x : 0.0f, sa);
-        sb = mfma4(h2f(kk.x >> 16), hv ? qa.y : 0.0f, sb);
-        sa = mfma4(h2f(kk.y), hv ? qa.z : 0.0f, sa);
-        sb = mfma4(h2f(kk.y >> 16), hv ? qa.w : 0.0f, sb);
-        sa = mfma4(h2f(kk.z), hv ? qb.x : 0.0f, sa);
-        sb = mfma4(h2f(kk.z >> 16), hv ? qb.y : 0.0f, sb);
-        sa = mfma4(h2f(kk.w), hv ? qb.z : 0.0f, sa);
-        sb = mfma4(h2f(kk.w >> 16), hv ? qb.w : 0.0f, sb);
+      for (int c = 0; c < D / 32; ++c) {
+        const h16x8 ka = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(krow + 32 * c));
+        const h16x8 bh = hv ? *reinterpret_cast<const h16x8*>(qh + hq * ROWH + 32 * c + 8 * kq) : zero8;
+        const h16x8 bl = hv ? *reinterpret_cast<const h16x8*>(ql + hq * ROWH + 32 * c + 8 * kq) : zero8;
+        sa = mfma16(ka, bh, sa);
+        sa = mfma16(ka, bl, sa);
       }
       if (hv) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) es[r * EROW + 16 * wave + 4 * kq + i] = (sa[i] + sb[i]) * a.scale;
+        for (int i = 0; i < 4; ++i) es[r * EROW + 16 * wave + 4 * kq + i] = sa[i] * a.scale;
       }
     }
     __syncthreads();
@@ -245,9 +269,10 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
     // dims 32w .. 32w+31 as two column tiles, even dims and odd dims, so one
     // 32-bit LDS read feeds both; lane (r, kq) contributes slots kq*16 .. +15.
     if (32 * wave < D) {
-      const int d = 32 * wave + 2 * r;
-      const float* erow = es + min(r, G - 1) * EROW + kq * 16;
-      const uint16_t* vcol = vs + (kq * 16) * ROWH + d;
+      // A = e (heads x 32 slots per step, hi then lo), B = V (32 slots x 16
+      // dims) from the transposed rows; wave w owns dims 32w .. 32w + 31 as
+      // two 16-column tiles
+      const float* erow = es + min(r, G - 1) * EROW + 8 * kq;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = 4 * kq + i;
@@ -256,15 +281,21 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
         oo[i] *= al;
       }
 #pragma unroll
-      for (int t4 = 0; t4 < 16; t4 += 4) {
-        const float4 ev = *reinterpret_cast<const float4*>(erow + t4);
-        const float e4[4] = {hv ? ev.x : 0.0f, hv ? ev.y : 0.0f, hv ? ev.z : 0.0f, hv ? ev.w : 0.0f};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t vv = *reinterpret_cast<const uint32_t*>(vcol + (t4 + i) * ROWH);
-          oe = mfma4(e4[i], h2f(vv), oe);
-          oo = mfma4(e4[i], h2f(vv >> 16), oo);
+      for (int c = 0; c < kChunk / 32; ++c) {
+        const float4 e0 = *reinterpret_cast<const float4*>(erow + 32 * c);
+        const float4 e1 = *reinterpret_cast<const float4*>(erow + 32 * c + 4);
+        h16x8 eh, el;
+        split_h8(e0, e1, eh, el);
+        if (!hv) {
+          eh = h16x8{};
+          el = h16x8{};
         }
+        const h16x8 v0 = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(vt + vti(32 * wave + r, 32 * c + 8 * kq)));
+        const h16x8 v1 = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(vt + vti(32 * wave + 16 + r, 32 * c + 8 * kq)));
+        oe = mfma16(eh, v0, oe);
+        oe = mfma16(el, v0, oe);
+        oo = mfma16(eh, v1, oo);
+        oo = mfma16(el, v1, oo);
       }
     }
     __syncthreads();  // the next chunk overwrites ks/vs/es
@@ -279,11 +310,14 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
     }
   }
   if (32 * wave < D) {
-    const int d = 32 * wave + 2 * r;
+    const int d = 32 * wave + r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * kq + i;
-      if (h < G) *reinterpret_cast<float2*>(part + h * hstride + 2 + d) = make_float2(oe[i], oo[i]);
+      if (h < G) {
+        part[h * hstride + 2 + d] = oe[i];
+        part[h * hstride + 2 + d + 16] = oo[i];
+      }
     }
   }
   KNJ_STAMP(5);
