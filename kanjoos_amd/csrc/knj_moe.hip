@@ -747,8 +747,13 @@ void launch_maybe_timed(F kernel, const char* name, dim3 grid, size_t lds, hipSt
 
 
 hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
-  // four rows (waves) per workgroup; the last workgroup also ranks the experts
-  KNJ_LAUNCH(k_router, dim3((a.n_expert + 3) / 4), dim3(kBlock), 0, s, a);
+  if (a.topk_idx) {
+    // four rows (waves) per workgroup; the last workgroup also ranks the experts
+    KNJ_LAUNCH(k_router, dim3((a.n_expert + 3) / 4), dim3(kBlock), 0, s, a);
+  } else {
+    // logits only: one row per single-wave workgroup, spread over n_expert CUs
+    KNJ_LAUNCH(k_router, dim3(a.n_expert), dim3(64), 0, s, a);
+  }
   return hipGetLastError();
 }
 
