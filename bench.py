@@ -238,7 +238,7 @@ def main() -> int:
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: this build runs the decode path on a single GPU "
-              "(expert-parallel sharding is described in DESIGN.md, not implemented); "
+              "(expert-parallel sharding across GPUs is a design, not implemented here); "
               "run with --gpus 1", file=sys.stderr)
         return 2
 
