@@ -449,6 +449,217 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge_head(AttnArgs a, int n_sp
   }
 }
 
+// Prefill, step 1: row t = blockIdx.x at position pos0 + t.  Each group of
+// D/4 threads holds one head (queries first, then keys): the query is
+// normalised and rotated in place, the key normalised, rotated and written to
+// the cache as f16, the value written as f16.  Same arithmetic as the decode
+// kernel's (norm_rope4).
+template <int D>
+__global__ __launch_bounds__(kBlock) void k_prefill_rope_append(PrefillAttnArgs a) {
+  constexpr int T = D / 4, HPB = kBlock / T;  // threads per head, heads per workgroup
+  const int t = blockIdx.x, p = a.pos0 + t;
+  const int nh = a.n_head + a.n_head_kv;
+  const int hh = blockIdx.y * HPB + threadIdx.x / T, c = threadIdx.x % T;
+  const int hc = min(hh, nh - 1);  // every lane computes; lanes past the heads store nothing
+  const bool is_q = hc < a.n_head;
+  float* row = a.qkv + (uint64_t)t * a.qkv_stride;
+  float* src = row + (uint64_t)hc * D + 4 * c;  // q heads, then k heads, are contiguous
+  const float4 raw = *reinterpret_cast<const float4*>(src);
+  const float4 w = *reinterpret_cast<const float4*>((is_q ? a.q_norm : a.k_norm) + 4 * c);
+  const int ri = (c < T / 2) ? 4 * c : 4 * c - D / 2;
+  const float4 cs = *reinterpret_cast<const float4*>(a.rope_cos + (uint64_t)p * (D / 2) + ri);
+  const float4 sn = *reinterpret_cast<const float4*>(a.rope_sin + (uint64_t)p * (D / 2) + ri);
+  const float4 r = norm_rope4<D>(raw, c, w, a.eps, cs, sn);
+  if (hh >= nh) return;
+  if (is_q) {
+    *reinterpret_cast<float4*>(src) = r;
+    return;
+  }
+  const int kvh = hc - a.n_head;
+  const uint64_t slot = ((uint64_t)kvh * a.n_ctx + p) * D + 4 * c;
+  const float4 v = *reinterpret_cast<const float4*>(row + (uint64_t)(a.n_head + a.n_head_kv) * D +
+                                                      (uint64_t)kvh * D + 4 * c);
+  uint2 kk, vv;
+  kk.x = (uint32_t)f2h(r.x) | ((uint32_t)f2h(r.y) << 16);
+  kk.y = (uint32_t)f2h(r.z) | ((uint32_t)f2h(r.w) << 16);
+  vv.x = (uint32_t)f2h(v.x) | ((uint32_t)f2h(v.y) << 16);
+  vv.y = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
+  *reinterpret_cast<uint2*>(a.k_cache + slot) = kk;
+  *reinterpret_cast<uint2*>(a.v_cache + slot) = vv;
+}
+
+// Prefill, step 2: causal attention of a tile of prompt rows.  Workgroup
+// (kv head, tile) takes 64 query columns, column = (row t0 + c / G, head
+// kvh*G + c % G), so every K/V chunk staged in LDS serves 64 queries.  Wave w
+// owns columns 16w .. 16w+15 for the whole pass, with its queries held in
+// registers (f16 high parts and remainders) as the B operand:
+//   scores   S[slot][col] = K (16 slots x 32 dims) x Q (32 dims x 16 cols),
+//            lane (r = l%16, kq = l/16) ends with column r's scores of slots
+//            16*st + 4*kq + i (st = slot tile, i < 4);
+//   softmax  per column in registers: the column's 16 scores of the lane,
+//            then the xor-16 and xor-32 partners (the other kq);
+//   values   O^T[d][col] = V^T (16 dims x 32 slots) x E (32 slots x 16 cols).
+//            A step's 32 reduction indices are the slots the lane already
+//            holds (32c + 4kq + i and 32c + 16 + 4kq + i), so the softmax
+//            weights feed the matrix cores without leaving the lane; the V^T
+//            operand reads the same slots from the transposed V rows.
+// Online softmax over 64-slot chunks as in the decode kernel; slot s counts
+// for the row at position qp when s <= qp.
+template <int D>
+__global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a) {
+  constexpr int ROWH = D + 8;
+  constexpr int VTS = kChunk + 8;
+  auto vti = [](int d, int p) { return d * VTS + ((((p >> 3) ^ (d >> 3)) & 7) << 3) + (p & 7); };
+  __shared__ __align__(16) uint16_t ks[kChunk * ROWH];
+  __shared__ __align__(16) uint16_t vt[D * VTS];
+  const int kvh = blockIdx.x;
+  const int G = a.n_head / a.n_head_kv, QT = 64 / G;
+  const int t0 = blockIdx.y * QT;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r = lane & 15, kq = lane >> 4;
+  const int col = 16 * wave + r, g = col % G;
+  const bool live = t0 + col / G < a.n_rows;
+  const int t = min(t0 + col / G, a.n_rows - 1);
+  const int qp = a.pos0 + t;
+  const int n_kv = a.pos0 + min(t0 + QT, a.n_rows);  // slots any row of the tile sees
+  const int nch = (n_kv + kChunk - 1) / kChunk;
+  const uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
+  const uint16_t* vc = a.v_cache + (uint64_t)kvh * a.n_ctx * D;
+  constexpr int PER = (kChunk * D * 2) / (16 * kBlock);
+  static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
+  uint4 k0, k1, k2, k3, v0, v1, v2, v3;
+  auto ld = [&](int p0, int j, uint4& kk, uint4& vv) {
+    const int c16 = tid + kBlock * j;
+    const int p = min(p0 + (c16 * 8) / D, a.n_ctx - 1), off = (c16 * 8) % D;
+    kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)p * D + off);
+    vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)p * D + off);
+  };
+  auto ld_chunk = [&](int p0) {
+    ld(p0, 0, k0, v0);
+    ld(p0, 1, k1, v1);
+    if constexpr (PER > 2) {
+      ld(p0, 2, k2, v2);
+      ld(p0, 3, k3, v3);
+    }
+  };
+  ld_chunk(0);
+  // this lane's query column: dims 32c + 8kq .. +7 of every 32-dim step
+  h16x8 qhi[D / 32], qlo[D / 32];
+  const float* qrow = a.qkv + (uint64_t)t * a.qkv_stride + (uint64_t)(kvh * G + g) * D;
+#pragma unroll
+  for (int c = 0; c < D / 32; ++c) {
+    const float4 x0 = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq);
+    const float4 x1 = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq + 4);
+    split_h8(x0, x1, qhi[c], qlo[c]);
+  }
+  float mrun = -INFINITY, lrun = 0.0f;
+  f32x4 acc[D / 16];
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int j = 0; j < nch; ++j) {
+    const int p0 = j * kChunk;
+    const int cnt = min(kChunk, n_kv - p0);
+    // stage the chunk: K rows, V transposed; slots past the tile's last
+    // position become zeros (a weight of 0 times a stale value stays 0)
+    auto st = [&](int jj, const uint4& kk, const uint4& vv) {
+      const int c16 = tid + kBlock * jj;
+      const int p = (c16 * 8) / D, off = (c16 * 8) % D;
+      const bool dead = p >= cnt;
+      const uint4 k4 = dead ? make_uint4(0u, 0u, 0u, 0u) : kk;
+      const uint4 v4 = dead ? make_uint4(0u, 0u, 0u, 0u) : vv;
+      *reinterpret_cast<uint4*>(ks + p * ROWH + off) = k4;
+      const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        vt[vti(off + 2 * i, p)] = (uint16_t)(w[i] & 0xFFFFu);
+        vt[vti(off + 2 * i + 1, p)] = (uint16_t)(w[i] >> 16);
+      }
+    };
+    st(0, k0, v0);
+    st(1, k1, v1);
+    if constexpr (PER > 2) {
+      st(2, k2, v2);
+      st(3, k3, v3);
+    }
+    if (j + 1 < nch) ld_chunk(p0 + kChunk);
+    __syncthreads();
+    // scores of this lane's column over the chunk's 64 slots
+    f32x4 sc[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f};
+      const uint16_t* krow = ks + (16 * s4 + r) * ROWH + 8 * kq;
+#pragma unroll
+      for (int c = 0; c < D / 32; ++c) {
+        const h16x8 ka = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(krow + 32 * c));
+        sa = mfma16(ka, qhi[c], sa);
+        sa = mfma16(ka, qlo[c], sa);
+      }
+      sc[s4] = sa;
+    }
+    float cmax = -INFINITY;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int ps = p0 + 16 * s4 + 4 * kq + i;
+        const float v = ps <= qp ? sc[s4][i] * a.scale : -INFINITY;
+        sc[s4][i] = v;
+        cmax = fmaxf(cmax, v);
+      }
+    }
+    cmax = fmaxf(cmax, xor16_f(cmax));
+    cmax = fmaxf(cmax, xor32_f(cmax));
+    const float mnew = fmaxf(mrun, cmax);  // finite: slot 0 counts for every row
+    const float alpha = expf(mrun - mnew);
+    float esum = 0.0f;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float e = expf(sc[s4][i] - mnew);  // exp(-inf) = 0 past the row's position
+        sc[s4][i] = e;
+        esum += e;
+      }
+    }
+    esum += xor16_f(esum);
+    esum += xor32_f(esum);
+    lrun = lrun * alpha + esum;
+    mrun = mnew;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
+    }
+    // values: step c covers slots 32c + 4kq + i (j < 4) and 32c + 16 + 4kq + i
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const float4 ea = make_float4(sc[2 * c][0], sc[2 * c][1], sc[2 * c][2], sc[2 * c][3]);
+      const float4 eb = make_float4(sc[2 * c + 1][0], sc[2 * c + 1][1], sc[2 * c + 1][2], sc[2 * c + 1][3]);
+      h16x8 eh, el;
+      split_h8(ea, eb, eh, el);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const int d = 16 * dt + r;
+        const uint2 va = *reinterpret_cast<const uint2*>(vt + vti(d, 32 * c + 4 * kq));
+        const uint2 vb = *reinterpret_cast<const uint2*>(vt + vti(d, 32 * c + 16 + 4 * kq));
+        const h16x8 vv = __builtin_bit_cast(h16x8, make_uint4(va.x, va.y, vb.x, vb.y));
+        acc[dt] = mfma16(vv, eh, acc[dt]);
+        acc[dt] = mfma16(vv, el, acc[dt]);
+      }
+    }
+    __syncthreads();  // the next chunk overwrites ks / vt
+  }
+  if (!live) return;
+  const float inv = 1.0f / lrun;
+  float* orow = a.out + (uint64_t)t * a.n_head * D + (uint64_t)(kvh * G + g) * D;
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) {
+    *reinterpret_cast<float4*>(orow + 16 * dt + 4 * kq) =
+        make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv);
+  }
+}
+
 }  // namespace
 
 int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
@@ -475,6 +686,31 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH(k_attn_merge_head<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
     return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+bool prefill_attention_ok(int n_head, int n_head_kv, int head_dim) {
+  if (n_head_kv <= 0 || n_head % n_head_kv) return false;
+  const int G = n_head / n_head_kv;
+  return (head_dim == 128 || head_dim == 64) && G <= 64 && 64 % G == 0;
+}
+
+hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
+  if (!prefill_attention_ok(a.n_head, a.n_head_kv, a.head_dim) || a.n_rows <= 0 || a.pos0 < 0 ||
+      a.pos0 + a.n_rows > a.n_ctx)
+    return hipErrorInvalidValue;
+  const int G = a.n_head / a.n_head_kv, QT = 64 / G;
+  const int nh = a.n_head + a.n_head_kv;
+  const dim3 tiles(a.n_head_kv, (a.n_rows + QT - 1) / QT);
+  if (a.head_dim == 128) {
+    constexpr int HPB = kBlock / 32;
+    KNJ_LAUNCH(k_prefill_rope_append<128>, dim3(a.n_rows, (nh + HPB - 1) / HPB), dim3(kBlock), 0, s, a);
+    KNJ_LAUNCH(k_prefill_attn<128>, tiles, dim3(kBlock), 0, s, a);
+  } else {
+    constexpr int HPB = kBlock / 16;
+    KNJ_LAUNCH(k_prefill_rope_append<64>, dim3(a.n_rows, (nh + HPB - 1) / HPB), dim3(kBlock), 0, s, a);
+    KNJ_LAUNCH(k_prefill_attn<64>, tiles, dim3(kBlock), 0, s, a);
   }
   return hipGetLastError();
 }

@@ -177,6 +177,31 @@ struct AttnArgs {
 int attn_splits(int n_ctx);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);
 
+// Attention of a prompt chunk (Model::forward with n > 1,
+// /root/reference/src/model/model.cpp:560-616): rows t < n_rows at positions
+// pos0 + t.  The first launch normalises and rotates every row's query (in
+// place) and key, and appends every row's key and value to the cache; the
+// second gives row t attention over slots 0 .. pos0 + t.  qkv rows are
+// [q | k | v] of qkv_stride floats; out rows are n_head * head_dim floats.
+struct PrefillAttnArgs {
+  float* qkv;
+  int qkv_stride;
+  const float* q_norm;
+  const float* k_norm;
+  float eps;
+  const float* rope_cos;     // [n_ctx][D/2] tables
+  const float* rope_sin;
+  int pos0, n_rows;
+  uint16_t* k_cache;         // [n_head_kv][n_ctx][D] of this layer
+  uint16_t* v_cache;
+  int n_head, n_head_kv, head_dim, n_ctx;
+  float scale;
+  float* out;
+};
+// False when the shape is not one the prefill kernels take (64 % group, D).
+bool prefill_attention_ok(int n_head, int n_head_kv, int head_dim);
+hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s);
+
 // Decode-step control block in device memory: the token fed to the step, its
 // position, the index into the output token ring, and the packed argmax of the
 // LM head.

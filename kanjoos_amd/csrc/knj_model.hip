@@ -704,11 +704,17 @@ int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_
   for (int t = 0; t < n; ++t) {
     KNJ_CHECK_ARG(tokens[t] >= 0 && tokens[t] < m->c.n_vocab, "token id out of range");
   }
-  for (int t = 0; t < n; ++t) {
-    int rc = set_state(m, tokens[t], 0);
+  const char* ps = std::getenv("KNJ_PROMPT_STEPS");
+  if (n > 1 && prefill_eligible(m) && !(ps && ps[0] == '1')) {
+    const int rc = prefill(m, tokens, n);
     if (rc) return rc;
-    if ((rc = run_step(m))) return rc;
-    m->pos += 1;
+  } else {
+    for (int t = 0; t < n; ++t) {
+      int rc = set_state(m, tokens[t], 0);
+      if (rc) return rc;
+      if ((rc = run_step(m))) return rc;
+      m->pos += 1;
+    }
   }
   if (logits_host) {
     KNJ_HIP(hipMemcpyAsync(logits_host, m->logits, (uint64_t)m->c.n_vocab * 4, hipMemcpyDeviceToHost,

@@ -10,6 +10,16 @@
 #include "../../include/knj_capi.h"
 #include "knj_common.h"
 
+// Buffers of the prompt pass (knj::prefill), allocated on its first use for
+// chunks of up to `cap` rows.
+struct knj_prefill_bufs {
+  int cap = 0;
+  float *x = nullptr, *hx = nullptr, *qkv = nullptr, *ctx = nullptr;
+  float *router_logits = nullptr, *topk_w = nullptr;
+  int32_t *topk_idx = nullptr, *tokens = nullptr;
+  void* scratch = nullptr;
+};
+
 struct knj_model {
   knj_model_config c{};
   uint8_t* image = nullptr;
@@ -32,6 +42,9 @@ struct knj_model {
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool use_graph = true;  // KNJ_NO_GRAPH=1 launches the step's kernels directly
+  // prompt pass over several rows at once (KNJ_PROMPT_STEPS=1 feeds prompts
+  // one decode step per token instead)
+  knj_prefill_bufs pf;
   hipEvent_t* expert_events = nullptr;  // set by knj_model_time_experts: 4 per layer per step
   int expert_slot = 0;
   // host<->device bytes copied by this model's calls (the profiler's transfer row)
@@ -55,6 +68,13 @@ struct SpanRun {
   hipEvent_t epoch = nullptr;
   hipError_t err = hipSuccess;
 };
+
+// Model::forward over n > 1 tokens as one pass (knj_prefill.hip): every
+// weight applied to up to 512 rows at once, causal attention over the cache,
+// the last row's hidden states, router choices and logits kept.  `eligible`
+// says whether the model's tensor types and shape allow it.
+bool prefill_eligible(const knj_model* m);
+int prefill(knj_model* m, const int32_t* tokens, int n);
 
 // Slots [0, n_elems / D) of `rows` cache rows of row_elems elements: seeded f16
 // values ~N(0, 1) (k_fill_kv).

@@ -119,6 +119,8 @@ def lib():
         L.knjo_model_threads.argtypes = [_P]
         L.knjo_model_forward.restype = C.c_int
         L.knjo_model_forward.argtypes = [_P, _P, C.c_int, _P]
+        L.knjo_model_forward_steps.restype = C.c_int
+        L.knjo_model_forward_steps.argtypes = [_P, _P, C.c_int, _P]
         L.knjo_model_hidden.restype = _f32p
         L.knjo_model_hidden.argtypes = [_P, C.c_int]
         L.knjo_model_topk_idx.restype = C.POINTER(C.c_int32)
@@ -257,9 +259,17 @@ class OracleModel:
         lib().knjo_model_reset(self.h)
 
     def forward(self, tokens) -> np.ndarray:
+        """One Model::forward call over all of `tokens` (the batched prefill)."""
+        return self._run(lib().knjo_model_forward, tokens)
+
+    def forward_steps(self, tokens) -> np.ndarray:
+        """`tokens` as single-token forward calls, one after another."""
+        return self._run(lib().knjo_model_forward_steps, tokens)
+
+    def _run(self, fn, tokens) -> np.ndarray:
         t = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
         logits = np.zeros(self.cfg.n_vocab, dtype=np.float32)
-        if lib().knjo_model_forward(self.h, _ptr(t), t.size, _ptr(logits)) != 0:
+        if fn(self.h, _ptr(t), t.size, _ptr(logits)) != 0:
             raise RuntimeError(lib().knjo_last_error().decode())
         return logits
 

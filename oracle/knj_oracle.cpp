@@ -677,13 +677,10 @@ int knjo_model_set_pos(knjo_model* m, int pos) {
   return 0;
 }
 
-// Model::forward (model.cpp:512-672), one token at a time.  The reference runs
-// a batch of n through each weight once; for n > 1 its matmul takes the
-// staged-block branch, which rounds differently from the fused m == 1 dot.
-// This restatement is used for decode parity, where every call has n == 1, and
-// for prefill as a sequence of single-token steps (each step is exactly a
-// reference decode step).
-int knjo_model_forward(knjo_model* m, const int32_t* tokens, int n, float* logits) {
+// n single-token steps of Model::forward (model.cpp:512-672): what the
+// reference computes when a prompt is fed one forward(&tok, 1) call at a time.
+// For n == 1 this is exactly Model::forward.
+int knjo_model_forward_steps(knjo_model* m, const int32_t* tokens, int n, float* logits) {
   try {
     const knj_model_config& c = m->c;
     if (n <= 0) throw std::runtime_error("forward needs at least one token");
@@ -791,6 +788,137 @@ int knjo_model_forward(knjo_model* m, const int32_t* tokens, int n, float* logit
                m->col);
       }
     }
+    if (logits) std::memcpy(logits, m->logits.data(), sizeof(float) * (size_t)V);
+    return 0;
+  } catch (const std::exception& e) {
+    g_err = e.what();
+    return -1;
+  }
+}
+
+// Model::forward (model.cpp:512-672) over n tokens at once: every weight
+// matrix is applied to the n rows together (matmul with m = n, whose m > 1
+// branch dequantises each 256-block and dots every row with it), all n keys
+// and values are appended before any attention (model.cpp:562-584), row t then
+// attends causally over slots 0..pos+t (:591-616), the MoE runs over the n
+// rows (:628-653), and only the last row goes through the final norm and the
+// head (:662-667).  n == 1 is the single-token step.
+int knjo_model_forward(knjo_model* m, const int32_t* tokens, int n, float* logits) {
+  if (n == 1) return knjo_model_forward_steps(m, tokens, n, logits);
+  try {
+    const knj_model_config& c = m->c;
+    if (n <= 0) throw std::runtime_error("forward needs at least one token");
+    if (m->pos + n > c.n_ctx) throw std::runtime_error("context exhausted");
+    const int H = c.n_embd, D = c.head_dim, QD = c.n_head * D, KVD = c.n_head_kv * D;
+    const int E = c.n_expert, K = c.n_expert_used, F = c.n_ff, V = c.n_vocab;
+    const float attn_scale = 1.0f / std::sqrt((float)D);
+    const uint8_t* img = m->img;
+    Pool& pool = *m->pool;
+    const size_t N = (size_t)n;
+    std::vector<float> x(N * H), xn(N * H), q(N * QD), k(N * KVD), v(N * KVD), ctx(N * QD);
+    std::vector<float> ao(N * H), hx(N * H), ffn(N * H), rlog(N * E), tw(N * K);
+    std::vector<int32_t> tk(N * K);
+    // embed (model.cpp:527-537)
+    for (int t = 0; t < n; ++t) {
+      const int32_t id = tokens[t];
+      if (id < 0 || id >= V) throw std::runtime_error("token id out of range");
+      dequant_row(c.type_embd, img + m->off_embd + (uint64_t)id * knj_row_bytes(c.type_embd, H),
+                  x.data() + (size_t)t * H, (uint64_t)H);
+    }
+    const int half = D / 2, group = c.n_head / c.n_head_kv;
+    const uint64_t rb = knj_row_bytes(c.type_attn, H);
+    for (int il = 0; il < c.n_layer; ++il) {
+      const knj_layer_offsets& lo = m->lo[il];
+      const float* qn = reinterpret_cast<const float*>(img + lo.q_norm);
+      const float* kn = reinterpret_cast<const float*>(img + lo.k_norm);
+      // rmsnorm_rows + QKV (model.cpp:546-558)
+      for (int t = 0; t < n; ++t)
+        rmsnorm(x.data() + (size_t)t * H, reinterpret_cast<const float*>(img + lo.attn_norm),
+                xn.data() + (size_t)t * H, H, c.rms_eps);
+      matmul(pool, c.type_attn, img + lo.wqkv, H, QD, xn.data(), n, H, q.data(), QD, m->col);
+      matmul(pool, c.type_attn, img + lo.wqkv + rb * QD, H, KVD, xn.data(), n, H, k.data(), KVD,
+             m->col);
+      matmul(pool, c.type_attn, img + lo.wqkv + rb * (QD + KVD), H, KVD, xn.data(), n, H, v.data(),
+             KVD, m->col);
+      // QK-norm, NEOX RoPE and the append of every row (model.cpp:562-584)
+      for (int t = 0; t < n; ++t) {
+        const int p = m->pos + t;
+        float* qt = q.data() + (size_t)t * QD;
+        float* kt = k.data() + (size_t)t * KVD;
+        for (int h = 0; h < c.n_head; ++h) {
+          rmsnorm(qt + (size_t)h * D, qn, m->head_tmp.data(), D, c.rms_eps);
+          std::memcpy(qt + (size_t)h * D, m->head_tmp.data(), sizeof(float) * D);
+        }
+        for (int h = 0; h < c.n_head_kv; ++h) {
+          rmsnorm(kt + (size_t)h * D, kn, m->head_tmp.data(), D, c.rms_eps);
+          std::memcpy(kt + (size_t)h * D, m->head_tmp.data(), sizeof(float) * D);
+        }
+        for (int pass = 0; pass < 2; ++pass) {
+          float* base = pass == 0 ? qt : kt;
+          const int nh = pass == 0 ? c.n_head : c.n_head_kv;
+          for (int h = 0; h < nh; ++h) {
+            float* pv = base + (size_t)h * D;
+            for (int i = 0; i < half; ++i) {
+              const float theta = (float)p * m->inv_freq[i];
+              const float cs = std::cos(theta), sn = std::sin(theta);
+              const float x0 = pv[i], x1 = pv[i + half];
+              pv[i] = x0 * cs - x1 * sn;
+              pv[i + half] = x0 * sn + x1 * cs;
+            }
+          }
+        }
+        for (int h = 0; h < c.n_head_kv; ++h) {
+          const size_t off = (((size_t)il * c.n_head_kv + h) * c.n_ctx + p) * D;
+          for (int d = 0; d < D; ++d) {
+            m->kv_k[off + d] = adopt_kv(m, kt[(size_t)h * D + d], m->src_k, off + d);
+            m->kv_v[off + d] = adopt_kv(m, v[(size_t)t * KVD + (size_t)h * D + d], m->src_v, off + d);
+          }
+        }
+      }
+      // causal attention, row t over slots 0..pos+t (model.cpp:591-616)
+      for (int t = 0; t < n; ++t) {
+        const int p = m->pos + t;
+        for (int h = 0; h < c.n_head; ++h) {
+          const float* qh = q.data() + (size_t)t * QD + (size_t)h * D;
+          const size_t hb = ((size_t)il * c.n_head_kv + h / group) * c.n_ctx;
+          for (int s = 0; s <= p; ++s) {
+            const uint16_t* kh = m->kv_k.data() + (hb + s) * D;
+            float acc = 0.0f;
+            for (int d = 0; d < D; ++d) acc += qh[d] * knj_f16_to_f32(kh[d]);
+            m->scores[s] = acc * attn_scale;
+          }
+          softmax(m->scores.data(), p + 1);
+          float* ch = ctx.data() + (size_t)t * QD + (size_t)h * D;
+          std::fill(ch, ch + D, 0.0f);
+          for (int s = 0; s <= p; ++s) {
+            const uint16_t* vh = m->kv_v.data() + (hb + s) * D;
+            const float a = m->scores[s];
+            for (int d = 0; d < D; ++d) ch[d] += a * knj_f16_to_f32(vh[d]);
+          }
+        }
+      }
+      // attn-o + residual (model.cpp:620-625)
+      matmul(pool, c.type_attn, img + lo.wo, QD, H, ctx.data(), n, QD, ao.data(), H, m->col);
+      for (size_t i = 0; i < N * H; ++i) x[i] += ao[i];
+      // ffn norm, MoE over the n rows, residual (model.cpp:628-653)
+      for (int t = 0; t < n; ++t)
+        rmsnorm(x.data() + (size_t)t * H, reinterpret_cast<const float*>(img + lo.ffn_norm),
+                hx.data() + (size_t)t * H, H, c.rms_eps);
+      moe(pool, hx.data(), n, H, F, E, K, reinterpret_cast<const float*>(img + lo.router),
+          img + lo.gate, img + lo.up, img + lo.down, c.type_gate_up, c.type_down, ffn.data(),
+          rlog.data(), tk.data(), tw.data(), m->ms);
+      for (size_t i = 0; i < N * H; ++i) x[i] += ffn[i];
+      const size_t last = (size_t)(n - 1);
+      std::memcpy(m->hidden.data() + (size_t)il * H, x.data() + last * H, sizeof(float) * H);
+      std::memcpy(m->topk_idx.data() + (size_t)il * K, tk.data() + last * K, sizeof(int32_t) * K);
+      std::memcpy(m->topk_w.data() + (size_t)il * K, tw.data() + last * K, sizeof(float) * K);
+    }
+    // final norm + head of the last row (model.cpp:662-667)
+    rmsnorm(x.data() + (size_t)(n - 1) * H, reinterpret_cast<const float*>(img + m->off_onorm),
+            m->xn.data(), H, c.rms_eps);
+    matmul(pool, c.type_head, img + m->off_head, H, V, m->xn.data(), 1, H, m->logits.data(), V,
+           m->col);
+    m->pos += n;
     if (logits) std::memcpy(logits, m->logits.data(), sizeof(float) * (size_t)V);
     return 0;
   } catch (const std::exception& e) {

@@ -66,9 +66,13 @@ uint64_t knjo_model_image_bytes(knjo_model* m);
 void knjo_model_reset(knjo_model* m);
 int knjo_model_pos(knjo_model* m);
 int knjo_model_threads(knjo_model* m);
-/* Runs n tokens; copies the last token's logits into `logits` (n_vocab floats).
- * Returns 0, or -1 with a message in knjo_last_error(). */
+/* Runs n tokens as one Model::forward call (all rows through each weight, all
+ * keys appended, causal attention); copies the last token's logits into
+ * `logits` (n_vocab floats).  Returns 0, or -1 with a message in
+ * knjo_last_error(). */
 int knjo_model_forward(knjo_model* m, const int32_t* tokens, int n, float* logits);
+/* The same n tokens as n single-token forward calls (identical for n == 1). */
+int knjo_model_forward_steps(knjo_model* m, const int32_t* tokens, int n, float* logits);
 /* Residual stream of the last token after layer il (model.cpp:654-658), from
  * the most recent forward call. */
 const float* knjo_model_hidden(knjo_model* m, int il);

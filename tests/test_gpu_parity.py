@@ -215,6 +215,80 @@ def test_small_model_greedy_parity(device, cfgkw):
     assert list(got) == list(want)
 
 
+def prefill_parity(om, gm, prompt, n_layer, tol=1e-5):
+    """One forward call over a prompt on both sides (the GPU's prompt pass, the
+    oracle's batched Model::forward).  As in step_parity the oracle adopts the
+    GPU's f16 cache values after checking each is the rounding of an f32 value
+    within 1e-5 of its own, so a flipped rounding does not propagate into
+    the comparison of the last row's per-layer residuals, top-k and logits."""
+    lg = gm.forward(prompt)
+    kg, vg = gm.kv_download()
+    om.set_kv_source(kg, vg)
+    lw = om.forward(prompt)
+    st = om.kv_stats()
+    om.set_kv_source(None, None)
+    assert st["adopted"] == 2 * n_layer * gm.cfg.n_head_kv * gm.cfg.head_dim * len(prompt), st
+    assert st["max_mid_dist"] <= 1e-5, st
+    worst = 0.0
+    for il in range(n_layer):
+        e = rel_rmse(gm.hidden(il), om.hidden(il))
+        worst = max(worst, e)
+        assert e <= tol, (il, e)
+        assert list(gm.topk(il)[0]) == list(om.topk(il)[0]), il
+    assert rel_rmse(lg, lw) <= tol
+    assert gm.pos == om.pos
+    return worst
+
+
+PREFILL_SHAPES = {
+    "g4_d64": dict(),
+    "g8_d128": dict(n_head=32, n_head_kv=4, head_dim=128),
+    "g1_d64": dict(n_head=4, n_head_kv=4),
+    "g2_d128": dict(n_head=8, n_head_kv=4, head_dim=128),
+}
+
+
+@pytest.mark.parametrize("shape", list(PREFILL_SHAPES))
+def test_prefill_parity(device, shape):
+    """A prompt in one call, a second prompt continuing from its cache (rows
+    at positions past 0, tiles that start mid-chunk), then decode steps from
+    the cache the prompt pass wrote."""
+    cfg = small_config(**PREFILL_SHAPES[shape])
+    say(f"prefill parity {shape} {cfg}")
+    om = O.OracleModel(O.make_config(**cfg), seed=SEED)
+    gm = K.Model.from_image(K.qwen3_30b_a3b(**cfg), om.image())
+    rng = np.random.default_rng(7)
+    p1 = [int(t) for t in rng.integers(0, cfg["n_vocab"], 37)]
+    p2 = [int(t) for t in rng.integers(0, cfg["n_vocab"], 21)]
+    w1 = prefill_parity(om, gm, p1, cfg["n_layer"])
+    w2 = prefill_parity(om, gm, p2, cfg["n_layer"])
+    w3, _, _ = step_parity(om, gm, [5, 6, 7], cfg["n_layer"])
+    say(f"worst per-layer rel-RMSE: prompt {w1:.3g}, continued {w2:.3g}, steps {w3:.3g}")
+
+
+def test_prefill_crosses_chunks(device):
+    """A 600-token prompt: two chunks of the prompt pass (512 + 88 rows)."""
+    cfg = small_config(n_ctx=640)
+    say(f"prefill across chunks {cfg}")
+    om = O.OracleModel(O.make_config(**cfg), seed=SEED)
+    gm = K.Model.from_image(K.qwen3_30b_a3b(**cfg), om.image())
+    prompt = [int(t) for t in np.random.default_rng(3).integers(0, cfg["n_vocab"], 600)]
+    worst = prefill_parity(om, gm, prompt, cfg["n_layer"])
+    say(f"worst per-layer rel-RMSE {worst:.3g}")
+
+
+def test_prefill_errors(device):
+    cfg = small_config()
+    gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    with pytest.raises(K.KnjError, match="context exhausted"):
+        gm.forward([1] * (cfg["n_ctx"] + 1))
+    with pytest.raises(K.KnjError, match="out of range"):
+        gm.forward([1, cfg["n_vocab"]])
+    assert gm.pos == 0
+    gm.forward([1, 2, 3])
+    assert gm.pos == 3
+
+
 def test_cpp_driver_runs(device):
     """The C++ Model/Backend classes end to end through kanjoos-run (small geometry)."""
     import os

@@ -242,3 +242,74 @@ def test_router_ties_go_to_lower_index():
     assert list(ti[0, :2]) == [lo, hi]
     assert tw[0, 0] == tw[0, 1]
     assert abs(float(tw[0].sum()) - 1.0) < 1e-6
+
+
+def f16_ulps(a, b):
+    """Distance in f16 ulps between two arrays of f16 bit patterns (same sign)."""
+    ia, ib = a.astype(np.int32), b.astype(np.int32)
+    ia = np.where(ia & 0x8000, 0x8000 - ia, ia)
+    ib = np.where(ib & 0x8000, 0x8000 - ib, ib)
+    return np.abs(ia - ib)
+
+
+@pytest.mark.parametrize("over", [dict(), dict(type_down=O.TYPE_Q6_K, type_head=O.TYPE_Q6_K)])
+def test_oracle_prefill_vs_numpy_float64(over):
+    """One forward call over a prompt (all rows through each weight, causal
+    attention over a cache appended for every row first) against the float64
+    model fed the same tokens one at a time, which is what the causal mask
+    means: a row attending to a later row, a row reading another row's
+    position or a missing append moves the logits far outside 1e-4."""
+    cfg = dict(TINY, **over)
+    oc = O.make_config(**cfg)
+    om = O.OracleModel(oc, seed=5, threads=2)
+    npm = NpModel(oc.as_dict(), om.image().copy())
+    prompt = [3, 100, 7, 511, 42, 42, 9]
+    lw = om.forward(prompt)
+    for tok in prompt:
+        ln = npm.step(tok)
+    assert om.pos == len(prompt)
+    assert rel_rmse(lw, ln) < 1e-4
+    for il in range(cfg["n_layer"]):
+        assert rel_rmse(om.hidden(il), npm.hidden[il]) < 1e-4, il  # (~3e-5 from f16 flips)
+        assert list(om.topk(il)[0]) == list(npm.topk[il]), il
+    # a decode step after the prefill continues from its cache
+    assert rel_rmse(om.forward([17]), npm.step(17)) < 1e-4
+
+
+def test_oracle_prefill_matches_single_steps_and_split_calls():
+    """Splitting a prompt over two forward calls changes nothing but the m > 1
+    matmul's per-call grouping: logits and hidden states agree to ~1e-6 and
+    the caches to an f16 ulp.  Single-token steps round differently (the fused
+    dot of the m == 1 matmul, and the f16 cache roundings that follow from it
+    flip), so they agree only to ~1e-4; both are pinned against the float64
+    model above.  n == 1 is the single-token step bit for bit."""
+    oc = O.make_config(**TINY)
+    prompt = [5, 6, 7, 8, 300, 301, 2, 1, 0, 77]
+    a = O.OracleModel(oc, seed=9, threads=2)
+    b = O.OracleModel(oc, seed=9, threads=2, image=a.image())
+    s = O.OracleModel(oc, seed=9, threads=2, image=a.image())
+    la = a.forward(prompt)
+    b.forward(prompt[:6])
+    lb = b.forward(prompt[6:])
+    ls = s.forward_steps(prompt)
+    assert a.pos == b.pos == s.pos == len(prompt)
+    assert rel_rmse(la, lb) < 1e-5
+    assert rel_rmse(la, ls) < 3e-4
+    n = len(prompt)
+    for il in range(TINY["n_layer"]):
+        assert rel_rmse(a.hidden(il), b.hidden(il)) < 1e-5
+        assert rel_rmse(a.hidden(il), s.hidden(il)) < 3e-4
+    for x, y in zip(a.kv(), b.kv()):
+        assert f16_ulps(x[:, :, :n], y[:, :, :n]).max() <= 1
+    t1 = O.OracleModel(oc, seed=9, threads=2, image=a.image())
+    t2 = O.OracleModel(oc, seed=9, threads=2, image=a.image())
+    assert np.array_equal(t1.forward([42]), t2.forward_steps([42]))
+
+
+def test_oracle_prefill_errors():
+    oc = O.make_config(**TINY)
+    om = O.OracleModel(oc, seed=1, threads=1)
+    with pytest.raises(RuntimeError, match="context exhausted"):
+        om.forward(list(range(TINY["n_ctx"] + 1)))
+    with pytest.raises(RuntimeError, match="out of range"):
+        om.forward([1, TINY["n_vocab"]])
