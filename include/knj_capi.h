@@ -190,9 +190,16 @@ int knj_model_download_image(const knj_model* m, void* host, uint64_t bytes);
 int knj_model_reset(knj_model* m);
 int knj_model_pos(const knj_model* m);
 int knj_model_set_pos(knj_model* m, int pos);
-/* Runs n tokens one decode step each; logits_host (n_vocab floats, may be NULL)
- * receives the last token's logits.  Errors: KNJ_E_ARG for token ids out of
- * range or a full context (model.cpp:514-517, 533). */
+/* Model::forward (/root/reference/src/model/model.cpp:512-672): runs n tokens at
+ * positions pos .. pos+n-1.  n == 1 is one decode step (the captured graph);
+ * n > 1 is the prompt pass: every weight applied to up to 512 rows at once,
+ * each row's key and value appended, causal attention (row t over slots
+ * 0 .. pos+t), the head on the last row -- for Q4_K attention and experts
+ * (other tensor types take one decode step per token).  logits_host (n_vocab
+ * floats, may be NULL) receives the last token's logits; the per-layer
+ * hidden/top-k queries then describe the last token.  Errors: KNJ_E_ARG for
+ * token ids out of range or a full context (model.cpp:514-517, 533), nothing
+ * run. */
 int knj_model_forward(knj_model* m, const int32_t* tokens, int n, float* logits_host);
 /* Greedy decode entirely on the device: feeds `first`, then `steps` argmax
  * tokens (first maximum wins, /root/reference/src/cli/main.cpp:126-132) into
