@@ -668,7 +668,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   // one 64-slot chunk per workgroup up to 128 chunks; beyond, several chunks
   // per workgroup so the merge sees at most 128 partials per head
   const int chunks = attn_splits(a.n_ctx);
-  const int cpw = (chunks + 127) / 128;
+  // several sequences fill the chip with their own splits: two chunks per
+  // workgroup there (measured 2% faster at 32 sequences x 2048 slots; one
+  // chunk is faster at batch 1)
+  const int cpw = std::max((chunks + 127) / 128, a.n_seq > 1 ? 2 : 1);
   const int n_split = (chunks + cpw - 1) / cpw;
   if (n_split > 128) return hipErrorInvalidValue;  // the merge folds at most 8 x 16 splits
   const int z = std::max(1, a.n_seq);

@@ -5,8 +5,9 @@
                     weights, and the MoE output of one layer (x ~ N(0,1), RMSNorm
                     weight 1, router f32 ~ N(0,0.02), 128 Q4_K experts).
   full_greedy.json  BASELINE config 3's model (48 layers, seed 0): 64 greedy
-                    tokens after the prompt [1, 2, 3, 4], with the top-1/top-2
-                    logit margin of every step.
+                    tokens after the prompt [1, 2, 3, 4] (one forward call over
+                    the prompt, as the reference's Model::forward runs it), with
+                    the top-1/top-2 logit margin of every step.
 
 The oracle restates the reference's CPU forward pass (oracle/); the weights come
 from the seeded generator in include/knj_synth.h, which the GPU reproduces bit
