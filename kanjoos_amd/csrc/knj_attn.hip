@@ -503,17 +503,21 @@ __global__ __launch_bounds__(kBlock) void k_prefill_rope_append(PrefillAttnArgs 
 //            holds (32c + 4kq + i and 32c + 16 + 4kq + i), so the softmax
 //            weights feed the matrix cores without leaving the lane; the V^T
 //            operand reads the same slots from the transposed V rows.
-// Online softmax over 64-slot chunks as in the decode kernel; slot s counts
-// for the row at position qp when s <= qp.
+// Online softmax over 64-slot chunks as in the decode kernel, in base 2 (the
+// scores scaled by log2 e, the exponentials 2^x on the hardware's exp2); slot
+// s counts for the row at position qp when s <= qp.  Grid z splits the KV
+// range: split z walks chunks [z cps, (z + 1) cps) and, when there are
+// several, leaves a partial record per column for k_prefill_merge.
 template <int D>
-__global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a) {
+__global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int cps) {
+  constexpr int NT = kBlock, NC = 64;  // query columns: 16 per wave
   constexpr int ROWH = D + 8;
   constexpr int VTS = kChunk + 8;
   auto vti = [](int d, int p) { return d * VTS + ((((p >> 3) ^ (d >> 3)) & 7) << 3) + (p & 7); };
   __shared__ __align__(16) uint16_t ks[kChunk * ROWH];
   __shared__ __align__(16) uint16_t vt[D * VTS];
   const int kvh = blockIdx.x;
-  const int G = a.n_head / a.n_head_kv, QT = 64 / G;
+  const int G = a.n_head / a.n_head_kv, QT = NC / G;
   const int t0 = blockIdx.y * QT;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int r = lane & 15, kq = lane >> 4;
@@ -522,27 +526,29 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a) {
   const int t = min(t0 + col / G, a.n_rows - 1);
   const int qp = a.pos0 + t;
   const int n_kv = a.pos0 + min(t0 + QT, a.n_rows);  // slots any row of the tile sees
-  const int nch = (n_kv + kChunk - 1) / kChunk;
+  // split z of gridDim.z walks chunks [c0, c1) of the tile's range
+  const int c0 = blockIdx.z * cps;
+  const int c1 = min((n_kv + kChunk - 1) / kChunk, c0 + cps);
   const uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
   const uint16_t* vc = a.v_cache + (uint64_t)kvh * a.n_ctx * D;
-  constexpr int PER = (kChunk * D * 2) / (16 * kBlock);
-  static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
+  constexpr int PER = (kChunk * D * 2) / (16 * NT);
+  static_assert(PER == 1 || PER == 2 || PER == 4, "head_dim 64 or 128");
   uint4 k0, k1, k2, k3, v0, v1, v2, v3;
   auto ld = [&](int p0, int j, uint4& kk, uint4& vv) {
-    const int c16 = tid + kBlock * j;
+    const int c16 = tid + NT * j;
     const int p = min(p0 + (c16 * 8) / D, a.n_ctx - 1), off = (c16 * 8) % D;
     kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)p * D + off);
     vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)p * D + off);
   };
   auto ld_chunk = [&](int p0) {
     ld(p0, 0, k0, v0);
-    ld(p0, 1, k1, v1);
+    if constexpr (PER > 1) ld(p0, 1, k1, v1);
     if constexpr (PER > 2) {
       ld(p0, 2, k2, v2);
       ld(p0, 3, k3, v3);
     }
   };
-  ld_chunk(0);
+  if (c0 < c1) ld_chunk(c0 * kChunk);
   // this lane's query column: dims 32c + 8kq .. +7 of every 32-dim step
   h16x8 qhi[D / 32], qlo[D / 32];
   const float* qrow = a.qkv + (uint64_t)t * a.qkv_stride + (uint64_t)(kvh * G + g) * D;
@@ -552,36 +558,51 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a) {
     const float4 x1 = *reinterpret_cast<const float4*>(qrow + 32 * c + 8 * kq + 4);
     split_h8(x0, x1, qhi[c], qlo[c]);
   }
+  // softmax in base 2: scores carry log2(e), e^(s - m) = 2^(s log2 e - m log2 e)
+  const float scale2 = a.scale * 1.4426950408889634f;
   float mrun = -INFINITY, lrun = 0.0f;
   f32x4 acc[D / 16];
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int j = 0; j < nch; ++j) {
+  for (int j = c0; j < c1; ++j) {
     const int p0 = j * kChunk;
     const int cnt = min(kChunk, n_kv - p0);
     // stage the chunk: K rows, V transposed; slots past the tile's last
     // position become zeros (a weight of 0 times a stale value stays 0)
+    // V goes in as (slot p, slot p + 1) pairs of one dim, 32 bits per write:
+    // the lanes staging slots p (even) and p + 1 hold the same 8 dims D/8
+    // lanes apart and swap half of them, the even lane then writing dims
+    // off .. off+3 and the odd lane dims off+4 .. off+7 of both slots
     auto st = [&](int jj, const uint4& kk, const uint4& vv) {
-      const int c16 = tid + kBlock * jj;
+      const int c16 = tid + NT * jj;
       const int p = (c16 * 8) / D, off = (c16 * 8) % D;
       const bool dead = p >= cnt;
       const uint4 k4 = dead ? make_uint4(0u, 0u, 0u, 0u) : kk;
       const uint4 v4 = dead ? make_uint4(0u, 0u, 0u, 0u) : vv;
       *reinterpret_cast<uint4*>(ks + p * ROWH + off) = k4;
-      const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        vt[vti(off + 2 * i, p)] = (uint16_t)(w[i] & 0xFFFFu);
-        vt[vti(off + 2 * i + 1, p)] = (uint16_t)(w[i] >> 16);
-      }
+      const bool even = (p & 1) == 0;
+      auto swap = [](uint32_t x) {
+        if constexpr (D == 128) return xor16_u32(x);
+        else return dpp_u32<kDppRor8>(x);
+      };
+      const uint32_t r0 = swap(even ? v4.z : v4.x), r1 = swap(even ? v4.w : v4.y);
+      // own and partner words of the four dims this lane writes
+      const uint32_t o0 = even ? v4.x : v4.z, o1 = even ? v4.y : v4.w;
+      const uint32_t lo0 = even ? o0 : r0, hi0 = even ? r0 : o0;  // slot p&~1, slot p|1
+      const uint32_t lo1 = even ? o1 : r1, hi1 = even ? r1 : o1;
+      const int d0 = off + (even ? 0 : 4), pe = p & ~1;
+      *reinterpret_cast<uint32_t*>(vt + vti(d0, pe)) = (lo0 & 0xFFFFu) | (hi0 << 16);
+      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 1, pe)) = (lo0 >> 16) | (hi0 & 0xFFFF0000u);
+      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 2, pe)) = (lo1 & 0xFFFFu) | (hi1 << 16);
+      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 3, pe)) = (lo1 >> 16) | (hi1 & 0xFFFF0000u);
     };
     st(0, k0, v0);
-    st(1, k1, v1);
+    if constexpr (PER > 1) st(1, k1, v1);
     if constexpr (PER > 2) {
       st(2, k2, v2);
       st(3, k3, v3);
     }
-    if (j + 1 < nch) ld_chunk(p0 + kChunk);
+    if (j + 1 < c1) ld_chunk(p0 + kChunk);
     __syncthreads();
     // scores of this lane's column over the chunk's 64 slots
     f32x4 sc[4];
@@ -603,21 +624,24 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int ps = p0 + 16 * s4 + 4 * kq + i;
-        const float v = ps <= qp ? sc[s4][i] * a.scale : -INFINITY;
+        const float v = ps <= qp ? sc[s4][i] * scale2 : -INFINITY;
         sc[s4][i] = v;
         cmax = fmaxf(cmax, v);
       }
     }
     cmax = fmaxf(cmax, xor16_f(cmax));
     cmax = fmaxf(cmax, xor32_f(cmax));
-    const float mnew = fmaxf(mrun, cmax);  // finite: slot 0 counts for every row
-    const float alpha = expf(mrun - mnew);
+    // -inf while every slot so far is past the row's position (a split that
+    // starts after it); the exponents then use 0 so that no -inf - -inf occurs
+    const float mnew = fmaxf(mrun, cmax);
+    const float mref = mnew == -INFINITY ? 0.0f : mnew;
+    const float alpha = exp2f(mrun - mref);
     float esum = 0.0f;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = expf(sc[s4][i] - mnew);  // exp(-inf) = 0 past the row's position
+        const float e = exp2f(sc[s4][i] - mref);  // 2^-inf = 0 past the row's position
         sc[s4][i] = e;
         esum += e;
       }
@@ -650,6 +674,19 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a) {
     }
     __syncthreads();  // the next chunk overwrites ks / vt
   }
+  if (gridDim.z > 1) {
+    // partial record {max, sum, sum e*v} of this column for the merge (a
+    // split past the tile's range leaves max = -inf, sum = 0, acc = 0)
+    float* rec = a.partial + ((((uint64_t)blockIdx.y * gridDim.x + kvh) * gridDim.z + blockIdx.z) * NC + col) * (D + 2);
+    if (kq == 0) {
+      rec[0] = mrun;
+      rec[1] = lrun;
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt)
+      *reinterpret_cast<float4*>(rec + 2 + 16 * dt + 4 * kq) = make_float4(acc[dt][0], acc[dt][1], acc[dt][2], acc[dt][3]);
+    return;
+  }
   if (!live) return;
   const float inv = 1.0f / lrun;
   float* orow = a.out + (uint64_t)t * a.n_head * D + (uint64_t)(kvh * G + g) * D;
@@ -658,6 +695,35 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a) {
     *reinterpret_cast<float4*>(orow + 16 * dt + 4 * kq) =
         make_float4(acc[dt][0] * inv, acc[dt][1] * inv, acc[dt][2] * inv, acc[dt][3] * inv);
   }
+}
+
+// Merge of the split partials: thread = one (row, head, dim) output,
+// M = max_s m_s, out = sum_s acc_s e^(m_s - M) / sum_s l_s e^(m_s - M), the
+// splits folded in order in one pass (running maximum, rescaled sums).  The
+// maxima are in the base-2 units of k_prefill_attn.
+template <int D>
+__global__ __launch_bounds__(kBlock) void k_prefill_merge(PrefillAttnArgs a, int n_split) {
+  constexpr int NC = 64;
+  const uint64_t i = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+  const int HD = a.n_head * D;
+  if (i >= (uint64_t)a.n_rows * HD) return;
+  const int t = (int)(i / HD), hd = (int)(i - (uint64_t)t * HD);
+  const int h = hd / D, d = hd - h * D;
+  const int G = a.n_head / a.n_head_kv, QT = NC / G;
+  const int tile = t / QT, kvh = h / G, col = (t - tile * QT) * G + h % G;
+  const uint64_t stride = (uint64_t)NC * (D + 2);
+  const float* rec = a.partial + (((uint64_t)tile * a.n_head_kv + kvh) * n_split * NC + col) * (D + 2);
+  float M = -INFINITY, L = 0.0f, o = 0.0f;
+  for (int sp = 0; sp < n_split; ++sp) {
+    const float m = rec[sp * stride], l = rec[sp * stride + 1], v = rec[sp * stride + 2 + d];
+    const float Mn = fmaxf(M, m);
+    const float ref = Mn == -INFINITY ? 0.0f : Mn;
+    const float fo = exp2f(M - ref), fn = exp2f(m - ref);
+    L = L * fo + l * fn;
+    o = o * fo + v * fn;
+    M = Mn;
+  }
+  a.out[i] = o / L;
 }
 
 }  // namespace
@@ -693,6 +759,8 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+constexpr int kPrefillWGs = 1024;  // split-KV target for the prompt-pass attention
+
 bool prefill_attention_ok(int n_head, int n_head_kv, int head_dim) {
   if (n_head_kv <= 0 || n_head % n_head_kv) return false;
   const int G = n_head / n_head_kv;
@@ -703,19 +771,41 @@ hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
   if (!prefill_attention_ok(a.n_head, a.n_head_kv, a.head_dim) || a.n_rows <= 0 || a.pos0 < 0 ||
       a.pos0 + a.n_rows > a.n_ctx)
     return hipErrorInvalidValue;
-  const int G = a.n_head / a.n_head_kv, QT = 64 / G;
+  const int G = a.n_head / a.n_head_kv;
   const int nh = a.n_head + a.n_head_kv;
-  const dim3 tiles(a.n_head_kv, (a.n_rows + QT - 1) / QT);
+  const int QT = 64 / G;
+  const int n_tiles = (a.n_rows + QT - 1) / QT;
+  // split the KV range when the tiles alone leave the chip short of work and
+  // the range is long: at most kPrefillWGs workgroups, at least 8 chunks each
+  const int nch = (a.pos0 + a.n_rows + kChunk - 1) / kChunk;
+  const int base = a.n_head_kv * n_tiles;
+  int n_split = 1;
+  if (nch >= 16 && base < kPrefillWGs) n_split = std::min(nch / 8, kPrefillWGs / base);
+  if (n_split > 1 && !a.partial) return hipErrorInvalidValue;
+  const int cps = (nch + n_split - 1) / n_split;
+  n_split = (nch + cps - 1) / cps;
+  const dim3 grid(a.n_head_kv, n_tiles, n_split);
+  const dim3 mgrid((unsigned)(((uint64_t)a.n_rows * a.n_head * a.head_dim + kBlock - 1) / kBlock));
+#define KNJ_PREFILL(DD, HPB)                                                                      \
+  KNJ_LAUNCH(k_prefill_rope_append<DD>, dim3(a.n_rows, (nh + (HPB) - 1) / (HPB)), dim3(kBlock), 0, s, a); \
+  KNJ_LAUNCH(k_prefill_attn<DD>, grid, dim3(kBlock), 0, s, a, cps);                                \
+  if (n_split > 1) KNJ_LAUNCH(k_prefill_merge<DD>, mgrid, dim3(kBlock), 0, s, a, n_split);
   if (a.head_dim == 128) {
-    constexpr int HPB = kBlock / 32;
-    KNJ_LAUNCH(k_prefill_rope_append<128>, dim3(a.n_rows, (nh + HPB - 1) / HPB), dim3(kBlock), 0, s, a);
-    KNJ_LAUNCH(k_prefill_attn<128>, tiles, dim3(kBlock), 0, s, a);
+    KNJ_PREFILL(128, kBlock / 32)
   } else {
-    constexpr int HPB = kBlock / 16;
-    KNJ_LAUNCH(k_prefill_rope_append<64>, dim3(a.n_rows, (nh + HPB - 1) / HPB), dim3(kBlock), 0, s, a);
-    KNJ_LAUNCH(k_prefill_attn<64>, tiles, dim3(kBlock), 0, s, a);
+    KNJ_PREFILL(64, kBlock / 16)
   }
+#undef KNJ_PREFILL
   return hipGetLastError();
+}
+
+uint64_t prefill_partial_bytes(int n_head, int n_head_kv, int head_dim, int max_rows) {
+  if (!prefill_attention_ok(n_head, n_head_kv, head_dim)) return 0;
+  // n_split <= kPrefillWGs / tiles when it is above 1
+  const int QT = 64 / (n_head / n_head_kv);
+  const uint64_t base = (uint64_t)n_head_kv * ((max_rows + QT - 1) / QT);
+  const uint64_t wgs = std::max<uint64_t>(base, kPrefillWGs);
+  return wgs * 64 * (head_dim + 2) * 4;
 }
 
 }  // namespace knj

@@ -197,9 +197,13 @@ struct PrefillAttnArgs {
   int n_head, n_head_kv, head_dim, n_ctx;
   float scale;
   float* out;
+  // scratch for split-KV partials: prefill_partial_bytes(...) bytes
+  float* partial = nullptr;
 };
 // False when the shape is not one the prefill kernels take (64 % group, D).
 bool prefill_attention_ok(int n_head, int n_head_kv, int head_dim);
+// Scratch the prompt-pass attention needs for up to max_rows rows.
+uint64_t prefill_partial_bytes(int n_head, int n_head_kv, int head_dim, int max_rows);
 hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s);
 
 // Decode-step control block in device memory: the token fed to the step, its

@@ -17,6 +17,7 @@ struct knj_prefill_bufs {
   float *x = nullptr, *hx = nullptr, *qkv = nullptr, *ctx = nullptr;
   float *router_logits = nullptr, *topk_w = nullptr;
   int32_t *topk_idx = nullptr, *tokens = nullptr;
+  float* attn_part = nullptr;  // split-KV partials of the prompt-pass attention
   void* scratch = nullptr;
 };
 

@@ -65,6 +65,7 @@ int ensure_bufs(knj_model* m) {
   A((void**)&b.topk_idx, (uint64_t)R * c.n_expert_used * 4);
   A((void**)&b.topk_w, (uint64_t)R * c.n_expert_used * 4);
   A((void**)&b.tokens, (uint64_t)R * 4);
+  A((void**)&b.attn_part, prefill_partial_bytes(c.n_head, c.n_head_kv, c.head_dim, R));
   A(&b.scratch, std::max({moe_batch_scratch_bytes(R, H, c.n_ff, c.n_expert, c.n_expert_used),
                           dense_scratch_bytes(R, H, QKV), dense_scratch_bytes(R, QD, H)}));
   if (!rc) b.cap = R;
@@ -95,7 +96,7 @@ int prefill_chunk(knj_model* m, const int32_t* tokens, int n, bool last) {
                        reinterpret_cast<const float*>(img + lo.q_norm),
                        reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos,
                        m->rope_sin, m->pos, n, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head,
-                       c.n_head_kv, D, c.n_ctx, 1.0f / std::sqrt((float)D), b.ctx};
+                       c.n_head_kv, D, c.n_ctx, 1.0f / std::sqrt((float)D), b.ctx, b.attn_part};
     KNJ_HIP(launch_prefill_attention(pa, s));
     KNJ_HIP(launch_dense_q4k(img + lo.wo, QD, H, n, b.ctx, b.x, b.x, b.scratch, s));
     MoeBatchArgs ma{b.x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,

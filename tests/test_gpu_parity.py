@@ -277,6 +277,24 @@ def test_prefill_crosses_chunks(device):
     say(f"worst per-layer rel-RMSE {worst:.3g}")
 
 
+@pytest.mark.parametrize("shape", ["g4_d64", "g8_d128"])
+def test_prefill_split_kv(device, shape):
+    """A 512-row prompt pass at positions 520-1031: the attention's KV range
+    (17 chunks of 64 slots) is split over two workgroups per tile and merged;
+    the second split starts at slot 576, past the positions of the rows at
+    520-575, which see none of its slots."""
+    cfg = small_config(n_ctx=1100, **PREFILL_SHAPES[shape])
+    say(f"prefill split-KV {shape} {cfg}")
+    om = O.OracleModel(O.make_config(**cfg), seed=SEED)
+    gm = K.Model.from_image(K.qwen3_30b_a3b(**cfg), om.image())
+    rng = np.random.default_rng(11)
+    p1 = [int(t) for t in rng.integers(0, cfg["n_vocab"], 520)]
+    p2 = [int(t) for t in rng.integers(0, cfg["n_vocab"], 512)]
+    w1 = prefill_parity(om, gm, p1, cfg["n_layer"])
+    w2 = prefill_parity(om, gm, p2, cfg["n_layer"])
+    say(f"worst per-layer rel-RMSE: {w1:.3g}, split {w2:.3g}")
+
+
 def test_prefill_errors(device):
     cfg = small_config()
     gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
