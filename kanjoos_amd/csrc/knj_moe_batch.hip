@@ -85,47 +85,68 @@ __global__ __launch_bounds__(kBlock) void k_norm_rows(const float* __restrict__ 
   }
 }
 
-// The A operand of the grouped GEMM for pair p (one workgroup each): row
-// row_of[p] of src (row p when row_of is null), n floats, as f16 high parts and
-// remainders in perm8 order and as per-32 sums split the same way.  Layouts
-// interleave the pairs so that a wave's 32 pairs read one contiguous run:
+// The A operand of the grouped GEMM: for each pair p, row row_of[p] of src
+// (row p when row_of is null), n floats, as f16 high parts and remainders in
+// perm8 order and as per-32 sums split the same way.  Layouts interleave the
+// pairs so that a wave's 32 pairs read one contiguous run:
 // hi/lo[(q * P + p) * 8 + j] for 8-group q; sums[((b / 8) * P + p) * 8 + b % 8]
-// for 32-sub-block b.
-__global__ __launch_bounds__(kBlock) void k_split_pairs(const float* __restrict__ src,
-                                                        const int* __restrict__ row_of, int n,
-                                                        int P, _Float16* __restrict__ hi,
-                                                        _Float16* __restrict__ lo,
-                                                        _Float16* __restrict__ shi,
-                                                        _Float16* __restrict__ slo) {
-  const int p = blockIdx.x, t = threadIdx.x;
-  const float* s = src + (uint64_t)(row_of ? row_of[p] : p) * n;
+// for 32-sub-block b.  Workgroup = a tile of 32 pairs x 256 elements
+// (blockIdx.x, blockIdx.y): each pair's row segment is read whole (32
+// consecutive threads, 1 KB), the 8-element groups pass through LDS, and each
+// output row [group][pairs] is written as 32 consecutive 16-byte records.
+// n % 256 == 0.
+__global__ __launch_bounds__(kBlock) void k_split_tile(const float* __restrict__ src,
+                                                       const int* __restrict__ row_of, int n,
+                                                       int P, _Float16* __restrict__ hi,
+                                                       _Float16* __restrict__ lo,
+                                                       _Float16* __restrict__ shi,
+                                                       _Float16* __restrict__ slo) {
+  __shared__ uint4 th[32][33], tl[32][33];  // [group][pair] (+1 against bank conflicts)
+  __shared__ __align__(16) _Float16 sh_h[32][8], sh_l[32][8];  // [pair][sub-block]
+  const int t = threadIdx.x, p0 = blockIdx.x * 32, c0 = blockIdx.y * 256;
 #pragma unroll
-  for (int q2 = 0; q2 < 2; ++q2) {
-    const int g = t + kBlock * q2;  // 8-group (n <= 4096)
-    if (8 * g < n) {                // uniform over aligned groups of 4 threads (n % 32 == 0)
-      const float4 a = *reinterpret_cast<const float4*>(s + 8 * g);
-      const float4 b = *reinterpret_cast<const float4*>(s + 8 * g + 4);
-      const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      half8 h, l;
-      float sum = 0.0f;
+  for (int u = 0; u < 4; ++u) {
+    const int i = t + kBlock * u, pr = i >> 5, g = i & 31;  // 32 consecutive threads: one pair
+    const int p = min(p0 + pr, P - 1);
+    const float* s = src + (uint64_t)(row_of ? row_of[p] : p) * n + c0 + 8 * g;
+    const float4 a = *reinterpret_cast<const float4*>(s);
+    const float4 b = *reinterpret_cast<const float4*>(s + 4);
+    const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    half8 h, l;
+    float sum = 0.0f;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float x = v[perm8(j)];
-        h[j] = (_Float16)x;
-        l[j] = (_Float16)(x - (float)h[j]);
-        sum += v[j];
-      }
-      const uint64_t o = ((uint64_t)g * P + p) * 8;
-      *reinterpret_cast<uint4*>(hi + o) = __builtin_bit_cast(uint4, h);
-      *reinterpret_cast<uint4*>(lo + o) = __builtin_bit_cast(uint4, l);
-      sum = group_sum<4>(sum);  // sub-block g/4 = four consecutive threads
-      if ((t & 3) == 0) {
-        const int sb = g / 4;
-        const uint64_t so = ((uint64_t)(sb / 8) * P + p) * 8 + sb % 8;
-        const _Float16 sh = (_Float16)sum;
-        shi[so] = sh;
-        slo[so] = (_Float16)(sum - (float)sh);
-      }
+    for (int j = 0; j < 8; ++j) {
+      const float x = v[perm8(j)];
+      h[j] = (_Float16)x;
+      l[j] = (_Float16)(x - (float)h[j]);
+      sum += v[j];
+    }
+    th[g][pr] = __builtin_bit_cast(uint4, h);
+    tl[g][pr] = __builtin_bit_cast(uint4, l);
+    sum = group_sum<4>(sum);  // sub-block g / 4: four consecutive threads
+    if ((t & 3) == 0) {
+      const _Float16 sv = (_Float16)sum;
+      sh_h[pr][g >> 2] = sv;
+      sh_l[pr][g >> 2] = (_Float16)(sum - (float)sv);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = t + kBlock * u, g = i >> 5, pr = i & 31;  // 32 consecutive threads: one group
+    if (p0 + pr < P) {
+      const uint64_t o = ((uint64_t)(c0 / 8 + g) * P + p0 + pr) * 8;
+      *reinterpret_cast<uint4*>(hi + o) = th[g][pr];
+      *reinterpret_cast<uint4*>(lo + o) = tl[g][pr];
+    }
+  }
+  if (t < 64) {
+    const int pr = t & 31;
+    if (p0 + pr < P) {
+      // the 8 sub-blocks of this tile are sub-block group c0 / 256
+      const uint64_t so = ((uint64_t)(c0 / 256) * P + p0 + pr) * 8;
+      *reinterpret_cast<uint4*>((t < 32 ? shi : slo) + so) =
+          *reinterpret_cast<const uint4*>(t < 32 ? sh_h[pr] : sh_l[pr]);
     }
   }
 }
@@ -243,7 +264,7 @@ struct GroupArgs {
   const uint8_t* w0;        // [E] Q4_K slabs of n_out rows x n_in (gate, or down)
   const uint8_t* w1;        // up slabs (gate/up only)
   int n_in, n_out;
-  const _Float16* ah;       // A operand of every pair (k_split_pairs layout), high parts
+  const _Float16* ah;       // A operand of every pair (k_split_tile layout), high parts
   const _Float16* al;       // f16 remainders
   const _Float16* sh;       // sub-block sums, high parts
   const _Float16* sl;
@@ -712,13 +733,13 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
                      a.topk_idx, a.topk_w);
   KNJ_LAUNCH(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
                      pair_of, items, n_items);
-  KNJ_LAUNCH(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, xin, pair_tok, H,
-                     (int)P, xh, xl, sxh, sxl);
+  KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), H / 256), dim3(kBlock), 0, s, xin,
+             pair_tok, H, (int)P, xh, xl, sxh, sxl);
   GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, (int)P, offsets, items, n_items, act};
   KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      kGroupLds, s, gu);
-  KNJ_LAUNCH(k_split_pairs, dim3((unsigned)P), dim3(kBlock), 0, s, act, nullptr, F, (int)P,
-                     ah, al, sah, sal);
+  KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), F / 256), dim3(kBlock), 0, s, act,
+             nullptr, F, (int)P, ah, al, sah, sal);
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
   KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      kGroupLds, s, dn);
@@ -773,8 +794,8 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
   int* meta = (int*)take(1024);  // offsets {0, m}, n_items, items
   const int ks = dense_ksplit(m, n_in, n_out);
   float* part = ks > 1 ? (float*)take((uint64_t)ks * P * n_out * 4) : nullptr;
-  KNJ_LAUNCH(k_split_pairs, dim3(m), dim3(kBlock), 0, s, x, nullptr, n_in, m, xh, xl, sh,
-                     sl);
+  KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 256), dim3(kBlock), 0, s, x, nullptr,
+             n_in, m, xh, xl, sh, sl);
   KNJ_LAUNCH(k_dense_meta, dim3(1), dim3(64), 0, s, m, meta);
   GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, meta, (const int2*)(meta + 64), meta + 2,
               out, resid};
