@@ -246,19 +246,6 @@ __global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ t
   }
 }
 
-// Work list of a dense GEMM over m rows seen as one expert: offsets {0, m} in
-// meta[0..1], the tile count in meta[2], tile t = (0, 32 t) at meta + 64.
-__global__ void k_dense_meta(int m, int* meta) {
-  const int tiles = (m + kTok - 1) / kTok;
-  if (threadIdx.x == 0) {
-    meta[0] = 0;
-    meta[1] = m;
-    meta[2] = tiles;
-  }
-  int2* items = reinterpret_cast<int2*>(meta + 64);
-  for (int t = threadIdx.x; t < tiles; t += blockDim.x) items[t] = make_int2(0, t * kTok);
-}
-
 // ------------------------------------------------------------------ grouped expert GEMM
 struct GroupArgs {
   const uint8_t* w0;        // [E] Q4_K slabs of n_out rows x n_in (gate, or down)
@@ -269,7 +256,7 @@ struct GroupArgs {
   const _Float16* sh;       // sub-block sums, high parts
   const _Float16* sl;
   int P;                    // pairs
-  const int* offsets;       // [E + 1]
+  const int* offsets;       // [E + 1]; null: dense, the P rows are one expert
   const int2* items;
   const int* n_items;
   float* out;               // [pairs][n_out]
@@ -304,12 +291,17 @@ struct WBlock {
 template <bool GATEUP>
 __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
   extern __shared__ uint4 lds[];
-  const int item = blockIdx.y;
-  if (item >= *a.n_items) return;  // uniform over the workgroup
-  const int2 it = a.items[item];
-  const int e = it.x;
-  const int p0 = a.offsets[e] + it.y;
-  const int cnt = min(kTok, a.offsets[e + 1] - p0);
+  // grouped: work item blockIdx.y of the list; dense (no offsets): the
+  // m rows are one expert, tile blockIdx.y
+  int e = 0, p0 = blockIdx.y * kTok, cnt = min(kTok, a.P - p0);
+  if (a.offsets) {
+    const int item = blockIdx.y;
+    if (item >= *a.n_items) return;  // uniform over the workgroup
+    const int2 it = a.items[item];
+    e = it.x;
+    p0 = a.offsets[e] + it.y;
+    cnt = min(kTok, a.offsets[e + 1] - p0);
+  }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int rbase = blockIdx.x * kRowsWG + wave * 32;
   const bool rows_ok = rbase < a.n_out;  // waves past the last row still stage and sync
@@ -765,7 +757,7 @@ uint64_t dense_scratch_bytes(int m, int n_in, int n_out) {
   const uint64_t P = (uint64_t)m;
   const int ks = dense_ksplit(m, n_in, n_out);
   const uint64_t part = ks > 1 ? (uint64_t)ks * P * n_out * 4 : 0;
-  return 4 * ((P * n_in * 2 + 255) & ~255ull) + 2 * ((P * n_in / 16 + 255) & ~255ull) + 1024 +
+  return 4 * ((P * n_in * 2 + 255) & ~255ull) + 2 * ((P * n_in / 16 + 255) & ~255ull) +
          ((part + 255) & ~255ull);
 }
 
@@ -791,14 +783,11 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
   _Float16* xl = (_Float16*)take(P * n_in * 2);
   _Float16* sh = (_Float16*)take(P * n_in / 16);
   _Float16* sl = (_Float16*)take(P * n_in / 16);
-  int* meta = (int*)take(1024);  // offsets {0, m}, n_items, items
   const int ks = dense_ksplit(m, n_in, n_out);
   float* part = ks > 1 ? (float*)take((uint64_t)ks * P * n_out * 4) : nullptr;
   KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 256), dim3(kBlock), 0, s, x, nullptr,
              n_in, m, xh, xl, sh, sl);
-  KNJ_LAUNCH(k_dense_meta, dim3(1), dim3(64), 0, s, m, meta);
-  GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, meta, (const int2*)(meta + 64), meta + 2,
-              out, resid};
+  GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, nullptr, nullptr, nullptr, out, resid};
   g.ksplit = ks;
   g.partial = part;
   const int tiles = (m + kTok - 1) / kTok;

@@ -41,6 +41,20 @@ __global__ void k_embed_rows(int type, const uint8_t* __restrict__ table, int n_
           : reinterpret_cast<const float*>(table)[idx];
 }
 
+// The last row's residual, router logits and routing into the decode step's
+// per-layer slots (one launch instead of four copies).
+__global__ void k_keep_last(const float* __restrict__ x, const float* __restrict__ logits,
+                            const int32_t* __restrict__ idx, const float* __restrict__ w, int H,
+                            int E, int K, float* __restrict__ hidden, float* __restrict__ rlog,
+                            int32_t* __restrict__ tk_idx, float* __restrict__ tk_w) {
+  for (int i = threadIdx.x; i < H; i += blockDim.x) hidden[i] = x[i];
+  for (int i = threadIdx.x; i < E; i += blockDim.x) rlog[i] = logits[i];
+  if ((int)threadIdx.x < K) {
+    tk_idx[threadIdx.x] = idx[threadIdx.x];
+    tk_w[threadIdx.x] = w[threadIdx.x];
+  }
+}
+
 int palloc(knj_model* m, void** p, uint64_t bytes) {
   KNJ_HIP(hipMalloc(p, std::max<uint64_t>(bytes, 256)));
   m->owned.push_back(*p);
@@ -106,14 +120,11 @@ int prefill_chunk(knj_model* m, const int32_t* tokens, int n, bool last) {
     KNJ_HIP(launch_moe_batch(ma, b.scratch, s));
     if (last) {
       const uint64_t r = (uint64_t)(n - 1);
-      KNJ_HIP(hipMemcpyAsync(m->hidden + (uint64_t)il * H, lastx, (uint64_t)H * 4,
-                             hipMemcpyDeviceToDevice, s));
-      KNJ_HIP(hipMemcpyAsync(m->router_logits + (uint64_t)il * E, b.router_logits + r * E,
-                             (uint64_t)E * 4, hipMemcpyDeviceToDevice, s));
-      KNJ_HIP(hipMemcpyAsync(m->topk_idx + (uint64_t)il * K, b.topk_idx + r * K, (uint64_t)K * 4,
-                             hipMemcpyDeviceToDevice, s));
-      KNJ_HIP(hipMemcpyAsync(m->topk_w + (uint64_t)il * K, b.topk_w + r * K, (uint64_t)K * 4,
-                             hipMemcpyDeviceToDevice, s));
+      k_keep_last<<<1, 256, 0, s>>>(lastx, b.router_logits + r * E, b.topk_idx + r * K,
+                                    b.topk_w + r * K, H, E, K, m->hidden + (uint64_t)il * H,
+                                    m->router_logits + (uint64_t)il * E,
+                                    m->topk_idx + (uint64_t)il * K, m->topk_w + (uint64_t)il * K);
+      KNJ_HIP(hipGetLastError());
     }
   }
   if (last) {
