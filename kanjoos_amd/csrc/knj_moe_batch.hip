@@ -153,38 +153,53 @@ __global__ __launch_bounds__(kBlock) void k_split_tile(const float* __restrict__
 
 // ------------------------------------------------------------------ router
 // logits[t][e] = sum_i hx[t][i] W[e][i] on the f32 matrix cores: workgroup =
-// 16 tokens x 16 experts, the four waves each take a quarter of n_embd and
-// their partial tiles are added in wave order.
-__global__ __launch_bounds__(kBlock) void k_router_batch(const float* __restrict__ hx,
-                                                         const float* __restrict__ w, int m,
-                                                         int n, int n_expert,
-                                                         float* __restrict__ logits) {
-  __shared__ float part[4][256];
+// 16 tokens x 16 experts with kRouterWaves waves, wave w taking the w-th
+// slice of n_embd (n_embd % (16 kRouterWaves) == 0); the partial tiles are
+// added in wave order.  Lane (r, kq) takes the float4 at 16 s + 4 kq of its
+// slice, so a row's four lanes read 64 contiguous bytes, eight float4 of each
+// operand in flight per round, and four accumulation chains (one per float4
+// component) are added at the end.
+constexpr int kRouterWaves = 16;
+__global__ __launch_bounds__(64 * kRouterWaves) void k_router_batch(const float* __restrict__ hx,
+                                                                    const float* __restrict__ w,
+                                                                    int m, int n, int n_expert,
+                                                                    float* __restrict__ logits) {
+  __shared__ float part[kRouterWaves][256];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
   const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
   const int tok = min(t0 + r, m - 1), ex = min(e0 + r, n_expert - 1);
-  const int per = n / 16;  // contiguous k per lane
-  const float* ap = hx + (uint64_t)tok * n + wave * (n / 4) + kq * per;
-  const float* bp = w + (uint64_t)ex * n + wave * (n / 4) + kq * per;
-  f32x4 c = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s = 0; s < per; s += 4) {
-    const float4 a = *reinterpret_cast<const float4*>(ap + s);
-    const float4 b = *reinterpret_cast<const float4*>(bp + s);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.x, b.x, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.y, b.y, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.z, b.z, c, 0, 0, 0);
-    c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.w, b.w, c, 0, 0, 0);
+  const int q = n / kRouterWaves;
+  const float* ap = hx + (uint64_t)tok * n + wave * q + 4 * kq;
+  const float* bp = w + (uint64_t)ex * n + wave * q + 4 * kq;
+  f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, c2 = c0, c3 = c0;
+  for (int s = 0; s < q; s += 128) {
+    float4 a[8], b[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool in = s + 16 * u < q;
+      a[u] = in ? *reinterpret_cast<const float4*>(ap + s + 16 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+      b[u] = in ? *reinterpret_cast<const float4*>(bp + s + 16 * u) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].x, b[u].x, c0, 0, 0, 0);
+      c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].y, b[u].y, c1, 0, 0, 0);
+      c2 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].z, b[u].z, c2, 0, 0, 0);
+      c3 = __builtin_amdgcn_mfma_f32_16x16x4f32(a[u].w, b[u].w, c3, 0, 0, 0);
+    }
   }
   // c[i] = C[token 4kq+i][expert r]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) part[wave][(4 * kq + i) * 16 + r] = c[i];
+  for (int i = 0; i < 4; ++i) part[wave][(4 * kq + i) * 16 + r] = (c0[i] + c1[i]) + (c2[i] + c3[i]);
   __syncthreads();
-  const int tt = threadIdx.x >> 4, ee = threadIdx.x & 15;
-  if (t0 + tt < m && e0 + ee < n_expert) {
-    const int q = tt * 16 + ee;
-    logits[(uint64_t)(t0 + tt) * n_expert + e0 + ee] =
-        ((part[0][q] + part[1][q]) + part[2][q]) + part[3][q];
+  if (threadIdx.x < 256) {
+    const int tt = threadIdx.x >> 4, ee = threadIdx.x & 15;
+    if (t0 + tt < m && e0 + ee < n_expert) {
+      float v = part[0][threadIdx.x];
+      for (int ww = 1; ww < kRouterWaves; ++ww) v += part[ww][threadIdx.x];
+      logits[(uint64_t)(t0 + tt) * n_expert + e0 + ee] = v;
+    }
   }
 }
 
@@ -594,7 +609,8 @@ __global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
                                                     const int32_t* __restrict__ topk_idx,
                                                     const float* __restrict__ topk_w, int k,
                                                     int n, const float* __restrict__ resid,
-                                                    float* __restrict__ out) {
+                                                    float* __restrict__ out,
+                                                    float* __restrict__ out2) {
   const int t = blockIdx.x;
   int ids[16], pr[16], rank[16];
   float wt[16];
@@ -651,6 +667,7 @@ __global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
     o.w = __fadd_rn(rs.w, o.w);
   }
   *reinterpret_cast<float4*>(out + (uint64_t)t * n + i) = o;
+  if (out2) *reinterpret_cast<float4*>(out2 + (uint64_t)t * n + i) = o;
 }
 
 }  // namespace
@@ -689,6 +706,8 @@ hipError_t group_lds_attr() {
 hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s) {
   if (hipError_t e = group_lds_attr()) return e;
   const int m = a.m, H = a.n_embd, F = a.n_ff, E = a.n_expert, K = a.k;
+  if (H % 256 || F % 256 || H > 4096 || F > 4096 || E > 256 || K > 16 || m <= 0)
+    return hipErrorInvalidValue;
   const uint64_t P = (uint64_t)m * K;
   const int max_items = E + (int)((P + kTok - 1) / kTok);
   uint8_t* p = (uint8_t*)scratch;
@@ -719,7 +738,7 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
     KNJ_LAUNCH(k_norm_rows, dim3(m), dim3(kBlock), 0, s, a.x, a.norm_w, a.eps, H, hx);
     xin = hx;
   }
-  KNJ_LAUNCH(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(kBlock), 0, s, xin,
+  KNJ_LAUNCH(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(64 * kRouterWaves), 0, s, xin,
                      a.router_w, m, H, E, a.logits);
   KNJ_LAUNCH(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, a.logits, m, E, K,
                      a.topk_idx, a.topk_w);
@@ -736,11 +755,8 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                      kGroupLds, s, dn);
   KNJ_LAUNCH(k_combine, dim3(m, (H + 4 * kBlock - 1) / (4 * kBlock)), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
-                     H, a.resid, a.out);
-  hipError_t e = hipGetLastError();
-  if (e == hipSuccess && a.hidden_copy)
-    e = hipMemcpyAsync(a.hidden_copy, a.out, (uint64_t)m * H * 4, hipMemcpyDeviceToDevice, s);
-  return e;
+                     H, a.resid, a.out, a.hidden_copy);
+  return hipGetLastError();
 }
 
 // ---- dense batched GEMMs of the batched decode step
