@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Decode benchmark: BASELINE config 3 on one MI355X.
+"""Decode benchmark: 48-layer Qwen3-30B-A3B-shaped greedy decode at batch 1 on one MI355X.
 
 Workload: the 48-layer Qwen3-30B-A3B-shaped model (hidden 2048, 32/4 heads x 128
 with QK-RMSNorm, RoPE theta 1e6, 128 experts top-8 of width 768, vocab 151936;
@@ -66,7 +66,7 @@ def expert_traffic():
 
 
 def moe_batch_leg(model: K.Model, cfg: K.ModelConfig, m: int, iters: int) -> dict:
-    """one MoE layer (the model's layer 0: router, 128 Q4_K
+    """Batched MoE leg (config 2): one MoE layer (the model's layer 0: router, 128 Q4_K
     experts) over m tokens at once, x ~ N(0,1) with ffn_norm, timed with HIP
     events over `iters` calls of knj_moe_batch_layer on the default stream."""
     import ctypes as C
@@ -108,7 +108,7 @@ def moe_batch_leg(model: K.Model, cfg: K.ModelConfig, m: int, iters: int) -> dic
 
 
 def long_ctx_leg(seed: int, ctx: int, steps: int) -> dict:
-    """the Q4_K_M-style mix (Q6_K expert down and LM head),
+    """Long-context leg (config 5): the Q4_K_M-style mix (Q6_K expert down and LM head),
     batch 1, f16 KV cache at `ctx` tokens, greedy decode timed over `steps`.  The
     cache is filled with seeded f16 values instead of running the prefill."""
     cfg = K.qwen3_30b_a3b(n_ctx=ctx + steps + 8, type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)
@@ -132,7 +132,7 @@ def long_ctx_leg(seed: int, ctx: int, steps: int) -> dict:
 
 
 def batch_leg(model: K.Model, seed: int, n_seq: int, ctx: int, steps: int) -> dict:
-    """n_seq concurrent greedy sequences on the same weights,
+    """Batched-decode leg (config 4): n_seq concurrent greedy sequences on the same weights,
     each with its own f16 KV cache at `ctx` tokens (filled with seeded values
     instead of a prefill), `steps` lockstep decode steps timed."""
     batch = K.Batch(model, n_seq, ctx + steps + 8)

@@ -1,5 +1,5 @@
 // kanjoos_amd/csrc/knj_batch.hip -- greedy decode of several sequences at once
-// (32 concurrent sequences, each with its own f16 KV cache).
+// (for example 32 concurrent sequences, each with its own f16 KV cache).
 //
 // One step runs Model::forward's per-token work (/root/reference/src/model/model.cpp:512-672)
 // for n_seq tokens together: every weight matrix is read once for all of them.

@@ -44,7 +44,7 @@ class ModelConfig(C.Structure):
 
 
 def make_config(**kw) -> ModelConfig:
-    """Qwen3-30B-A3B geometry by default (BASELINE config 3); override any field."""
+    """Qwen3-30B-A3B geometry by default; override any field."""
     base = dict(n_layer=48, n_embd=2048, n_head=32, n_head_kv=4, head_dim=128, n_ff=768,
                 n_expert=128, n_expert_used=8, n_vocab=151936, n_ctx=4352, rms_eps=1e-6,
                 rope_base=1e6, type_embd=TYPE_BF16, type_attn=TYPE_Q4_K,

@@ -1,10 +1,10 @@
 #!/usr/bin/env python3
 """Writes the golden fixtures under tests/golden/ from the CPU oracle.
 
-  config1.json      BASELINE config 1 at seed 0: router logits, top-8 indices and
+  config1.json      one MoE layer, one token, seed 0: router logits, top-8 indices and
                     weights, and the MoE output of one layer (x ~ N(0,1), RMSNorm
                     weight 1, router f32 ~ N(0,0.02), 128 Q4_K experts).
-  full_greedy.json  BASELINE config 3's model (48 layers, seed 0): 64 greedy
+  full_greedy.json  the 48-layer Qwen3-30B-A3B-shaped model (seed 0): 64 greedy
                     tokens after the prompt [1, 2, 3, 4] (one forward call over
                     the prompt, as the reference's Model::forward runs it), with
                     the top-1/top-2 logit margin of every step.

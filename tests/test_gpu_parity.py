@@ -1,6 +1,6 @@
 """GPU parity: the HIP path through the C ABI against the CPU oracle, same seeded inputs.
 
-Bars (BASELINE north star): dequantised weights and top-k indices bit-exact;
+Bars: dequantised weights and top-k indices bit-exact;
 fp32 outputs within 1e-5 relative RMSE (the reference's metric,
 tests/host_oracle.h:143-171); greedy tokens identical.
 """
@@ -74,7 +74,7 @@ def test_gemv_fused_norm_and_residual(device):
 
 
 def moe_layer_inputs(n_embd=2048, n_ff=768, n_expert=128, type_down=K.TYPE_Q4_K, layer=0):
-    """x ~ N(0,1), router f32 ~ N(0,0.02), Q4_K experts ~ N(0,0.02)."""
+    """One MoE layer, one token: x ~ N(0,1), router f32 ~ N(0,0.02), Q4_K experts ~ N(0,0.02)."""
     x = O.synth_f32(O.tensor_key(SEED, layer, "input"), n_embd)
     router = O.synth_tensor(O.tensor_key(SEED, layer, "router"), K.TYPE_F32, n_embd, n_expert)
     gate = np.concatenate([O.synth_tensor(O.tensor_key(SEED, layer, "gate", e), K.TYPE_Q4_K, n_embd, n_ff)
@@ -325,7 +325,7 @@ GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 
 
 def test_config1_against_golden(device):
-    """BASELINE config 1 on the GPU against the committed oracle fixture."""
+    """One MoE layer, one token, on the GPU against the committed oracle fixture."""
     want = json.load(open(os.path.join(GOLDEN, "config1.json")))
     n_embd, n_ff, n_expert, k = 2048, 768, 128, 8
     x, router, gate, up, down = moe_layer_inputs()
