@@ -110,8 +110,8 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
  *   expert's weights are read once for all its tokens; gate/up, silu(gate)*up,
  *   down; out[t] = resid[t] + sum over t's experts in ascending index of
  *   w * down.  x, resid, out: [n_tokens][n_embd]; logits: [n_tokens][n_expert];
- *   topk_idx/topk_w: [n_tokens][k].  Q4_K gate/up/down; n_embd and n_ff
- *   multiples of 256, at most 4096; n_expert <= 256; k <= 16. */
+ *   topk_idx/topk_w: [n_tokens][k].  Q4_K gate/up, Q4_K or Q6_K down; n_embd
+ *   and n_ff multiples of 256, at most 4096; n_expert <= 256; k <= 16. */
 int knj_moe_batch_layer(const float* x, const float* norm_w, float eps, const float* router_w,
                         const void* gate, const void* up, const void* down, int type_gate_up,
                         int type_down, int n_tokens, int n_embd, int n_ff, int n_expert, int k,
@@ -194,8 +194,9 @@ int knj_model_set_pos(knj_model* m, int pos);
  * positions pos .. pos+n-1.  n == 1 is one decode step (the captured graph);
  * n > 1 is the prompt pass: every weight applied to up to 512 rows at once,
  * each row's key and value appended, causal attention (row t over slots
- * 0 .. pos+t), the head on the last row -- for Q4_K attention and experts
- * (other tensor types take one decode step per token).  logits_host (n_vocab
+ * 0 .. pos+t), the head on the last row -- for Q4_K attention and gate/up
+ * and Q4_K or Q6_K expert down (other tensor types take one decode step per
+ * token).  logits_host (n_vocab
  * floats, may be NULL) receives the last token's logits; the per-layer
  * hidden/top-k queries then describe the last token.  Errors: KNJ_E_ARG for
  * token ids out of range or a full context (model.cpp:514-517, 533), nothing

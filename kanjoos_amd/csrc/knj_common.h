@@ -111,7 +111,7 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0 
 
 // MoE layer over m tokens at once (prefill chunks, batched decode): RMSNorm,
 // router, per-token top-k, experts grouped on the matrix cores, combine.
-// Q4_K gate/up/down, n_embd and n_ff multiples of 256 and <= 4096,
+// Q4_K gate/up, Q4_K or Q6_K down, n_embd and n_ff multiples of 256 and <= 4096,
 // n_expert <= 256, k <= 16.
 struct MoeBatchArgs {
   const float* x;          // [m][n_embd] residual stream
@@ -128,6 +128,7 @@ struct MoeBatchArgs {
   int32_t* topk_idx;       // [m][k], selection order
   float* topk_w;           // [m][k]
   float* hidden_copy = nullptr;  // optional second destination of out
+  int type_down = KNJ_TYPE_Q4_K;  // Q4_K or Q6_K
 };
 uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int k);
 hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s);

@@ -307,8 +307,9 @@ int knj_moe_batch_layer(const float* x, const float* norm_w, float eps, const fl
                 "n_ff must be a positive multiple of 256, at most 4096");
   KNJ_CHECK_ARG(n_expert > 0 && n_expert <= 256, "n_expert must be in [1, 256]");
   KNJ_CHECK_ARG(k > 0 && k <= 16 && k <= n_expert, "k must be in [1, min(16, n_expert)]");
-  KNJ_CHECK_ARG(type_gate_up == KNJ_TYPE_Q4_K && type_down == KNJ_TYPE_Q4_K,
-                "the batched expert path takes Q4_K gate/up/down");
+  KNJ_CHECK_ARG(type_gate_up == KNJ_TYPE_Q4_K &&
+                    (type_down == KNJ_TYPE_Q4_K || type_down == KNJ_TYPE_Q6_K),
+                "the batched expert path takes Q4_K gate/up and Q4_K or Q6_K down");
   KNJ_CHECK_ARG(x && router_w && gate && up && down && out && logits && topk_idx && topk_w,
                 "null pointer");
   hipStream_t s = (hipStream_t)stream;
@@ -317,6 +318,7 @@ int knj_moe_batch_layer(const float* x, const float* norm_w, float eps, const fl
   MoeBatchArgs a{x, norm_w, eps, router_w, (const uint8_t*)gate, (const uint8_t*)up,
                  (const uint8_t*)down, n_tokens, n_embd, n_ff, n_expert, k, resid, out, logits,
                  topk_idx, topk_w};
+  a.type_down = type_down;
   KNJ_HIP(launch_moe_batch(a, scr, s));
   return KNJ_OK;
 }

@@ -465,6 +465,116 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
   }
 }
 
+// Q6_K down projection of the grouped MoE (d * sc * (q - 32) per weight,
+// sc per 16 weights): the same workgroup tiling and A staging as
+// k_group_q4k, but one matrix-core step covers exactly one 16-weight scale
+// group G of a super-block: lane half kh supplies weights 16 G + 8 kh + (0..7)
+// of its row (in the staging's perm8 order) as exact f16 values q - 32, and
+// reads the activations of 8-group 2 G + kh.  A step's two products (high
+// parts, remainders) start from zero and are added to the accumulator scaled
+// by d * sc_G.  Q6_K blocks are 210 bytes, so the lane's byte runs are read
+// as aligned words and shifted into place (ld8_u2).  ksplit 1, no residual.
+struct Q6WBlock {
+  uint32_t la[2][2][2], lb[2][2][2], qh[2][2][2];  // [half n][16-run lh][word]: ql +0, ql +32, qh
+  uint32_t sc[4];                                   // the 16 int8 scales
+  uint32_t d;                                       // f16 bits
+};
+
+__global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
+  extern __shared__ uint4 lds[];
+  const int item = blockIdx.y;
+  if (item >= *a.n_items) return;  // uniform over the workgroup
+  const int2 it = a.items[item];
+  const int e = it.x;
+  const int p0 = a.offsets[e] + it.y;
+  const int cnt = min(kTok, a.offsets[e + 1] - p0);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int rbase = blockIdx.x * kRowsWG + wave * 32;
+  const bool rows_ok = rbase < a.n_out;
+  const int row = min(rbase + (lane & 31), a.n_out - 1), kh = lane >> 5;
+  const int j = lane & 31;
+  const int nsb = a.n_in >> 8;
+  const uint64_t P = (uint64_t)a.P;
+  const uint64_t rb = (uint64_t)nsb * KNJ_Q6K_BLOCK;
+  const uint8_t* wr = a.w0 + (uint64_t)e * rb * (uint64_t)a.n_out + (uint64_t)row * rb;
+  auto a_src = [&](int sb, int u) -> const uint4* {
+    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
+    const _Float16* base = part ? a.al : a.ah;
+    return reinterpret_cast<const uint4*>(base + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8);
+  };
+  auto a_dst = [&](int buf, int u) -> uint4* {
+    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
+    return lds + buf * kBuf + part * kPart + q * kQStride + jj;
+  };
+  auto w_load = [&](int sb, Q6WBlock& w) {
+    const uint8_t* b = wr + (uint64_t)sb * KNJ_Q6K_BLOCK;
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int lh = 0; lh < 2; ++lh) {
+        const int l = 16 * lh + 8 * kh;
+        ld8_u2(b + KNJ_Q6K_QL + 64 * n + l, w.la[n][lh][0], w.la[n][lh][1]);
+        ld8_u2(b + KNJ_Q6K_QL + 64 * n + 32 + l, w.lb[n][lh][0], w.lb[n][lh][1]);
+        ld8_u2(b + KNJ_Q6K_QH + 32 * n + l, w.qh[n][lh][0], w.qh[n][lh][1]);
+      }
+    ld8_u2(b + KNJ_Q6K_SC, w.sc[0], w.sc[1]);
+    ld8_u2(b + KNJ_Q6K_SC + 8, w.sc[2], w.sc[3]);
+    w.d = *reinterpret_cast<const uint16_t*>(b + KNJ_Q6K_D);
+  };
+  uint4 st[8];
+  Q6WBlock wc, wn;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) st[u] = *a_src(0, u);
+  w_load(0, wc);
+#pragma unroll
+  for (int u = 0; u < 8; ++u) *a_dst(0, u) = st[u];
+  __syncthreads();
+  f32x16 acc = {};
+  const half2v bias = half2v{(_Float16)1056.0f, (_Float16)1056.0f};  // 1024 + 32
+  auto cv = [&](uint32_t w) { return as_h2((w & 0x00FF00FFu) | 0x64006400u) - bias; };
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int buf = sb & 1;
+    const int nx = min(sb + 1, nsb - 1);  // the last iteration reloads its own block, unused
+#pragma unroll
+    for (int u = 0; u < 8; ++u) st[u] = *a_src(nx, u);
+    w_load(nx, wn);
+    const uint4* L = lds + buf * kBuf;
+    const float d = h2f(wc.d);
+#pragma unroll
+    for (int n = 0; n < 2; ++n)
+#pragma unroll
+      for (int lh = 0; lh < 2; ++lh)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const int G = 8 * n + 2 * s4 + lh;  // weights 16 G .. 16 G + 15
+          const uint32_t* ql = (s4 & 1) ? wc.lb[n][lh] : wc.la[n][lh];
+          const int nsh = 4 * (s4 >> 1), hsh = 2 * s4;
+          const uint32_t q0 = ((ql[0] >> nsh) & 0x0F0F0F0Fu) | (((wc.qh[n][lh][0] >> hsh) & 0x03030303u) << 4);
+          const uint32_t q1 = ((ql[1] >> nsh) & 0x0F0F0F0Fu) | (((wc.qh[n][lh][1] >> hsh) & 0x03030303u) << 4);
+          const half2v b0 = cv(q0), b1 = cv(q0 >> 8), b2 = cv(q1), b3 = cv(q1 >> 8);
+          const half8 bw = half8{b0.x, b0.y, b1.x, b1.y, b2.x, b2.y, b3.x, b3.y};
+          const half8 xh = __builtin_bit_cast(half8, L[(2 * G + kh) * kQStride + j]);
+          const half8 xl = __builtin_bit_cast(half8, L[kPart + (2 * G + kh) * kQStride + j]);
+          f32x16 c = mfma32(xh, bw, f32x16{});
+          c = mfma32(xl, bw, c);
+          const float sg = d * (float)(int8_t)((wc.sc[G >> 2] >> (8 * (G & 3))) & 0xFFu);
+#pragma unroll
+          for (int i = 0; i < 16; ++i) acc[i] += sg * c[i];
+        }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) *a_dst(buf ^ 1, u) = st[u];
+    wc = wn;
+    __syncthreads();
+  }
+  if (!rows_ok || rbase + (lane & 31) >= a.n_out) return;
+  // acc[i] = C[token 8*(i/4) + 4*kh + i%4][row]
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int tj = 8 * (i / 4) + 4 * kh + (i % 4);
+    if (tj < cnt) a.out[(uint64_t)(p0 + tj) * a.n_out + row] = acc[i];
+  }
+}
+
 // out[i] = resid[i] + sum_z partial[z][i], the ranges added in order (resid
 // may alias out).
 __global__ __launch_bounds__(kBlock) void k_ksum(const float* __restrict__ partial, int ksplit,
@@ -698,6 +808,9 @@ hipError_t group_lds_attr() {
     if (r == hipSuccess)
       r = hipFuncSetAttribute((const void*)k_group_q4k<false>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGroupLds);
+    if (r == hipSuccess)
+      r = hipFuncSetAttribute((const void*)k_group_q6k,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGroupLds);
     return r;
   }();
   return e;
@@ -706,7 +819,8 @@ hipError_t group_lds_attr() {
 hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s) {
   if (hipError_t e = group_lds_attr()) return e;
   const int m = a.m, H = a.n_embd, F = a.n_ff, E = a.n_expert, K = a.k;
-  if (H % 256 || F % 256 || H > 4096 || F > 4096 || E > 256 || K > 16 || m <= 0)
+  if (H % 256 || F % 256 || H > 4096 || F > 4096 || E > 256 || K > 16 || m <= 0 ||
+      (a.type_down != KNJ_TYPE_Q4_K && a.type_down != KNJ_TYPE_Q6_K))
     return hipErrorInvalidValue;
   const uint64_t P = (uint64_t)m * K;
   const int max_items = E + (int)((P + kTok - 1) / kTok);
@@ -752,8 +866,12 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), F / 256), dim3(kBlock), 0, s, act,
              nullptr, F, (int)P, ah, al, sah, sal);
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
-  KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
-                     kGroupLds, s, dn);
+  if (a.type_down == KNJ_TYPE_Q6_K)
+    KNJ_LAUNCH(k_group_q6k, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock), kGroupLds,
+               s, dn);
+  else
+    KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+               kGroupLds, s, dn);
   KNJ_LAUNCH(k_combine, dim3(m, (H + 4 * kBlock - 1) / (4 * kBlock)), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
                      H, a.resid, a.out, a.hidden_copy);
   return hipGetLastError();

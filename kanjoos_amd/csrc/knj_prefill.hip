@@ -117,6 +117,7 @@ int prefill_chunk(knj_model* m, const int32_t* tokens, int n, bool last) {
                     reinterpret_cast<const float*>(img + lo.router), img + lo.gate, img + lo.up,
                     img + lo.down, n, H, c.n_ff, E, K, b.x, b.x, b.router_logits, b.topk_idx,
                     b.topk_w};
+    ma.type_down = c.type_down;
     KNJ_HIP(launch_moe_batch(ma, b.scratch, s));
     if (last) {
       const uint64_t r = (uint64_t)(n - 1);
@@ -145,7 +146,8 @@ bool prefill_eligible(const knj_model* m) {
   const knj_model_config& c = m->c;
   const int QD = c.n_head * c.head_dim;
   return c.type_attn == KNJ_TYPE_Q4_K && c.type_gate_up == KNJ_TYPE_Q4_K &&
-         c.type_down == KNJ_TYPE_Q4_K && c.type_head != KNJ_TYPE_Q4_K &&
+         (c.type_down == KNJ_TYPE_Q4_K || c.type_down == KNJ_TYPE_Q6_K) &&
+         c.type_head != KNJ_TYPE_Q4_K &&
          c.n_embd % 256 == 0 && c.n_embd <= 4096 && QD % 256 == 0 && QD <= 4096 &&
          c.n_ff % 256 == 0 && c.n_ff <= 4096 && c.n_expert <= 256 && c.n_expert_used <= 16 &&
          prefill_attention_ok(c.n_head, c.n_head_kv, c.head_dim);

@@ -115,19 +115,29 @@ def config1_weights():
     return moe_layer_inputs()
 
 
-@pytest.mark.parametrize("m", [1, 7, 64, 512])
-def test_moe_batch_layer(device, config1_weights, m):
+@pytest.fixture(scope="module")
+def q6_down_weights():
+    return moe_layer_inputs(type_down=K.TYPE_Q6_K)
+
+
+@pytest.mark.parametrize("m,type_down", [(1, K.TYPE_Q4_K), (7, K.TYPE_Q4_K), (64, K.TYPE_Q4_K),
+                                         (512, K.TYPE_Q4_K), (7, K.TYPE_Q6_K), (64, K.TYPE_Q6_K),
+                                         (512, K.TYPE_Q6_K)])
+def test_moe_batch_layer(device, config1_weights, q6_down_weights, m, type_down):
     """Config 2 (m = 512) and smaller batches: the batched MoE layer against the
-    oracle's Model::moe on the same m rows (top-k bit-exact, out <= 1e-5)."""
+    oracle's Model::moe on the same m rows (top-k bit-exact, out <= 1e-5), with
+    Q4_K or Q6_K (d * sc * (q - 32) per 16 weights) expert down."""
     n_embd, n_ff, n_expert, k = 2048, 768, 128, 8
-    say(f"moe batch layer m={m}")
-    _, router, gate, up, down = config1_weights
+    say(f"moe batch layer m={m} type_down={type_down}")
+    w = config1_weights if type_down == K.TYPE_Q4_K else q6_down_weights
+    _, router, gate, up, down = w
     rng = np.random.default_rng(100 + m)
     x = rng.standard_normal((m, n_embd)).astype(np.float32)
     resid = rng.standard_normal((m, n_embd)).astype(np.float32)
     ones = np.ones(n_embd, np.float32)
     hx = np.stack([O.rmsnorm(x[t], ones, 1e-6) for t in range(m)])
-    out_w, logits_w, ti_w, tw_w = O.moe(hx, router, gate, up, down, n_embd, n_ff, n_expert, k)
+    out_w, logits_w, ti_w, tw_w = O.moe(hx, router, gate, up, down, n_embd, n_ff, n_expert, k,
+                                       type_down=type_down)
     d = {nm: K.DeviceBuffer.from_array(a) for nm, a in
          dict(x=x, resid=resid, router=router, gate=gate, up=up, down=down, ones=ones).items()}
     out = K.DeviceBuffer(4 * m * n_embd)
@@ -135,7 +145,8 @@ def test_moe_batch_layer(device, config1_weights, m):
     ti = K.DeviceBuffer(4 * m * k)
     tw = K.DeviceBuffer(4 * m * k)
     K.moe_batch_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], m, n_embd, n_ff, n_expert,
-                      k, out, logits, ti, tw, norm_w=d["ones"], eps=1e-6, resid=d["resid"])
+                      k, out, logits, ti, tw, norm_w=d["ones"], eps=1e-6, resid=d["resid"],
+                      type_down=type_down)
     got_ti = ti.download(np.int32).reshape(m, k)
     bad = np.flatnonzero((got_ti != ti_w).any(axis=1))
     assert bad.size == 0, f"top-k differs for tokens {bad[:8]}"
@@ -245,6 +256,7 @@ PREFILL_SHAPES = {
     "g8_d128": dict(n_head=32, n_head_kv=4, head_dim=128),
     "g1_d64": dict(n_head=4, n_head_kv=4),
     "g2_d128": dict(n_head=8, n_head_kv=4, head_dim=128),
+    "q6k_down": dict(type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K),
 }
 
 
