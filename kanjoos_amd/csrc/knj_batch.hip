@@ -133,11 +133,15 @@ int enqueue_batch_step(knj_batch* b, hipStream_t s) {
                     b->topk_idx + (uint64_t)il * B * c.n_expert_used,
                     b->topk_w + (uint64_t)il * B * c.n_expert_used};
     ma.hidden_copy = b->hidden + (uint64_t)il * B * H;
+    ma.type_down = c.type_down;
     KNJ_HIP(launch_moe_batch(ma, b->scratch, s));
   }
   KNJ_HIP(launch_norm_rows(b->x, reinterpret_cast<const float*>(img + m->off_onorm), c.rms_eps, B,
                            H, b->hx, s));
-  KNJ_HIP(launch_dense_bf16(reinterpret_cast<const uint16_t*>(img + m->off_head), H, c.n_vocab, B,
+  if (c.type_head == KNJ_TYPE_Q6_K)
+    KNJ_HIP(launch_dense_q6k(img + m->off_head, H, c.n_vocab, B, b->hx, b->logits, b->scratch, s));
+  else
+    KNJ_HIP(launch_dense_bf16(reinterpret_cast<const uint16_t*>(img + m->off_head), H, c.n_vocab, B,
                             b->hx, b->logits, b->scratch, s));
   KNJ_HIP(launch_argmax_rows(b->logits, B, c.n_vocab, b->keys, b->next, s));
   KNJ_LAUNCH(k_batch_close, dim3(1), dim3(std::max(64, (B + 63) / 64 * 64)), 0, s, B,
@@ -202,8 +206,10 @@ int knj_batch_create(knj_model* m, int n_seq, int n_ctx, knj_batch** out) {
   KNJ_CHECK_ARG(n_ctx >= 1 && n_ctx <= c.n_ctx,
                 "n_ctx must be in [1, the model's n_ctx] (the RoPE tables are the model's)");
   KNJ_CHECK_ARG(c.type_attn == KNJ_TYPE_Q4_K && c.type_gate_up == KNJ_TYPE_Q4_K &&
-                    c.type_down == KNJ_TYPE_Q4_K && c.type_head == KNJ_TYPE_BF16,
-                "the batched step takes Q4_K attention and experts and a bf16 LM head");
+                    (c.type_down == KNJ_TYPE_Q4_K || c.type_down == KNJ_TYPE_Q6_K) &&
+                    (c.type_head == KNJ_TYPE_BF16 || c.type_head == KNJ_TYPE_Q6_K),
+                "the batched step takes Q4_K attention and gate/up, Q4_K or Q6_K down and a "
+                "bf16 or Q6_K LM head");
   KNJ_CHECK_ARG(c.n_head * c.head_dim <= 4096 && (c.n_head * c.head_dim) % 256 == 0,
                 "n_head * head_dim must be a multiple of 256, at most 4096");
   KNJ_CHECK_ARG(c.n_ff <= 4096 && c.n_ff % 256 == 0, "n_ff must be a multiple of 256, at most 4096");

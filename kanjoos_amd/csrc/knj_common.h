@@ -145,6 +145,9 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
                             const float* resid, float* out, void* scratch, hipStream_t s);
 hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, const float* x,
                              float* out, void* scratch, hipStream_t s);
+// Q6_K (no residual, no reduction split): scratch dense_scratch_bytes(m, n_in, 0).
+hipError_t launch_dense_q6k(const uint8_t* w, int n_in, int n_out, int m, const float* x,
+                            float* out, void* scratch, hipStream_t s);
 // Greedy token of every row of logits [m][n]; keys: m * argmax_key_count(n) scratch.
 int argmax_key_count(int n);
 hipError_t launch_argmax_rows(const float* logits, int m, int n, unsigned long long* keys,

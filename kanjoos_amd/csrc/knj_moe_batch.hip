@@ -474,6 +474,8 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
 // parts, remainders) start from zero and are added to the accumulator scaled
 // by d * sc_G.  Q6_K blocks are 210 bytes, so the lane's byte runs are read
 // as aligned words and shifted into place (ld8_u2).  ksplit 1, no residual.
+// With null offsets the P rows are one expert (a dense product, e.g. a Q6_K
+// LM head over a batch of rows).
 struct Q6WBlock {
   uint32_t la[2][2][2], lb[2][2][2], qh[2][2][2];  // [half n][16-run lh][word]: ql +0, ql +32, qh
   uint32_t sc[4];                                   // the 16 int8 scales
@@ -482,12 +484,17 @@ struct Q6WBlock {
 
 __global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
   extern __shared__ uint4 lds[];
-  const int item = blockIdx.y;
-  if (item >= *a.n_items) return;  // uniform over the workgroup
-  const int2 it = a.items[item];
-  const int e = it.x;
-  const int p0 = a.offsets[e] + it.y;
-  const int cnt = min(kTok, a.offsets[e + 1] - p0);
+  // grouped: work item blockIdx.y; dense (no offsets): tile blockIdx.y of the
+  // P rows seen as one expert
+  int e = 0, p0 = blockIdx.y * kTok, cnt = min(kTok, a.P - p0);
+  if (a.offsets) {
+    const int item = blockIdx.y;
+    if (item >= *a.n_items) return;  // uniform over the workgroup
+    const int2 it = a.items[item];
+    e = it.x;
+    p0 = a.offsets[e] + it.y;
+    cnt = min(kTok, a.offsets[e + 1] - p0);
+  }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int rbase = blockIdx.x * kRowsWG + wave * 32;
   const bool rows_ok = rbase < a.n_out;
@@ -951,6 +958,29 @@ hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, cons
   KNJ_LAUNCH(k_split_bf16x3, dim3(m), dim3(kBlock), 0, s, x, n_in, m, xh, xm, xl);
   KNJ_LAUNCH(k_dense_bf16, dim3((n_out + kRowsWG - 1) / kRowsWG, (m + kTok - 1) / kTok),
                      dim3(kBlock), 0, s, w, n_in, n_out, m, xh, xm, xl, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_q6k(const uint8_t* w, int n_in, int n_out, int m, const float* x,
+                            float* out, void* scratch, hipStream_t s) {
+  if (hipError_t e = group_lds_attr()) return e;
+  if (n_in > 4096 || n_in % 256 || n_out % 32 || m > 1024 || m <= 0) return hipErrorInvalidValue;
+  const uint64_t P = (uint64_t)m;
+  uint8_t* p = (uint8_t*)scratch;
+  auto take = [&](uint64_t bytes) {
+    uint8_t* q = p;
+    p += (bytes + 255) & ~255ull;
+    return q;
+  };
+  _Float16* xh = (_Float16*)take(P * n_in * 2);
+  _Float16* xl = (_Float16*)take(P * n_in * 2);
+  _Float16* sh = (_Float16*)take(P * n_in / 16);
+  _Float16* sl = (_Float16*)take(P * n_in / 16);
+  KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 256), dim3(kBlock), 0, s, x, nullptr,
+             n_in, m, xh, xl, sh, sl);
+  GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, nullptr, nullptr, nullptr, out, nullptr};
+  KNJ_LAUNCH(k_group_q6k, dim3((n_out + kRowsWG - 1) / kRowsWG, (m + kTok - 1) / kTok),
+             dim3(kBlock), kGroupLds, s, g);
   return hipGetLastError();
 }
 

@@ -464,12 +464,13 @@ def test_attention_step(device, n_head, n_kv, D, pos, n_ctx):
     assert rel_rmse(out, ref_out) <= 1e-5
 
 
-def test_batch_decode_parity(device):
+@pytest.mark.parametrize("cfgkw", [dict(), dict(type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)])
+def test_batch_decode_parity(device, cfgkw):
     """Config 4's batched step on a small model: three sequences with different
     prompts stepped together; every step, every sequence against its own oracle
     model (per-layer hidden <= 1e-5, top-k exact, logits <= 1e-5), with the same
-    f16 KV adoption as the single-sequence parity test."""
-    cfg = small_config()
+    f16 KV adoption as the single-sequence parity test; bf16 or Q6_K head."""
+    cfg = small_config(**cfgkw)
     n_ctx = cfg["n_ctx"]
     gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
     img = gm.download_image()
@@ -500,10 +501,11 @@ def test_batch_decode_parity(device):
     gm.close()
 
 
-def test_batch_greedy_matches_single(device):
+@pytest.mark.parametrize("cfgkw", [dict(), dict(type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)])
+def test_batch_greedy_matches_single(device, cfgkw):
     """The batched greedy loop and the single-sequence loop give the same tokens
     for every sequence (small model, 24 steps)."""
-    cfg = small_config()
+    cfg = small_config(**cfgkw)
     gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
     B, steps = 4, 24
     prompts = np.array([[1, 2, 3], [9, 8, 7], [11, 12, 13], [3, 2, 1]], dtype=np.int32)
