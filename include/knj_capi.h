@@ -165,7 +165,8 @@ int knj_model_fill_kv(knj_model* m, int n_pos, uint64_t seed);
  * (model.cpp:512-672) for n_seq tokens at once, each sequence with its own f16
  * KV cache of n_ctx slots (n_ctx <= the model's) and its own position.  Every
  * weight matrix is read once per step for all sequences (matrix-core GEMMs;
- * the MoE pairs grouped by expert).  Q4_K attention and experts, bf16 head.
+ * the MoE pairs grouped by expert).  Q4_K attention and gate/up, Q4_K or Q6_K
+ * expert down, bf16 or Q6_K head.
  * knj_batch_forward: one step on tokens[n_seq]; logits_out [n_seq][n_vocab]
  *   (may be NULL).  knj_batch_decode_greedy: `steps` greedy steps from
  *   first[n_seq]; out_tokens [steps][n_seq].  Hidden states, top-k and caches
