@@ -176,46 +176,71 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   const int r = lane & 15, kq = lane >> 4;
   const bool hv = r < G;
   const int h0 = 2 * wave, h1 = 2 * wave + 1;
+  // softmax in base 2: scores carry log2(e), so e^(s - m) = 2^(s log2 e - m log2 e);
+  // the partial records' maxima are in these units (the merges use exp2)
+  const float scale2 = a.scale * 1.4426950408889634f;
   float m0 = -INFINITY, m1 = -INFINITY, l0 = 0.0f, l1 = 0.0f;  // running max / sum (softmax waves)
   f32x4 oe = {0.0f, 0.0f, 0.0f, 0.0f}, oo = {0.0f, 0.0f, 0.0f, 0.0f};
   for (int j = 0; j < nch; ++j) {
     const int p0 = (c0 + j) * kChunk;
     const int cnt = min(kChunk, n_kv - p0);
-    // 3) the slot written this step, if it is in this chunk
-    if (pos >= p0 && pos < p0 + cnt && tid < T) {
-      const int lp = pos - p0;
+    // 3) the slot written this step goes to the cache now; in LDS it is
+    // written over the staged chunk below
+    const bool here = pos >= p0 && pos < p0 + cnt;  // uniform
+    if (here && tid < T) {
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         kc[(uint64_t)pos * D + 4 * tid + k] = kh[k];
         vc[(uint64_t)pos * D + 4 * tid + k] = vh[k];
-        ks[lp * ROWH + 4 * tid + k] = kh[k];
-        vt[vti(4 * tid + k, lp)] = vh[k];
       }
     }
     KNJ_STAMP(2);
     // cache rows past the valid length become zeros: the value product below
-    // runs over all 64 rows with weight 0 there
+    // runs over all 64 rows with weight 0 there.  V goes in as (slot p, slot
+    // p + 1) pairs of one dim, 32 bits per write: the lanes staging slots p
+    // (even) and p + 1 hold the same 8 dims D/8 lanes apart and swap half of
+    // them, the even lane then writing dims off .. off+3 and the odd lane dims
+    // off+4 .. off+7 of both slots
     auto st = [&](int jj, const uint4& kk, const uint4& vv) {
       const int c16 = tid + kBlock * jj;
       const int p = (c16 * 8) / D, off = (c16 * 8) % D;
       const bool dead = p >= cnt;
-      if (dead || p0 + p != pos) {
-        const uint4 k4 = dead ? make_uint4(0u, 0u, 0u, 0u) : kk;
-        const uint4 v4 = dead ? make_uint4(0u, 0u, 0u, 0u) : vv;
-        *reinterpret_cast<uint4*>(ks + p * ROWH + off) = k4;
-        const uint32_t w[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          vt[vti(off + 2 * i, p)] = (uint16_t)(w[i] & 0xFFFFu);
-          vt[vti(off + 2 * i + 1, p)] = (uint16_t)(w[i] >> 16);
-        }
-      }
+      const uint4 k4 = dead ? make_uint4(0u, 0u, 0u, 0u) : kk;
+      const uint4 v4 = dead ? make_uint4(0u, 0u, 0u, 0u) : vv;
+      *reinterpret_cast<uint4*>(ks + p * ROWH + off) = k4;
+      const bool even = (p & 1) == 0;
+      auto swap = [](uint32_t x) {
+        if constexpr (D == 128) return xor16_u32(x);
+        else return dpp_u32<kDppRor8>(x);
+      };
+      const uint32_t r0 = swap(even ? v4.z : v4.x), r1 = swap(even ? v4.w : v4.y);
+      const uint32_t o0 = even ? v4.x : v4.z, o1 = even ? v4.y : v4.w;
+      const uint32_t lo0 = even ? o0 : r0, hi0 = even ? r0 : o0;  // slot p&~1, slot p|1
+      const uint32_t lo1 = even ? o1 : r1, hi1 = even ? r1 : o1;
+      const int d0 = off + (even ? 0 : 4), pe = p & ~1;
+      *reinterpret_cast<uint32_t*>(vt + vti(d0, pe)) = (lo0 & 0xFFFFu) | (hi0 << 16);
+      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 1, pe)) = (lo0 >> 16) | (hi0 & 0xFFFF0000u);
+      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 2, pe)) = (lo1 & 0xFFFFu) | (hi1 << 16);
+      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 3, pe)) = (lo1 >> 16) | (hi1 & 0xFFFF0000u);
     };
     st(0, k0, v0);
     st(1, k1, v1);
     if constexpr (PER > 2) {
       st(2, k2, v2);
       st(3, k3, v3);
+    }
+    if (here) {
+      // the staged copy of slot pos (the cache's value before this step) is
+      // replaced once every lane's pair write has landed
+      __syncthreads();
+      if (tid < T) {
+        const int lp = pos - p0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          ks[lp * ROWH + 4 * tid + k] = kh[k];
+          vt[vti(4 * tid + k, lp)] = vh[k];
+        }
+      }
     }
     // the next chunk's slots load while this one is computed
     if (j + 1 < nch) ld_chunk(p0 + kChunk);
@@ -240,7 +265,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
       }
       if (hv) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) es[r * EROW + 16 * wave + 4 * kq + i] = sa[i] * a.scale;
+        for (int i = 0; i < 4; ++i) es[r * EROW + 16 * wave + 4 * kq + i] = sa[i] * scale2;
       }
     }
     __syncthreads();
@@ -249,9 +274,9 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
       const float s0 = lane < cnt ? es[h0 * EROW + lane] : -INFINITY;
       const float s1 = (lane < cnt && h1 < G) ? es[h1 * EROW + lane] : -INFINITY;
       const float n0 = fmaxf(m0, group_max<64>(s0)), n1 = fmaxf(m1, group_max<64>(s1));
-      const float a0 = expf(m0 - n0), a1 = h1 < G ? expf(m1 - n1) : 0.0f;  // exp(-inf) = 0 first
-      const float e0 = lane < cnt ? expf(s0 - n0) : 0.0f;
-      const float e1 = (lane < cnt && h1 < G) ? expf(s1 - n1) : 0.0f;
+      const float a0 = exp2f(m0 - n0), a1 = h1 < G ? exp2f(m1 - n1) : 0.0f;  // 2^-inf = 0 first
+      const float e0 = lane < cnt ? exp2f(s0 - n0) : 0.0f;
+      const float e1 = (lane < cnt && h1 < G) ? exp2f(s1 - n1) : 0.0f;
       l0 = l0 * a0 + group_sum<64>(e0);
       l1 = l1 * a1 + group_sum<64>(e1);
       m0 = n0;
@@ -361,7 +386,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
   float ls = 0.0f, acc = 0.0f;
 #pragma unroll
   for (int i = 0; i < PMAX; ++i) {
-    const float f = m[i] == -INFINITY ? 0.0f : expf(m[i] - M);
+    const float f = m[i] == -INFINITY ? 0.0f : exp2f(m[i] - M);
     ls += l[i] * f;
     acc += v[i] * f;
   }
@@ -422,7 +447,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge_head(AttnArgs a, int n_sp
   for (int j = 0; j < 4; ++j) {
     const int s2 = tid + kBlock * j;
     if (s2 < n_split) {
-      const float f = m_own[j] == -INFINITY ? 0.0f : expf(m_own[j] - M);
+      const float f = m_own[j] == -INFINITY ? 0.0f : exp2f(m_own[j] - M);
       fs[s2] = f;
       lsum += l_own[j] * f;
     }
