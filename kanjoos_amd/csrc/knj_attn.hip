@@ -806,7 +806,10 @@ hipError_t launch_prefill_attention(const PrefillAttnArgs& a, hipStream_t s) {
   const int base = a.n_head_kv * n_tiles;
   int n_split = 1;
   if (nch >= 16 && base < kPrefillWGs) n_split = std::min(nch / 8, kPrefillWGs / base);
-  if (n_split > 1 && !a.partial) return hipErrorInvalidValue;
+  if (n_split > 1 &&
+      (!a.partial ||
+       (uint64_t)base * n_split * 64 * (a.head_dim + 2) * sizeof(float) > a.partial_bytes))
+    return hipErrorInvalidValue;
   const int cps = (nch + n_split - 1) / n_split;
   n_split = (nch + cps - 1) / cps;
   const dim3 grid(a.n_head_kv, n_tiles, n_split);

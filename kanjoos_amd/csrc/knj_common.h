@@ -201,8 +201,10 @@ struct PrefillAttnArgs {
   int n_head, n_head_kv, head_dim, n_ctx;
   float scale;
   float* out;
-  // scratch for split-KV partials: prefill_partial_bytes(...) bytes
+  // scratch for split-KV partials, partial_bytes long
+  // (prefill_partial_bytes(n_head, n_head_kv, head_dim, n_rows) suffices)
   float* partial = nullptr;
+  uint64_t partial_bytes = 0;
 };
 // False when the shape is not one the prefill kernels take (64 % group, D).
 bool prefill_attention_ok(int n_head, int n_head_kv, int head_dim);

@@ -110,7 +110,8 @@ int prefill_chunk(knj_model* m, const int32_t* tokens, int n, bool last) {
                        reinterpret_cast<const float*>(img + lo.q_norm),
                        reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos,
                        m->rope_sin, m->pos, n, m->kv_k + kv_layer, m->kv_v + kv_layer, c.n_head,
-                       c.n_head_kv, D, c.n_ctx, 1.0f / std::sqrt((float)D), b.ctx, b.attn_part};
+                       c.n_head_kv, D, c.n_ctx, 1.0f / std::sqrt((float)D), b.ctx, b.attn_part,
+                       prefill_partial_bytes(c.n_head, c.n_head_kv, D, b.cap)};
     KNJ_HIP(launch_prefill_attention(pa, s));
     KNJ_HIP(launch_dense_q4k(img + lo.wo, QD, H, n, b.ctx, b.x, b.x, b.scratch, s));
     MoeBatchArgs ma{b.x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
