@@ -626,3 +626,40 @@ def test_moe_routing_ties(device, config1_weights, case):
             "two_groups": [9, 17, 33, 70, 101, 2, 11, 50]}[case]
     assert got[:len(want)] == want
     assert np.allclose(tw.download(np.float32), tw_w[0], rtol=1e-6, atol=0)
+
+
+def test_runs_are_bit_identical(device, config1_weights):
+    """Fixed reduction order everywhere (no float atomics): the same inputs give
+    the same bits on every run -- a prompt pass with split-KV attention, decode
+    steps, and the batched MoE layer, each run twice."""
+    cfg = small_config(n_ctx=1100)
+    a = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    b = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    try:
+        prompt = [int(t) for t in np.random.default_rng(5).integers(0, cfg["n_vocab"], 1030)]
+        la, lb = a.forward(prompt), b.forward(prompt)
+        assert np.array_equal(la.view(np.uint32), lb.view(np.uint32))
+        for il in range(cfg["n_layer"]):
+            assert np.array_equal(a.hidden(il).view(np.uint32), b.hidden(il).view(np.uint32))
+        ta, tb = a.decode_greedy(int(np.argmax(la)), 8), b.decode_greedy(int(np.argmax(lb)), 8)
+        assert list(ta) == list(tb)
+        ka, kb = a.kv_download(), b.kv_download()
+        assert np.array_equal(ka[0], kb[0]) and np.array_equal(ka[1], kb[1])
+    finally:
+        a.close()
+        b.close()
+    n_embd, n_ff, n_expert, k, m = 2048, 768, 128, 8, 96
+    _, router, gate, up, down = config1_weights
+    x = np.random.default_rng(6).standard_normal((m, n_embd)).astype(np.float32)
+    d = {nm: K.DeviceBuffer.from_array(v) for nm, v in
+         dict(x=x, router=router, gate=gate, up=up, down=down).items()}
+    outs = []
+    for _ in range(2):
+        out = K.DeviceBuffer(4 * m * n_embd)
+        logits = K.DeviceBuffer(4 * m * n_expert)
+        ti = K.DeviceBuffer(4 * m * k)
+        tw = K.DeviceBuffer(4 * m * k)
+        K.moe_batch_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], m, n_embd, n_ff,
+                          n_expert, k, out, logits, ti, tw)
+        outs.append(out.download(np.float32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
