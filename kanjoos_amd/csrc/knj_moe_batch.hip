@@ -231,27 +231,42 @@ __global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ t
                                                    int* __restrict__ pair_of,
                                                    int2* __restrict__ items,
                                                    int* __restrict__ n_items) {
-  __shared__ int cnt[256], off[257], cur[256], ioff[257];
-  const int t = threadIdx.x, P = m * k;
+  __shared__ int cnt[256], cur[256];
+  __shared__ int wsum[2][kBlock / 64];
+  const int t = threadIdx.x, P = m * k, lane = t & 63, wave = t >> 6;
   if (t < n_expert) cnt[t] = 0;
   __syncthreads();
   for (int p = t; p < P; p += kBlock) atomicAdd(&cnt[topk_idx[p]], 1);
   __syncthreads();
-  if (t == 0) {
-    off[0] = 0;
-    ioff[0] = 0;
-    for (int e = 0; e < n_expert; ++e) {
-      off[e + 1] = off[e] + cnt[e];
-      ioff[e + 1] = ioff[e] + (cnt[e] + kTok - 1) / kTok;
+  // exclusive prefix sums over the experts (thread t = expert t) of the pair
+  // counts and the tile counts: a scan within each wave, then the wave totals
+  const int c = t < n_expert ? cnt[t] : 0, ct = (c + kTok - 1) / kTok;
+  int sc = c, st = ct;
+  for (int d = 1; d < 64; d <<= 1) {
+    const int yc = __shfl_up(sc, d, 64), yt = __shfl_up(st, d, 64);
+    if (lane >= d) {
+      sc += yc;
+      st += yt;
     }
-    offsets[n_expert] = off[n_expert];
-    *n_items = ioff[n_expert];
+  }
+  if (lane == 63) {
+    wsum[0][wave] = sc;
+    wsum[1][wave] = st;
   }
   __syncthreads();
+  int oc = sc - c, ot = st - ct;
+  for (int w = 0; w < wave; ++w) {
+    oc += wsum[0][w];
+    ot += wsum[1][w];
+  }
   if (t < n_expert) {
-    offsets[t] = off[t];
-    cur[t] = off[t];
-    for (int i = 0; i < ioff[t + 1] - ioff[t]; ++i) items[ioff[t] + i] = make_int2(t, i * kTok);
+    offsets[t] = oc;
+    cur[t] = oc;
+    for (int i = 0; i < ct; ++i) items[ot + i] = make_int2(t, i * kTok);
+    if (t == n_expert - 1) {
+      offsets[n_expert] = oc + c;
+      *n_items = ot + ct;
+    }
   }
   __syncthreads();
   for (int p = t; p < P; p += kBlock) {
