@@ -307,6 +307,24 @@ def test_prefill_split_kv(device, shape):
     say(f"worst per-layer rel-RMSE: {w1:.3g}, split {w2:.3g}")
 
 
+def test_prefill_edges(device):
+    """A 513-token prompt (a 512-row chunk, then a chunk of one row) against the
+    oracle; a prompt that fills the context exactly, after which one more
+    token is refused as the reference refuses it (model.cpp:514-517)."""
+    cfg = small_config(n_ctx=520)
+    say(f"prefill edges {cfg}")
+    om = O.OracleModel(O.make_config(**cfg), seed=SEED)
+    gm = K.Model.from_image(K.qwen3_30b_a3b(**cfg), om.image())
+    prompt = [int(t) for t in np.random.default_rng(13).integers(0, cfg["n_vocab"], 513)]
+    worst = prefill_parity(om, gm, prompt, cfg["n_layer"])
+    say(f"worst per-layer rel-RMSE {worst:.3g}")
+    gm.reset()
+    gm.forward([1] * cfg["n_ctx"])
+    assert gm.pos == cfg["n_ctx"]
+    with pytest.raises(K.KnjError, match="context exhausted"):
+        gm.forward([2])
+
+
 def test_prefill_errors(device):
     cfg = small_config()
     gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
