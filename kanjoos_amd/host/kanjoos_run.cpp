@@ -10,6 +10,11 @@
 //               [--profiling[=table|json|csv|no-subtract|off]] [--profile-dir DIR]
 //               [--profile-floor N] [--profile-warmup N] [--profile-detail=class|layer|kernel]
 //
+// --bench PP runs the PP tokens as one forward call (the prompt pass, as the
+// reference's normal mode runs a prompt, main.cpp:521-528); the reference's
+// --bench feeds them one call each (main.cpp:255-257), which KNJ_PROMPT_STEPS=1
+// reproduces here.
+//
 // --profiling (main.cpp:47-56, 94-98, 198-223, 314-318) times the decode with
 // a dispatch event pair around every kernel launch (Model::decode_greedy_profiled)
 // and prints the profiler's report before the token line; the tokens are the
