@@ -16,6 +16,8 @@
 // keeps ~22 significant bits.  The min term is one more matrix-core step over
 // the per-sub-block sums of x (also split hi/lo) against the 6-bit mins.  d and
 // dmin scale the two accumulators once per 256-weight super-block.
+#include <cstdlib>
+
 #include "knj_common.h"
 #include "knj_dev.h"
 
@@ -901,11 +903,14 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
 
 // ---- dense batched GEMMs of the batched decode step
 // Ranges of the reduction a dense Q4_K product is split into: enough
-// workgroups for the chip (at most 16 ranges, at most one per super-block).
+// workgroups for the chip, about 512 (at most 16 ranges, at most one per
+// super-block).
 int dense_ksplit(int m, int n_in, int n_out) {
   if (m <= 0 || n_out <= 0) return 1;
   const int tiles = (m + kTok - 1) / kTok, rows = (n_out + kRowsWG - 1) / kRowsWG;
-  const int want = (256 + tiles * rows - 1) / (tiles * rows);
+  // about two workgroups per CU (measured: 512 beats 256 and 1024)
+  constexpr int target = 512;
+  const int want = (target + tiles * rows - 1) / (tiles * rows);
   return std::max(1, std::min({want, n_in >> 8, 16}));
 }
 
