@@ -16,8 +16,6 @@
 // keeps ~22 significant bits.  The min term is one more matrix-core step over
 // the per-sub-block sums of x (also split hi/lo) against the 6-bit mins.  d and
 // dmin scale the two accumulators once per 256-weight super-block.
-#include <cstdlib>
-
 #include "knj_common.h"
 #include "knj_dev.h"
 
