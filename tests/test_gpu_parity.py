@@ -325,6 +325,31 @@ def test_prefill_edges(device):
         gm.forward([2])
 
 
+def test_prompt_steps_switch(device):
+    """KNJ_PROMPT_STEPS=1 feeds a prompt one decode step per token; the prompt
+    pass and the steps agree as the reference's batched and single-token
+    forwards do (~1e-4: their products round differently)."""
+    cfg = small_config()
+    prompt = [int(t) for t in np.random.default_rng(21).integers(0, cfg["n_vocab"], 40)]
+    a = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    b = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    try:
+        la = a.forward(prompt)
+        os.environ["KNJ_PROMPT_STEPS"] = "1"
+        try:
+            lb = b.forward(prompt)
+        finally:
+            del os.environ["KNJ_PROMPT_STEPS"]
+        assert a.pos == b.pos == len(prompt)
+        assert not np.array_equal(la, lb)  # the two paths did run
+        assert rel_rmse(la, lb) < 3e-4
+        for il in range(cfg["n_layer"]):
+            assert rel_rmse(a.hidden(il), b.hidden(il)) < 3e-4
+    finally:
+        a.close()
+        b.close()
+
+
 def test_prefill_errors(device):
     cfg = small_config()
     gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
