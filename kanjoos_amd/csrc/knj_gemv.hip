@@ -435,6 +435,15 @@ int pow2_at_least(int v) {
   return p;
 }
 
+// The bf16 fast path is instantiated for 512, 1024, 2048 and 4096 inputs only;
+// gemv_grid and launch_gemv both decide through this one predicate, so the
+// number of argmax keys the step reads always matches the launch.
+bool bf16_fast(int n_in) {
+  if (n_in % 512 != 0) return false;
+  const int nj = n_in / 512;
+  return nj == 1 || nj == 2 || nj == 4 || nj == 8;
+}
+
 }  // namespace
 
 // Grids of the argmax-capable GEMVs (Q6_K, BF16, F32); one key per workgroup.
@@ -448,7 +457,7 @@ int gemv_grid(int type, int n_in, int n_out) {
     const int rows_per_block = 4 * (64 / lpr);
     return std::max(1, std::min(kMaxKeys, (n_out + rows_per_block - 1) / rows_per_block));
   }
-  if (type == KNJ_TYPE_BF16 && n_in % 512 == 0 && n_in <= 4096 && n_in / 512 != 3) {
+  if (type == KNJ_TYPE_BF16 && bf16_fast(n_in)) {
     constexpr int RS = 4;
     const int waves_needed = (n_out + RS - 1) / RS;
     return std::max(1, std::min(512, (waves_needed + 3) / 4));
@@ -501,7 +510,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
 #undef G6
     return hipErrorInvalidValue;
   }
-  if (a.type == KNJ_TYPE_BF16 && a.n_in % 512 == 0 && a.n_in <= 4096 && a.n_in / 512 != 3) {
+  if (a.type == KNJ_TYPE_BF16 && bf16_fast(a.n_in)) {
     const int nj = a.n_in / 512;
     constexpr int RS = 4;
     const int grid = gemv_grid(a.type, a.n_in, a.n_out);

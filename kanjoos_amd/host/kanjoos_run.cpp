@@ -101,7 +101,7 @@ int main(int argc, char** argv) {
       return 3;
     }
   }
-  auto backend = knj::Backend::create(0);
+  auto backend = knj::Backend::create();
   if (!backend) {
     std::fprintf(stderr, "device refused: %s\n", knj::Backend::knj_last_refusal());
     return 6;

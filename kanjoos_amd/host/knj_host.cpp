@@ -162,61 +162,130 @@ std::vector<int32_t> Model::decode_greedy(int32_t first, int steps) {
 // ------------------------------------------------------------------ Backend
 namespace {
 thread_local char g_refusal[256] = "";
+
+bool plan_is_empty(const ExpertPlan& p) { return p.out == nullptr; }
+
+// The one concrete backend: gfx950 through the C ABI.
+class Gfx950Backend final : public Backend {
+ public:
+  using Backend::Backend;
+
+  bool launch_expert_gemm_wmma(const ExpertPlan& p) override {
+    if (!would_instantiate(KnjCap::WmmaF16)) return false;
+    if (plan_is_empty(p)) return true;
+    return knj_moe_batch_layer(p.x, p.norm_w, p.eps, p.router_w, p.gate, p.up, p.down,
+                               p.type_gate_up, p.type_down, p.n_tokens, p.n_embd, p.n_ff,
+                               p.n_expert, p.k, p.resid, p.out, p.logits, p.topk_idx, p.topk_w,
+                               p.stream) == KNJ_OK;
+  }
+
+  bool launch_expert_gemm_simt(const ExpertPlan& p) override {
+    if (!would_instantiate(KnjCap::Wave64)) return false;
+    if (plan_is_empty(p)) return true;
+    if (p.n_tokens != 1) return launch_expert_gemm_wmma(p);
+    return knj_moe_decode_layer(p.x, p.norm_w, p.eps, p.router_w, p.gate, p.up, p.down,
+                                p.type_gate_up, p.type_down, p.n_embd, p.n_ff, p.n_expert, p.k,
+                                p.resid, p.out, p.logits, p.topk_idx, p.topk_w,
+                                p.stream) == KNJ_OK;
+  }
+
+  bool launch_attention(const AttentionPlan& p) override {
+    if (!would_instantiate(KnjCap::Wave64)) return false;
+    if (p.out == nullptr) return true;
+    return knj_attention_step(p.q, p.k, p.v, p.q_norm, p.k_norm, p.eps, p.rope_base, p.pos,
+                              p.n_head, p.n_head_kv, p.head_dim, p.n_ctx, p.k_cache, p.v_cache,
+                              p.out, p.stream) == KNJ_OK;
+  }
+
+  void launch_kv_write(const KvWritePlan& p) override {
+    if (p.scratch_out == nullptr) return;
+    AttentionPlan a = p.attn;
+    a.out = p.scratch_out;
+    (void)launch_attention(a);
+  }
+};
+
+void copy_arch(char (&dst)[16], const char* src) {
+  size_t i = 0;
+  for (; i + 1 < sizeof(dst) && src[i] != '\0'; ++i) dst[i] = src[i];
+  dst[i] = '\0';
 }
+}  // namespace
 
 const char* Backend::knj_last_refusal() { return g_refusal; }
 
-std::unique_ptr<Backend> Backend::create(int device) {
+std::unique_ptr<Backend> Backend::create() {
+  const char* env = std::getenv("KNJ_DEVICE");
+  const int device = (env && *env) ? std::atoi(env) : 0;
   DeviceCaps c;
-  const int rc = knj_device_open(device);
-  if (rc != KNJ_OK) {
+  if (knj_device_open(device) != KNJ_OK || knj_device_caps_get(&c.device) != KNJ_OK) {
     std::snprintf(g_refusal, sizeof(g_refusal), "%s", knj_last_error());
     return nullptr;
   }
-  if (knj_device_caps_get(&c.caps) != KNJ_OK) {
-    std::snprintf(g_refusal, sizeof(g_refusal), "%s", knj_last_error());
-    return nullptr;
-  }
-  c.arch_ok = true;
+  copy_arch(c.gcn_arch, c.device.gcn_arch);
+  c.has_wmma = c.device.has_mfma_bf16 != 0;
+  c.has_fp8 = c.device.has_fp8 != 0;
+  c.has_dot_builtin = knj_cap_available(c.gcn_arch, KnjCap::Sdot4Builtin);
+  c.wave_size = c.device.wave_size;
+  c.vram_total = c.device.vram_total;
+  c.vram_usable = c.device.vram_free;
+  c.rebar_full_aperture = false;
+  c.sms = (uint32_t)c.device.cu_count;
+  c.clock_khz = (uint32_t)c.device.clock_khz;
+  c.max_streams = 4;  // hardware queues per process (GPU_MAX_HW_QUEUES default)
+  c.num_queue_groups = 1;
+  c.arch_ok = c.device.arch_ok != 0;
+  c.arch_reason = "";
   g_refusal[0] = '\0';
-  return std::unique_ptr<Backend>(new Backend(c));
+  return std::unique_ptr<Backend>(new Gfx950Backend(c));
 }
 
 std::unique_ptr<Backend> Backend::from_caps(const DeviceCaps& caps) {
   g_refusal[0] = '\0';
-  return std::unique_ptr<Backend>(new Backend(caps));
+  return std::unique_ptr<Backend>(new Gfx950Backend(caps));
 }
 
 bool Backend::would_instantiate(KnjCap cap) const noexcept {
-  if (!caps_.arch_ok) return false;
+  if (!caps_.arch_ok || !knj_cap_available(caps_.gcn_arch, cap)) return false;
+  // probed caps can be absent where the arch nominally has them
   switch (cap) {
-    case KnjCap::Wave64: return caps_.caps.wave_size == 64;
-    case KnjCap::MfmaBf16: return caps_.caps.has_mfma_bf16 != 0;
-    case KnjCap::MfmaI8: return caps_.caps.has_mfma_i8 != 0;
-    case KnjCap::Fp8: return caps_.caps.has_fp8 != 0;
-    case KnjCap::Dot4I32I8: return true;
+    case KnjCap::WmmaF16:
+    case KnjCap::MfmaBf16: return caps_.has_wmma;
+    case KnjCap::Fp8: return caps_.has_fp8;
+    case KnjCap::Wave64: return caps_.wave_size == 64;
+    default: return true;
+  }
+}
+
+}  // namespace knj
+
+bool knj_cap_available(const char* arch, KnjCap cap) {
+  if (arch == nullptr || std::strcmp(arch, knj_built_arch()) != 0) return false;
+  switch (cap) {
+    case KnjCap::Dot4I32I8:
+    case KnjCap::Dot8I32I4:
+    case KnjCap::PkFmaF16:
+    case KnjCap::WmmaF16:
+    case KnjCap::Fp8:
+    case KnjCap::Sdot4Builtin:
+    case KnjCap::Wave64:
+    case KnjCap::MfmaBf16:
+    case KnjCap::MfmaI8: return true;
   }
   return false;
 }
 
-bool Backend::launch_expert_gemv(const ExpertPlan& p) {
-  if (!would_instantiate(KnjCap::Wave64)) return false;
-  return knj_moe_decode_layer(p.x, p.norm_w, p.eps, p.router_w, p.gate, p.up, p.down,
-                              p.type_gate_up, p.type_down, p.n_embd, p.n_ff, p.n_expert, p.k,
-                              p.resid, p.out, p.logits, p.topk_idx, p.topk_w, p.stream) == KNJ_OK;
+const char* knj_cap_label(KnjCap cap) {
+  switch (cap) {
+    case KnjCap::Dot4I32I8: return "dot4_i32_i8";
+    case KnjCap::Dot8I32I4: return "dot8_i32_i4";
+    case KnjCap::PkFmaF16: return "pk_fma_f16";
+    case KnjCap::WmmaF16: return "mfma_f16";
+    case KnjCap::Fp8: return "fp8";
+    case KnjCap::Sdot4Builtin: return "sdot4";
+    case KnjCap::Wave64: return "wave64";
+    case KnjCap::MfmaBf16: return "mfma_bf16";
+    case KnjCap::MfmaI8: return "mfma_i8";
+  }
+  return "unknown";
 }
-
-bool Backend::launch_attention(const AttentionPlan& p) {
-  if (!would_instantiate(KnjCap::Wave64)) return false;
-  return knj_attention_step(p.q, p.k, p.v, p.q_norm, p.k_norm, p.eps, p.rope_base, p.pos,
-                            p.n_head, p.n_head_kv, p.head_dim, p.n_ctx, p.k_cache, p.v_cache,
-                            p.out, p.stream) == KNJ_OK;
-}
-
-void Backend::launch_kv_write(const KvWritePlan& p) {
-  AttentionPlan a = p.attn;
-  a.out = p.scratch_out;
-  (void)launch_attention(a);
-}
-
-}  // namespace knj

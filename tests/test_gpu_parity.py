@@ -226,6 +226,30 @@ def test_small_model_greedy_parity(device, cfgkw):
     assert list(got) == list(want)
 
 
+@pytest.mark.parametrize("n_embd", [2560, 3072])
+def test_bf16_head_odd_width_greedy(device, n_embd):
+    """A bf16 LM head whose input width has no instantiated fast kernel (2560 and
+    3072 = 5 and 6 x 512) runs the general bf16 GEMV; the step's argmax must
+    read every one of its per-workgroup keys: per-step parity and free-running
+    greedy tokens against the oracle."""
+    cfg = small_config(n_layer=2, n_embd=n_embd, n_vocab=6000)
+    say(f"bf16 head width {n_embd} {cfg}")
+    om = O.OracleModel(O.make_config(**cfg), seed=SEED)
+    gm = K.Model.from_image(K.qwen3_30b_a3b(**cfg), om.image())
+    step_parity(om, gm, [3, 9], cfg["n_layer"])
+    gm.reset()
+    om.reset()
+    prompt = [5, 6, 7]
+    lw = om.forward(prompt)
+    lg = gm.forward(prompt)
+    assert int(np.argmax(lg)) == int(np.argmax(lw))
+    want = om.greedy([int(np.argmax(lw))], 24)
+    got = gm.decode_greedy(int(np.argmax(lg)), 24)
+    assert list(got) == list(want)
+    gm.close()
+    om.close()
+
+
 def prefill_parity(om, gm, prompt, n_layer, tol=1e-5):
     """One forward call over a prompt on both sides (the GPU's prompt pass, the
     oracle's batched Model::forward).  As in step_parity the oracle adopts the
