@@ -73,8 +73,8 @@ class Profiler {
   static Profiler& get();
 
   void configure(const ProfileConfig& c);
-  const ProfileConfig& config() const { return cfg_; }
-  bool on() const { return cfg_.on; }
+  const ProfileConfig& config() const { return opts_; }
+  bool on() const { return opts_.on; }
 
   // Marker pair.  `name` is "class", "class:layer" or "class:layer:kernel";
   // detail "class" keeps the part before the first ':', "layer" the part
@@ -86,36 +86,29 @@ class Profiler {
   void set_domain(ClockDomain d) { domain_ = d; }
   ClockDomain domain() const { return domain_; }
 
-  void enable_device_backend() {
-    device_backend_ = true;
-    domain_ = ClockDomain::Device;
-  }
-  bool device_backend() const { return device_backend_; }
+  void enable_device_backend();
+  bool device_backend() const { return dev_.enabled; }
   // One device interval, as offsets (ns) from the stream's epoch event.
   void device_span(const char* name, uint64_t start_ns, uint64_t end_ns, int stream = 0);
-  void set_device_floor(uint64_t ns, int n) {
-    dev_floor_ns_ = ns;
-    dev_floor_n_ = n;
-    dev_floor_measured_ = true;
-  }
-  bool device_floor_measured() const { return dev_floor_measured_; }
-  void set_device_dropped(uint64_t spans) { dev_dropped_ = spans; }
-  uint64_t device_spans() const { return dev_recorded_; }
-  uint64_t device_dropped() const { return dev_dropped_; }
+  void set_device_floor(uint64_t ns, int n);
+  bool device_floor_measured() const { return dev_.floor_known; }
+  void set_device_dropped(uint64_t spans) { dev_.dropped = spans; }
+  uint64_t device_spans() const { return dev_.recorded; }
+  uint64_t device_dropped() const { return dev_.dropped; }
 
   void note_residency(const ResidencyStats& r) { res_ = r; }
   void note_transfer(const TransferStats& t) { xfer_ = t; }
 
   void measure_floor();
-  uint64_t floor_host_ns() const { return floor_host_ns_; }
-  uint64_t floor_dev_ns() const { return floor_dev_ns_; }
-  int floor_n() const { return floor_n_; }
+  uint64_t floor_host_ns() const { return host_floor_.ns; }
+  uint64_t floor_dev_ns() const { return host_floor_.ns; }  // host domain: one clock
+  int floor_n() const { return host_floor_.n; }
 
-  uint64_t steps_kept() const { return steps_kept_; }
-  uint64_t steps_discarded() const { return steps_discarded_; }
-  uint64_t nested_ops() const { return nested_ops_; }
-  uint64_t max_depth() const { return max_depth_; }
-  uint64_t op_count() const { return total_ops_; }
+  uint64_t steps_kept() const { return count_.kept; }
+  uint64_t steps_discarded() const { return count_.discarded; }
+  uint64_t nested_ops() const { return count_.nested; }
+  uint64_t max_depth() const { return count_.depth; }
+  uint64_t op_count() const { return count_.ops; }
 
   void print_header(std::FILE* f, const std::string& version, const std::string& device_line,
                     const std::string& budgets_line) const;
@@ -130,46 +123,68 @@ class Profiler {
  private:
   Profiler() = default;
 
-  struct Row {
-    std::string group;
-    uint64_t ops = 0, dev_ns = 0, idle_ns = 0, host_ns = 0;
-    uint64_t dev_spans = 0;  // device measurements in the row
+  // Everything measured is an interval on a lane: a host-marker lane (the
+  // stream named by the outermost open marker) or a device stream.  Closed
+  // intervals are logged and turned into per-component tallies by one sweep
+  // (settle()), the same for both sources: sorted by start, a containment
+  // stack gives each interval's children (self time) and each outermost
+  // interval's gap to the previous one on its lane (idle).
+  enum class Source : uint8_t { Host = 0, Device = 1 };
+  static constexpr int kLanes = 8;
+  struct Interval {
+    uint32_t comp;
+    uint8_t lane;
+    Source src;
+    bool counted;  // false: closed during warmup (still shapes nesting and idle)
+    uint64_t t0, t1, seq;
   };
-  struct Frame {
-    std::string group;
-    uint64_t t0, child_ns;
+  struct Tally {
+    uint64_t ops = 0, spans = 0;              // host intervals, device intervals
+    uint64_t host_self = 0, dev_self = 0, idle = 0;
   };
-  struct Span {
-    size_t row;
-    uint64_t start, end;
+  struct OpenMarker {
+    uint32_t comp;
+    uint64_t t0, seq;
+  };
+  struct LaneEdge {
+    bool any = false;
+    uint64_t last_end = 0;  // end of the last outermost interval swept
+  };
+  struct DeviceInfo {
+    bool enabled = false, floor_known = false;
+    uint64_t floor_ns = 0;
+    int floor_n = 0;
+    uint64_t recorded = 0, dropped = 0;
+  };
+  struct HostFloor {
+    int n = 0;
+    uint64_t ns = 0;
+  };
+  struct Counters {
+    uint64_t steps = 0, kept = 0, discarded = 0;
+    uint64_t nested = 0, depth = 0, ops = 0, seq = 0;
   };
 
-  size_t row_of(const std::string& group) const;  // creates the row
-  std::string group_for(const char* name) const;
-  void fold() const;
-  std::vector<const Row*> ordered() const;
-  double dev_floor_for(const Row& r) const;   // ns to subtract from dev
-  double host_floor_for(const Row& r) const;  // ns to subtract from host
+  uint32_t component(const char* name) const;  // interned at the configured detail
+  void settle() const;                         // sweeps the logged intervals
+  std::vector<uint32_t> by_dev_time() const;
+  double dev_floor_of(const Tally& t) const;
+  double host_floor_of(const Tally& t) const;
 
-  ProfileConfig cfg_;
+  ProfileConfig opts_;
   ClockDomain domain_ = ClockDomain::None;
-  mutable std::vector<Row> rows_;
-  mutable std::unordered_map<std::string, size_t> index_;
-  std::vector<Frame> stack_;
-  int stream_ = 0;
-  uint64_t gap_ = 0;
-  uint64_t last_end_[8] = {};
-  uint64_t steps_seen_ = 0, steps_kept_ = 0, steps_discarded_ = 0;
-  uint64_t nested_ops_ = 0, max_depth_ = 0, total_ops_ = 0;
-  uint64_t floor_host_ns_ = 0, floor_dev_ns_ = 0;
-  int floor_n_ = 0;
+  mutable std::vector<std::string> names_;
+  mutable std::unordered_map<std::string, uint32_t> ids_;
+  mutable std::vector<Tally> tally_;
+  mutable std::vector<Interval> log_;
+  mutable LaneEdge edge_[2][kLanes];
+  std::vector<OpenMarker> open_;
+  uint8_t open_lane_ = 0;
+  Counters count_;
+  DeviceInfo dev_;
+  HostFloor host_floor_;
   ResidencyStats res_;
   TransferStats xfer_;
-  bool device_backend_ = false, dev_floor_measured_ = false;
-  uint64_t dev_floor_ns_ = 0;
-  int dev_floor_n_ = 0;
-  uint64_t dev_recorded_ = 0, dev_dropped_ = 0;
-  mutable std::vector<Span> pending_[8];
 };
 
 // RAII marker.

@@ -1,38 +1,36 @@
 // kanjoos_amd/host/knj_profiler.cpp -- the profiler of include/knj/profiler.h.
 //
-// Host markers are a stack of open frames; device spans are queued per stream
-// and folded (sorted, nested by containment) when a report is written.  Output
-// formats follow the reference's writers (/root/reference/src/profiler/
-// profiler.cpp:396-517): the same CSV columns and JSON keys, so tools that read
-// the reference's profile files read these.
+// Design: an interval log and one sweep.
+//  * A host marker pair, once closed, and a device span are both an
+//    Interval {component, lane, source, t0, t1}.  Closing a marker does no
+//    arithmetic beyond logging; nesting is not tracked while the step runs.
+//  * settle() sorts the log by (source, lane, start, longer first, begin
+//    order) and walks each lane with a containment stack: an interval that
+//    starts before the innermost open one ends is its child, so the parent's
+//    self time loses the overlap; an interval with nothing open is outermost,
+//    and its distance from the previous outermost end on the lane is its idle.
+//    Host markers and device spans therefore follow one rule.
+//  * The lane edges (last outermost end per lane) outlive a sweep, so the log
+//    can be settled at every step boundary and stays small.
+//  * The host floor is timed on a private Profiler instance through the same
+//    begin/end path, so this instance's state is never touched.
+// The CSV columns and JSON keys are the reference's file format
+// (/root/reference/src/profiler/profiler.h:44-175 describes them), so readers
+// of its profile files read these.
 #include "../../include/knj/profiler.h"
 
 #include <algorithm>
+#include <cerrno>
 #include <chrono>
 #include <cstring>
-#include <filesystem>
-#include <system_error>
+#include <sys/stat.h>
 
 namespace knj {
 namespace {
 
-uint64_t now_ns() {
-  return (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(
-             std::chrono::steady_clock::now().time_since_epoch())
-      .count();
-}
-
-std::string escape_json(const std::string& s) {
-  std::string o;
-  for (char c : s) {
-    if (c == '"' || c == '\\') o += '\\';
-    if (c == '\n') {
-      o += "\\n";
-      continue;
-    }
-    o += c;
-  }
-  return o;
+uint64_t clock_ns() {
+  using namespace std::chrono;
+  return (uint64_t)duration_cast<nanoseconds>(steady_clock::now().time_since_epoch()).count();
 }
 
 // Peak resident set of this process in MiB (VmHWM), 0 when unreadable.
@@ -47,218 +45,319 @@ double peak_rss_mib() {
   return kib / 1024.0;
 }
 
-constexpr int kStreams = 8;
-int clamp_stream(int s) { return s < 0 || s >= kStreams ? 0 : s; }
+// The part of `name` kept at a detail level: the first `fields` ':'-separated
+// fields (all of them when fields <= 0 or the name has fewer).
+std::string leading_fields(const char* name, int fields) {
+  const char* s = name ? name : "";
+  if (fields <= 0) return s;
+  const char* p = s;
+  for (int seen = 0; *p; ++p)
+    if (*p == ':' && ++seen == fields) break;
+  return std::string(s, (size_t)(p - s));
+}
+
+// Minimal streaming JSON object writer: commas and quoting are its business.
+class Json {
+ public:
+  explicit Json(std::FILE* f) : f_(f) {}
+  void open(const char* key, char bracket) {
+    sep(key);
+    std::fputc(bracket, f_);
+    first_ = true;
+    ++depth_;
+  }
+  void close(char bracket) {
+    --depth_;
+    std::fputc('\n', f_);
+    indent();
+    std::fputc(bracket, f_);
+    first_ = false;
+  }
+  void str(const char* key, const std::string& v) {
+    sep(key);
+    quoted(v);
+  }
+  void u64(const char* key, uint64_t v) {
+    sep(key);
+    std::fprintf(f_, "%llu", (unsigned long long)v);
+  }
+  void i32(const char* key, int v) {
+    sep(key);
+    std::fprintf(f_, "%d", v);
+  }
+  void num(const char* key, double v, int prec) {
+    sep(key);
+    std::fprintf(f_, "%.*f", prec, v);
+  }
+  void flag(const char* key, bool v) {
+    sep(key);
+    std::fputs(v ? "true" : "false", f_);
+  }
+  // a one-line object inside an array or as a value
+  void inline_open(const char* key) {
+    sep(key);
+    std::fputc('{', f_);
+    inline_first_ = true;
+    inline_ = true;
+  }
+  void inline_close() {
+    std::fputc('}', f_);
+    inline_ = false;
+  }
+
+ private:
+  void indent() {
+    for (int i = 0; i < depth_; ++i) std::fputs("  ", f_);
+  }
+  void quoted(const std::string& v) {
+    std::fputc('"', f_);
+    for (char c : v) {
+      if (c == '"' || c == '\\') std::fputc('\\', f_);
+      if (c == '\n') {
+        std::fputs("\\n", f_);
+        continue;
+      }
+      std::fputc(c, f_);
+    }
+    std::fputc('"', f_);
+  }
+  void sep(const char* key) {
+    if (inline_) {
+      if (!inline_first_) std::fputs(", ", f_);
+      inline_first_ = false;
+    } else {
+      if (!first_) std::fputc(',', f_);
+      if (depth_ > 0) std::fputc('\n', f_);
+      indent();
+      first_ = false;
+    }
+    if (key) {
+      quoted(key);
+      std::fputs(": ", f_);
+    }
+  }
+  std::FILE* f_;
+  int depth_ = 0;
+  bool first_ = true, inline_ = false, inline_first_ = true;
+};
 
 }  // namespace
 
 const char* clock_domain_name(ClockDomain d) {
-  return d == ClockDomain::Host ? "host" : d == ClockDomain::Device ? "device" : "none";
+  switch (d) {
+    case ClockDomain::Host: return "host";
+    case ClockDomain::Device: return "device";
+    default: return "none";
+  }
 }
 
 Profiler& Profiler::get() {
-  static Profiler p;
-  return p;
+  static Profiler instance;
+  return instance;
 }
 
+// A new configuration starts a new session: no device backend until one is
+// attached again, host clock when on.
 void Profiler::configure(const ProfileConfig& c) {
-  cfg_ = c;
-  if (cfg_.on && domain_ == ClockDomain::None) domain_ = ClockDomain::Host;
+  opts_ = c;
+  dev_ = DeviceInfo{};
+  domain_ = opts_.on ? ClockDomain::Host : ClockDomain::None;
   reset();
 }
 
 void Profiler::reset() {
-  rows_.clear();
-  index_.clear();
-  stack_.clear();
-  gap_ = 0;
-  std::fill(std::begin(last_end_), std::end(last_end_), 0);
-  for (auto& v : pending_) v.clear();
-  dev_recorded_ = dev_dropped_ = 0;
-  steps_seen_ = steps_kept_ = steps_discarded_ = 0;
-  nested_ops_ = max_depth_ = total_ops_ = 0;
+  names_.clear();
+  ids_.clear();
+  tally_.clear();
+  log_.clear();
+  open_.clear();
+  for (auto& src : edge_)
+    for (auto& e : src) e = LaneEdge{};
+  count_ = Counters{};
+  dev_.recorded = dev_.dropped = 0;
 }
 
-size_t Profiler::row_of(const std::string& group) const {
-  auto it = index_.find(group);
-  if (it != index_.end()) return it->second;
-  rows_.push_back(Row{group});
-  index_.emplace(group, rows_.size() - 1);
-  return rows_.size() - 1;
+void Profiler::enable_device_backend() {
+  dev_.enabled = true;
+  domain_ = ClockDomain::Device;
 }
 
-std::string Profiler::group_for(const char* name) const {
-  std::string n = name ? name : "";
-  const int keep = cfg_.detail == "class" ? 1 : cfg_.detail == "layer" ? 2 : 0;
-  if (keep == 0) return n;
-  size_t p = 0;
-  for (int i = 0; i < keep; ++i) {
-    p = n.find(':', i ? p + 1 : 0);
-    if (p == std::string::npos) return n;
-  }
-  return n.substr(0, p);
+void Profiler::set_device_floor(uint64_t ns, int n) {
+  dev_.floor_ns = ns;
+  dev_.floor_n = n;
+  dev_.floor_known = true;
+}
+
+uint32_t Profiler::component(const char* name) const {
+  const int fields = opts_.detail == "class" ? 1 : opts_.detail == "layer" ? 2 : 0;
+  std::string key = leading_fields(name, fields);
+  auto it = ids_.find(key);
+  if (it != ids_.end()) return it->second;
+  const uint32_t id = (uint32_t)names_.size();
+  names_.push_back(key);
+  tally_.emplace_back();
+  ids_.emplace(std::move(key), id);
+  return id;
 }
 
 void Profiler::begin(const char* name, int stream) {
-  if (!cfg_.on) return;
-  const uint64_t t = now_ns();
-  if (stack_.empty()) {
-    stream_ = clamp_stream(stream);
-    const uint64_t prev = last_end_[stream_];
-    gap_ = prev && t > prev ? t - prev : 0;
+  if (!opts_.on) return;
+  if (open_.empty()) {
+    open_lane_ = (uint8_t)(stream >= 0 && stream < kLanes ? stream : 0);
   } else {
-    ++nested_ops_;
+    ++count_.nested;
   }
-  stack_.push_back(Frame{group_for(name), t, 0});
-  max_depth_ = std::max<uint64_t>(max_depth_, stack_.size());
+  const uint32_t comp = component(name);
+  open_.push_back(OpenMarker{comp, clock_ns(), count_.seq++});
+  count_.depth = std::max<uint64_t>(count_.depth, open_.size());
 }
 
 void Profiler::end() {
-  if (!cfg_.on || stack_.empty()) return;
-  const uint64_t t = now_ns();
-  const Frame f = stack_.back();
-  stack_.pop_back();
-  const uint64_t span = t - f.t0;
-  const uint64_t self = span > f.child_ns ? span - f.child_ns : 0;
-  const bool outer = stack_.empty();
-  if (outer)
-    last_end_[stream_] = t;
-  else
-    stack_.back().child_ns += span;
-  if (steps_seen_ < (uint64_t)cfg_.warmup_steps) return;
-  Row& r = rows_[row_of(f.group)];
-  ++r.ops;
-  r.host_ns += self;
-  if (!device_backend_) {  // with a device backend, dev belongs to device spans
-    r.dev_ns += self;
-    if (outer) r.idle_ns += gap_;
-  }
-  ++total_ops_;
+  if (!opts_.on || open_.empty()) return;
+  const uint64_t t1 = clock_ns();
+  const OpenMarker m = open_.back();
+  open_.pop_back();
+  const bool counted = count_.steps >= (uint64_t)opts_.warmup_steps;
+  log_.push_back(Interval{m.comp, open_lane_, Source::Host, counted, m.t0, std::max(t1, m.t0), m.seq});
+  if (counted) ++count_.ops;
 }
 
 void Profiler::step_done() {
-  if (!cfg_.on) return;
-  if (steps_seen_ < (uint64_t)cfg_.warmup_steps)
-    ++steps_discarded_;
+  if (!opts_.on) return;
+  if (count_.steps < (uint64_t)opts_.warmup_steps)
+    ++count_.discarded;
   else
-    ++steps_kept_;
-  ++steps_seen_;
+    ++count_.kept;
+  ++count_.steps;
+  if (open_.empty()) settle();
 }
 
 void Profiler::device_span(const char* name, uint64_t start_ns, uint64_t end_ns, int stream) {
-  if (!cfg_.on || !device_backend_) return;
-  const size_t row = row_of(group_for(name));
-  ++rows_[row].dev_spans;
-  pending_[clamp_stream(stream)].push_back(Span{row, start_ns, std::max(start_ns, end_ns)});
-  ++dev_recorded_;
+  if (!opts_.on || !dev_.enabled) return;
+  const uint8_t lane = (uint8_t)(stream >= 0 && stream < kLanes ? stream : 0);
+  log_.push_back(Interval{component(name), lane, Source::Device, true, start_ns,
+                          std::max(start_ns, end_ns), count_.seq++});
+  ++dev_.recorded;
 }
 
-// Folds queued device spans into the rows.  Per stream, spans are taken in
-// start order (the longer first on a tie, so a parent precedes a child that
-// starts with it); a span that starts before the innermost open span ends is
-// nested in it and its time leaves the parent's self time.  A gap before an
-// outermost span is that span's idle.
-void Profiler::fold() const {
-  struct Open {
-    size_t row;
-    uint64_t start, end, child;
+void Profiler::settle() const {
+  // Host intervals wait while a marker is open: their parent is not logged yet.
+  const bool host_ready = open_.empty();
+  auto ready = [&](const Interval& iv) { return iv.src == Source::Device || host_ready; };
+  auto split = std::stable_partition(log_.begin(), log_.end(), ready);
+  std::vector<Interval> todo(log_.begin(), split);
+  log_.erase(log_.begin(), split);
+  std::sort(todo.begin(), todo.end(), [](const Interval& a, const Interval& b) {
+    if (a.src != b.src) return a.src < b.src;
+    if (a.lane != b.lane) return a.lane < b.lane;
+    if (a.t0 != b.t0) return a.t0 < b.t0;
+    if (a.t1 != b.t1) return a.t1 > b.t1;
+    return a.seq < b.seq;
+  });
+  struct Frame {
+    const Interval* iv;
+    uint64_t covered;  // time taken by children
   };
-  for (auto& q : pending_) {
-    if (q.empty()) continue;
-    std::sort(q.begin(), q.end(), [](const Span& a, const Span& b) {
-      return a.start != b.start ? a.start < b.start : a.end > b.end;
-    });
-    std::vector<Open> open;
-    uint64_t prev_end = 0;
-    bool any = false;
-    auto close = [&]() {
-      const Open& o = open.back();
-      const uint64_t dur = o.end - o.start;
-      rows_[o.row].dev_ns += dur > o.child ? dur - o.child : 0;
-      open.pop_back();
-    };
-    for (const Span& s : q) {
-      while (!open.empty() && s.start >= open.back().end) close();
-      if (open.empty()) {
-        if (any && s.start > prev_end) rows_[s.row].idle_ns += s.start - prev_end;
-      } else {
-        open.back().child += std::min(s.end, open.back().end) - s.start;
-      }
-      open.push_back(Open{s.row, s.start, s.end, 0});
-      prev_end = any ? std::max(prev_end, s.end) : s.end;
-      any = true;
+  std::vector<Frame> stack;
+  auto retire = [&]() {
+    const Frame fr = stack.back();
+    stack.pop_back();
+    const Interval& iv = *fr.iv;
+    const uint64_t len = iv.t1 - iv.t0;
+    const uint64_t self = len > fr.covered ? len - fr.covered : 0;
+    if (!iv.counted) return;
+    Tally& t = tally_[iv.comp];
+    if (iv.src == Source::Device) {
+      t.dev_self += self;
+    } else {
+      t.host_self += self;
+      if (!dev_.enabled) t.dev_self += self;  // host domain: one interval, both columns
     }
-    while (!open.empty()) close();
-    q.clear();
+  };
+  for (size_t i = 0; i < todo.size(); ++i) {
+    const Interval& iv = todo[i];
+    if (i > 0 && (todo[i - 1].src != iv.src || todo[i - 1].lane != iv.lane))
+      while (!stack.empty()) retire();
+    while (!stack.empty() && iv.t0 >= stack.back().iv->t1) retire();
+    if (stack.empty()) {
+      LaneEdge& e = edge_[(int)iv.src][iv.lane];
+      const bool idle_applies = iv.src == Source::Device || !dev_.enabled;
+      if (iv.counted && idle_applies && e.any && iv.t0 > e.last_end)
+        tally_[iv.comp].idle += iv.t0 - e.last_end;
+      e.last_end = e.any ? std::max(e.last_end, iv.t1) : iv.t1;
+      e.any = true;
+    } else {
+      Frame& parent = stack.back();
+      parent.covered += std::min(iv.t1, parent.iv->t1) - iv.t0;
+    }
+    if (iv.counted) {
+      Tally& t = tally_[iv.comp];
+      if (iv.src == Source::Device)
+        ++t.spans;
+      else
+        ++t.ops;
+    }
+    stack.push_back(Frame{&iv, 0});
   }
+  while (!stack.empty()) retire();
 }
 
 void Profiler::measure_floor() {
-  floor_n_ = std::max(0, cfg_.floor_ops);
-  floor_host_ns_ = floor_dev_ns_ = 0;
-  if (floor_n_ == 0) return;
-  // the same begin/end path, on a row of its own that is removed afterwards
-  const ProfileConfig keep = cfg_;
-  const uint64_t keep_seen = steps_seen_, keep_ops = total_ops_, keep_nested = nested_ops_;
-  const uint64_t keep_end = last_end_[kStreams - 1];
-  const size_t keep_rows = rows_.size();
-  cfg_.on = true;
-  cfg_.detail = "kernel";
-  cfg_.warmup_steps = 0;
-  steps_seen_ = 0;
-  for (int i = 0; i < 32; ++i) {  // warm the row and the clock
-    begin("__floor", kStreams - 1);
-    end();
+  host_floor_ = HostFloor{};
+  const int n = std::max(0, opts_.floor_ops);
+  if (n == 0) return;
+  // A scratch instance runs the identical marker path; nothing of this one changes.
+  Profiler probe;
+  probe.opts_.on = true;
+  probe.opts_.detail = "kernel";
+  probe.opts_.warmup_steps = 0;
+  probe.log_.reserve((size_t)n + 64);
+  for (int i = 0; i < 64; ++i) {
+    probe.begin("floor");
+    probe.end();
   }
-  const uint64_t t0 = now_ns();
-  for (int i = 0; i < floor_n_; ++i) {
-    begin("__floor", kStreams - 1);
-    end();
+  const uint64_t t0 = clock_ns();
+  for (int i = 0; i < n; ++i) {
+    probe.begin("floor");
+    probe.end();
   }
-  const uint64_t t1 = now_ns();
-  if (rows_.size() > keep_rows) {
-    index_.erase("__floor");
-    rows_.resize(keep_rows);
-  }
-  cfg_ = keep;
-  steps_seen_ = keep_seen;
-  total_ops_ = keep_ops;
-  nested_ops_ = keep_nested;
-  last_end_[kStreams - 1] = keep_end;
-  floor_host_ns_ = (t1 - t0) / (uint64_t)floor_n_;
-  floor_dev_ns_ = floor_host_ns_;  // host domain: one clock, one floor
+  const uint64_t t1 = clock_ns();
+  host_floor_.n = n;
+  host_floor_.ns = (t1 - t0) / (uint64_t)n;
 }
 
-std::vector<const Profiler::Row*> Profiler::ordered() const {
-  fold();
-  std::vector<const Row*> v;
-  for (const Row& r : rows_) v.push_back(&r);
-  std::sort(v.begin(), v.end(), [](const Row* a, const Row* b) {
-    return a->dev_ns != b->dev_ns ? a->dev_ns > b->dev_ns : a->group < b->group;
+std::vector<uint32_t> Profiler::by_dev_time() const {
+  settle();
+  std::vector<uint32_t> ids;
+  for (uint32_t i = 0; i < (uint32_t)tally_.size(); ++i)
+    if (tally_[i].ops || tally_[i].spans) ids.push_back(i);
+  std::sort(ids.begin(), ids.end(), [&](uint32_t a, uint32_t b) {
+    if (tally_[a].dev_self != tally_[b].dev_self) return tally_[a].dev_self > tally_[b].dev_self;
+    return names_[a] < names_[b];
   });
-  return v;
+  return ids;
 }
 
-// Floors are subtracted per measurement and never beyond what a row holds.
-// Device rows use the device floor only once one was measured; a device-only
-// row's measurements are its spans.
-double Profiler::dev_floor_for(const Row& r) const {
-  if (!cfg_.subtract_floor) return 0.0;
-  uint64_t per = 0, n = 0;
-  if (device_backend_) {
-    if (!dev_floor_measured_) return 0.0;
-    per = dev_floor_ns_;
-    n = r.ops ? r.ops : r.dev_spans;
+// Floors come off per measurement and never below zero.  Device time takes the
+// device floor only once one was measured (a host floor is never subtracted
+// from device time); a component measured only by spans counts its spans.
+double Profiler::dev_floor_of(const Tally& t) const {
+  if (!opts_.subtract_floor) return 0.0;
+  double per, n;
+  if (dev_.enabled) {
+    if (!dev_.floor_known) return 0.0;
+    per = (double)dev_.floor_ns;
+    n = (double)(t.ops ? t.ops : t.spans);
   } else {
-    per = floor_dev_ns_;
-    n = r.ops;
+    per = (double)host_floor_.ns;
+    n = (double)t.ops;
   }
-  return std::min((double)per * (double)n, (double)r.dev_ns);
+  return std::min(per * n, (double)t.dev_self);
 }
 
-double Profiler::host_floor_for(const Row& r) const {
-  if (!cfg_.subtract_floor) return 0.0;
-  return std::min((double)floor_host_ns_ * (double)r.ops, (double)r.host_ns);
+double Profiler::host_floor_of(const Tally& t) const {
+  if (!opts_.subtract_floor) return 0.0;
+  return std::min((double)host_floor_.ns * (double)t.ops, (double)t.host_self);
 }
 
 void Profiler::print_header(std::FILE* f, const std::string& version, const std::string& device_line,
@@ -268,53 +367,54 @@ void Profiler::print_header(std::FILE* f, const std::string& version, const std:
   std::fprintf(f,
                "    clock %s; rows are self time (max depth %llu); steps kept %llu, discarded "
                "%llu (warmup %d); %llu host op(s); peak rss %.0f MiB\n",
-               clock_domain_name(domain_), (unsigned long long)max_depth_,
-               (unsigned long long)steps_kept_, (unsigned long long)steps_discarded_,
-               cfg_.warmup_steps, (unsigned long long)total_ops_, peak_rss_mib());
+               clock_domain_name(domain_), (unsigned long long)count_.depth,
+               (unsigned long long)count_.kept, (unsigned long long)count_.discarded,
+               opts_.warmup_steps, (unsigned long long)count_.ops, peak_rss_mib());
   std::fprintf(f, "    profiling measures the run; it does not change what the step computes\n");
 }
 
 void Profiler::report_table(std::FILE* f) const {
-  if (!cfg_.on) {
+  if (!opts_.on) {
     std::fprintf(f, "\nprofile: off\n");
     return;
   }
-  const auto v = ordered();
-  double tdev = 0, tidle = 0, thost = 0;
-  for (const Row* r : v) {
-    tdev += (double)r->dev_ns - dev_floor_for(*r);
-    tidle += (double)r->idle_ns;
-    thost += (double)r->host_ns - host_floor_for(*r);
+  const std::vector<uint32_t> ids = by_dev_time();
+  double sum_dev = 0, sum_idle = 0, sum_host = 0;
+  size_t width = 20;
+  for (uint32_t i : ids) {
+    sum_dev += (double)tally_[i].dev_self - dev_floor_of(tally_[i]);
+    sum_idle += (double)tally_[i].idle;
+    sum_host += (double)tally_[i].host_self - host_floor_of(tally_[i]);
+    width = std::max(width, names_[i].size());
   }
-  int w = 20;
-  for (const Row* r : v) w = std::max(w, (int)r->group.size());
+  const int w = (int)width;
   std::fprintf(f, "\n  %-*s %7s %8s %7s %12s %12s %12s\n", w, "component", "ops", "spans", "%dev",
                "dev us", "idle us", "host us");
-  for (const Row* r : v) {
-    const double dev = (double)r->dev_ns - dev_floor_for(*r);
-    std::fprintf(f, "  %-*s %7llu %8llu %6.1f%% %12.2f %12.2f %12.2f\n", w, r->group.c_str(),
-                 (unsigned long long)r->ops, (unsigned long long)r->dev_spans,
-                 tdev > 0 ? 100.0 * dev / tdev : 0.0, dev / 1e3, (double)r->idle_ns / 1e3,
-                 ((double)r->host_ns - host_floor_for(*r)) / 1e3);
+  for (uint32_t i : ids) {
+    const Tally& t = tally_[i];
+    const double dev = (double)t.dev_self - dev_floor_of(t);
+    std::fprintf(f, "  %-*s %7llu %8llu %6.1f%% %12.2f %12.2f %12.2f\n", w, names_[i].c_str(),
+                 (unsigned long long)t.ops, (unsigned long long)t.spans,
+                 sum_dev > 0 ? 100.0 * dev / sum_dev : 0.0, dev / 1e3, (double)t.idle / 1e3,
+                 ((double)t.host_self - host_floor_of(t)) / 1e3);
   }
-  std::fprintf(f, "  total: dev %.2f us, idle %.2f us, host %.2f us\n", tdev / 1e3, tidle / 1e3,
-               thost / 1e3);
-  if (floor_n_ > 0)
+  std::fprintf(f, "  total: dev %.2f us, idle %.2f us, host %.2f us\n", sum_dev / 1e3,
+               sum_idle / 1e3, sum_host / 1e3);
+  const char* sub = opts_.subtract_floor ? ", subtracted" : ", not subtracted (no-subtract)";
+  if (host_floor_.n > 0)
     std::fprintf(f, "  host floor: %.3f us per marker pair (%d timed)%s\n",
-                 (double)floor_host_ns_ / 1e3, floor_n_,
-                 cfg_.subtract_floor ? ", subtracted" : ", not subtracted (no-subtract)");
+                 (double)host_floor_.ns / 1e3, host_floor_.n, sub);
   else
     std::fprintf(f, "  host floor: not measured\n");
   std::fprintf(f, "  clock domain: %s%s\n", clock_domain_name(domain_),
                domain_ == ClockDomain::Host ? " (dev and host are the same host interval)" : "");
-  if (device_backend_) {
+  if (dev_.enabled) {
     std::fprintf(f, "  device spans: %llu recorded, %llu dropped%s\n",
-                 (unsigned long long)dev_recorded_, (unsigned long long)dev_dropped_,
-                 dev_dropped_ ? " -- the dev total is short by the dropped spans" : "");
-    if (dev_floor_measured_)
+                 (unsigned long long)dev_.recorded, (unsigned long long)dev_.dropped,
+                 dev_.dropped ? " -- the dev total is short by the dropped spans" : "");
+    if (dev_.floor_known)
       std::fprintf(f, "  device floor: %.3f us per span (%d empty kernels)%s\n",
-                   (double)dev_floor_ns_ / 1e3, dev_floor_n_,
-                   cfg_.subtract_floor ? ", subtracted" : ", not subtracted (no-subtract)");
+                   (double)dev_.floor_ns / 1e3, dev_.floor_n, sub);
     else
       std::fprintf(f, "  device floor: not measured -- dev rows are raw\n");
     std::fprintf(f, "  device resolution: event times are float ms; sub-0.1 us differences are "
@@ -341,102 +441,120 @@ void Profiler::report_table(std::FILE* f) const {
 }
 
 void Profiler::report_json(std::FILE* f) const {
-  const auto v = ordered();
-  std::fprintf(f, "{\n  \"clock_domain\": \"%s\",\n  \"detail\": \"%s\",\n",
-               clock_domain_name(domain_), escape_json(cfg_.detail).c_str());
-  std::fprintf(f, "  \"subtract_floor\": %s,\n  \"warmup_steps\": %d,\n",
-               cfg_.subtract_floor ? "true" : "false", cfg_.warmup_steps);
-  std::fprintf(f, "  \"steps_kept\": %llu,\n  \"steps_discarded\": %llu,\n",
-               (unsigned long long)steps_kept_, (unsigned long long)steps_discarded_);
-  std::fprintf(f, "  \"max_depth\": %llu,\n  \"nested_scopes_self_time\": %llu,\n  \"ops\": %llu,\n",
-               (unsigned long long)max_depth_, (unsigned long long)nested_ops_,
-               (unsigned long long)total_ops_);
-  std::fprintf(f, "  \"floor\": {\"n\": %d, \"host_ns\": %llu, \"dev_ns\": %llu},\n", floor_n_,
-               (unsigned long long)floor_host_ns_,
-               (unsigned long long)(device_backend_ ? dev_floor_ns_ : floor_dev_ns_));
-  std::fprintf(f, "  \"device_backend\": %s,\n  \"device_spans\": %llu,\n",
-               device_backend_ ? "true" : "false", (unsigned long long)dev_recorded_);
-  std::fprintf(f, "  \"device_spans_dropped\": %llu,\n  \"device_floor_measured\": %s,\n",
-               (unsigned long long)dev_dropped_, dev_floor_measured_ ? "true" : "false");
-  std::fprintf(f, "  \"components\": [\n");
-  for (size_t i = 0; i < v.size(); ++i) {
-    const Row& r = *v[i];
-    std::fprintf(f,
-                 "    {\"component\": \"%s\", \"ops\": %llu, \"dev_ns\": %llu, \"dev_ns_self\": "
-                 "%.1f, \"idle_ns\": %llu, \"host_ns\": %llu, \"host_ns_self\": %.1f}%s\n",
-                 escape_json(r.group).c_str(), (unsigned long long)r.ops,
-                 (unsigned long long)r.dev_ns, (double)r.dev_ns - dev_floor_for(r),
-                 (unsigned long long)r.idle_ns, (unsigned long long)r.host_ns,
-                 (double)r.host_ns - host_floor_for(r), i + 1 < v.size() ? "," : "");
+  const std::vector<uint32_t> ids = by_dev_time();
+  Json j(f);
+  j.open(nullptr, '{');
+  j.str("clock_domain", clock_domain_name(domain_));
+  j.str("detail", opts_.detail);
+  j.flag("subtract_floor", opts_.subtract_floor);
+  j.i32("warmup_steps", opts_.warmup_steps);
+  j.u64("steps_kept", count_.kept);
+  j.u64("steps_discarded", count_.discarded);
+  j.u64("max_depth", count_.depth);
+  j.u64("nested_scopes_self_time", count_.nested);
+  j.u64("ops", count_.ops);
+  j.inline_open("floor");
+  j.i32("n", host_floor_.n);
+  j.u64("host_ns", host_floor_.ns);
+  j.u64("dev_ns", dev_.enabled ? dev_.floor_ns : host_floor_.ns);
+  j.inline_close();
+  j.flag("device_backend", dev_.enabled);
+  j.u64("device_spans", dev_.recorded);
+  j.u64("device_spans_dropped", dev_.dropped);
+  j.flag("device_floor_measured", dev_.floor_known);
+  j.open("components", '[');
+  for (uint32_t i : ids) {
+    const Tally& t = tally_[i];
+    j.inline_open(nullptr);
+    j.str("component", names_[i]);
+    j.u64("ops", t.ops);
+    j.u64("dev_ns", t.dev_self);
+    j.num("dev_ns_self", (double)t.dev_self - dev_floor_of(t), 1);
+    j.u64("idle_ns", t.idle);
+    j.u64("host_ns", t.host_self);
+    j.num("host_ns_self", (double)t.host_self - host_floor_of(t), 1);
+    j.inline_close();
   }
-  std::fprintf(f, "  ],\n  \"residency_measured\": %s,\n", res_.measured ? "true" : "false");
-  if (res_.measured)
-    std::fprintf(f,
-                 "  \"residency\": {\"vram_pct\": %.4f, \"ram_pct\": %.4f, \"nvme_pct\": %.4f, "
-                 "\"slots_used\": %llu, \"slots_total\": %llu, \"evictions\": %llu, "
-                 "\"prefetch_hit\": %.4f, \"stall_ms\": %.4f},\n",
-                 res_.vram_pct, res_.ram_pct, res_.nvme_pct, (unsigned long long)res_.slots_used,
-                 (unsigned long long)res_.slots_total, (unsigned long long)res_.evictions,
-                 res_.prefetch_hit, res_.stall_ms);
-  std::fprintf(f, "  \"transfer_measured\": %s", xfer_.measured ? "true" : "false");
-  if (xfer_.measured)
-    std::fprintf(f,
-                 ",\n  \"transfer\": {\"h2d_bytes\": %llu, \"d2h_bytes\": %llu, "
-                 "\"nvme_read_bytes\": %llu, \"nvme_write_bytes\": %llu, \"peak_pinned_bytes\": "
-                 "%llu}",
-                 (unsigned long long)xfer_.h2d_bytes, (unsigned long long)xfer_.d2h_bytes,
-                 (unsigned long long)xfer_.nvme_read_bytes,
-                 (unsigned long long)xfer_.nvme_write_bytes,
-                 (unsigned long long)xfer_.peak_pinned_bytes);
-  std::fprintf(f, "\n}\n");
+  j.close(']');
+  j.flag("residency_measured", res_.measured);
+  if (res_.measured) {
+    j.inline_open("residency");
+    j.num("vram_pct", res_.vram_pct, 4);
+    j.num("ram_pct", res_.ram_pct, 4);
+    j.num("nvme_pct", res_.nvme_pct, 4);
+    j.u64("slots_used", res_.slots_used);
+    j.u64("slots_total", res_.slots_total);
+    j.u64("evictions", res_.evictions);
+    j.num("prefetch_hit", res_.prefetch_hit, 4);
+    j.num("stall_ms", res_.stall_ms, 4);
+    j.inline_close();
+  }
+  j.flag("transfer_measured", xfer_.measured);
+  if (xfer_.measured) {
+    j.inline_open("transfer");
+    j.u64("h2d_bytes", xfer_.h2d_bytes);
+    j.u64("d2h_bytes", xfer_.d2h_bytes);
+    j.u64("nvme_read_bytes", xfer_.nvme_read_bytes);
+    j.u64("nvme_write_bytes", xfer_.nvme_write_bytes);
+    j.u64("peak_pinned_bytes", xfer_.peak_pinned_bytes);
+    j.inline_close();
+  }
+  j.close('}');
+  std::fputc('\n', f);
 }
 
 void Profiler::report_csv(std::FILE* f) const {
-  const auto v = ordered();
-  std::fprintf(f, "component,ops,dev_ns,idle_ns,host_ns,clock_domain,detail,floor_dev_ns\n");
-  const uint64_t floor = device_backend_ ? dev_floor_ns_ : floor_dev_ns_;
-  for (const Row* r : v)
-    std::fprintf(f, "%s,%llu,%llu,%llu,%llu,%s,%s,%llu\n", r->group.c_str(),
-                 (unsigned long long)r->ops, (unsigned long long)r->dev_ns,
-                 (unsigned long long)r->idle_ns, (unsigned long long)r->host_ns,
-                 clock_domain_name(domain_), cfg_.detail.c_str(), (unsigned long long)floor);
+  const std::vector<uint32_t> ids = by_dev_time();
+  const uint64_t floor = dev_.enabled ? dev_.floor_ns : host_floor_.ns;
+  const char* clock = clock_domain_name(domain_);
+  std::fputs("component,ops,dev_ns,idle_ns,host_ns,clock_domain,detail,floor_dev_ns\n", f);
+  for (uint32_t i : ids) {
+    const Tally& t = tally_[i];
+    std::fprintf(f, "%s,%llu,%llu,%llu,%llu,%s,%s,%llu\n", names_[i].c_str(),
+                 (unsigned long long)t.ops, (unsigned long long)t.dev_self,
+                 (unsigned long long)t.idle, (unsigned long long)t.host_self, clock,
+                 opts_.detail.c_str(), (unsigned long long)floor);
+  }
 }
 
 int Profiler::write_dir() const {
-  if (cfg_.dir.empty()) return 0;
-  std::error_code ec;
-  std::filesystem::create_directories(cfg_.dir, ec);
-  if (ec && !std::filesystem::is_directory(cfg_.dir)) {
-    std::fprintf(stderr, "profile-dir: cannot create %s: %s\n", cfg_.dir.c_str(),
-                 ec.message().c_str());
-    return 0;
-  }
-  int n = 0;
-  const char* names[3] = {"profile.txt", "profile.json", "profile.csv"};
-  for (int i = 0; i < 3; ++i) {
-    const std::string path = cfg_.dir + "/" + names[i];
-    std::FILE* out = std::fopen(path.c_str(), "w");
-    if (!out) {
-      std::fprintf(stderr, "profile-dir: cannot write %s\n", path.c_str());
-      continue;
+  if (opts_.dir.empty()) return 0;
+  // make the directory and its parents (mkdir -p)
+  std::string path;
+  for (size_t i = 0; i <= opts_.dir.size(); ++i) {
+    if (i == opts_.dir.size() || (opts_.dir[i] == '/' && i > 0)) {
+      path = opts_.dir.substr(0, i);
+      if (::mkdir(path.c_str(), 0755) != 0 && errno != EEXIST) {
+        std::fprintf(stderr, "profile: no directory %s (%s)\n", path.c_str(), std::strerror(errno));
+        return 0;
+      }
     }
-    if (i == 0)
-      report_table(out);
-    else if (i == 1)
-      report_json(out);
-    else
-      report_csv(out);
-    std::fclose(out);
-    ++n;
   }
-  return n;
+  struct Out {
+    const char* file;
+    void (Profiler::*emit)(std::FILE*) const;
+  };
+  const Out outs[] = {{"profile.txt", &Profiler::report_table},
+                      {"profile.json", &Profiler::report_json},
+                      {"profile.csv", &Profiler::report_csv}};
+  int written = 0;
+  for (const Out& o : outs) {
+    const std::string file = opts_.dir + "/" + o.file;
+    if (std::FILE* out = std::fopen(file.c_str(), "w")) {
+      (this->*o.emit)(out);
+      written += std::fclose(out) == 0 ? 1 : 0;
+    } else {
+      std::fprintf(stderr, "profile: %s not written (%s)\n", file.c_str(), std::strerror(errno));
+    }
+  }
+  return written;
 }
 
 void Profiler::report(std::FILE* f) const {
-  if (!cfg_.on) return;
-  if (cfg_.format == "json")
+  if (!opts_.on) return;
+  if (opts_.format == "json")
     report_json(f);
-  else if (cfg_.format == "csv")
+  else if (opts_.format == "csv")
     report_csv(f);
   else
     report_table(f);

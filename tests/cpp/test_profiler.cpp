@@ -88,7 +88,7 @@ void arm(bool subtract, const char* detail = "class", int warmup = 0) {
 
 }  // namespace
 
-int main() {
+int main(int argc, char** argv) {
   knj::Profiler& p = knj::Profiler::get();
 
   // host domain: dev == host; a gap between outer ops is idle of the next op
@@ -203,6 +203,64 @@ int main() {
   p.measure_floor();
   EXPECT(p.floor_n() == 64 && p.floor_host_ns() > 0 && p.op_count() == 0);
   EXPECT(capture(&knj::Profiler::report_csv).find("__floor") == std::string::npos);
+
+  // an outer marker left open across step boundaries: its children are
+  // settled with it, not before (self time of the outer = span - children)
+  arm(false, "class", 0);
+  p.begin("outer");
+  for (int s = 0; s < 3; ++s) {
+    p.begin("inner");
+    const auto w0 = std::chrono::steady_clock::now();
+    while (std::chrono::steady_clock::now() - w0 < std::chrono::microseconds(300)) {
+    }
+    p.end();
+    p.step_done();
+  }
+  p.end();
+  p.step_done();
+  {
+    Csv o = csv("outer"), in = csv("inner");
+    EXPECT(o.found && in.found && o.ops == 1 && in.ops == 3);
+    EXPECT(in.host >= 900000ull && o.host < in.host);
+    EXPECT(in.idle == 0);  // nested: gaps inside an open marker are not idle
+  }
+
+  // idle across settled steps: the gap between the last op of one step and
+  // the first of the next is charged even though a step boundary settled the log
+  arm(false, "class", 0);
+  p.begin("x");
+  p.end();
+  p.step_done();
+  {
+    const auto w0 = std::chrono::steady_clock::now();
+    while (std::chrono::steady_clock::now() - w0 < std::chrono::milliseconds(1)) {
+    }
+  }
+  p.begin("y");
+  p.end();
+  p.step_done();
+  EXPECT(csv("y").idle >= 900000ull && csv("x").idle == 0);
+
+  // files: profile.{txt,json,csv} in the directory given on the command line
+  if (argc > 1) {
+    knj::ProfileConfig fc;
+    fc.on = true;
+    fc.floor_ops = 16;
+    fc.warmup_steps = 0;
+    fc.dir = argv[1];
+    p.configure(fc);
+    p.enable_device_backend();
+    p.set_device_floor(100, 8);
+    p.device_span("head:0:k", 0, 1000, 0);
+    p.device_span("qkv:1:k", 1500, 2000, 0);
+    p.begin("decode");
+    p.end();
+    knj::ResidencyStats rs;
+    rs.measured = true;
+    rs.vram_pct = 100.0;
+    p.note_residency(rs);
+    EXPECT(p.write_dir() == 3);
+  }
 
   // off: nothing is recorded
   knj::ProfileConfig off;
