@@ -174,40 +174,102 @@ def calib_probe() -> None:
     log("calibration probe: 2 x (bf16 GEMV 256 MiB read, Q4_K dequant 64 MiB write)")
 
 
-def cpu_baseline(model: K.Model, cfg: K.ModelConfig, budget_s: float, max_tokens: int) -> dict:
-    """The CPU oracle (restating the reference's CPU forward pass) on the host
-    cores, continuing from the GPU's weights and KV cache at the same position."""
+def host_cpus() -> dict:
+    """Logical CPUs, the CPUs this process may run on, physical cores and the
+    CPU model, from os and /proc/cpuinfo."""
+    info = {"logical": os.cpu_count() or 1, "affinity": len(os.sched_getaffinity(0)),
+            "physical": None, "model": None}
+    try:
+        cores, phys, core = set(), None, None
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and info["model"] is None:
+                    info["model"] = val
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    core = val
+                elif not key and phys is not None and core is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
+        info["physical"] = len(cores) or None
+    except OSError:
+        pass
+    return info
+
+
+def cpu_baseline(model: K.Model, cfg: K.ModelConfig, cells: list[tuple[int, int]],
+                 share: int) -> dict:
+    """The CPU oracle (restating the reference's CPU forward pass, with its
+    ThreadPool strategy) on the host cores, continuing from the GPU's weights and
+    KV cache at the same position.  One cell per thread count: a fresh oracle
+    model (the weight image shared, the cache copied), then `tokens` greedy
+    decode tokens timed one by one; the best cell is the headline."""
     import oracle as O  # test infrastructure: only the baseline leg uses it
 
-    threads = min(16, os.cpu_count() or 1)
-    log(f"cpu baseline: downloading {model.image_bytes() / 1e9:.1f} GB weight image")
+    cpus = host_cpus()
+    log(f"cpu baseline: host {cpus}; downloading {model.image_bytes() / 1e9:.1f} GB weight image")
     image = model.download_image()
     ocfg = O.make_config(**cfg.as_dict())
-    om = O.OracleModel(ocfg, seed=0, image=image, threads=threads)
     kg, vg = model.kv_download()
-    ko, vo = om.kv()
-    ko[...] = kg
-    vo[...] = vg
-    om.set_pos(model.pos)
-    tok = int(model.logits().argmax())
-    log(f"cpu baseline: warmup token at pos {om.pos} with {threads} threads")
-    t0 = time.perf_counter()
-    logits = om.forward([tok])
-    warm = time.perf_counter() - t0
-    n = max(1, min(max_tokens, int(budget_s / max(warm, 1e-3))))
-    log(f"cpu baseline: warmup {warm:.2f} s, timing {n} tokens")
-    times = []
-    for _ in range(n):
-        tok = int(np.argmax(logits))
-        t0 = time.perf_counter()
-        logits = om.forward([tok])
-        times.append(time.perf_counter() - t0)
-    best = min(times)
-    om.close()
-    return {"value": round(1.0 / best, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} greedy decode tokens (best of {n}, after 1 warmup) of the 48-layer "
-                      f"model at context {model.pos}, oracle/libknj_oracle.so, "
-                      f"{threads} threads; mean {np.mean(times):.3f} s/token"}
+    pos0 = model.pos
+    tok0 = int(model.logits().argmax())
+    sweep = []
+    for ci, (threads, tokens) in enumerate(cells):
+        om = O.OracleModel(ocfg, seed=0, image=image, threads=threads)
+        ko, vo = om.kv()
+        ko[...] = kg
+        vo[...] = vg
+        om.set_pos(pos0)
+        tok = tok0
+        if ci == 0:  # page the weight image in once
+            t0 = time.perf_counter()
+            logits = om.forward([tok])
+            log(f"cpu baseline: warmup token {time.perf_counter() - t0:.2f} s")
+            om.set_pos(pos0)
+        times = []
+        for _ in range(tokens):
+            t0 = time.perf_counter()
+            logits = om.forward([tok])
+            times.append(time.perf_counter() - t0)
+            tok = int(np.argmax(logits))
+        om.close()
+        cell = {"threads": threads, "tokens": tokens, "best_s": round(min(times), 4),
+                "mean_s": round(float(np.mean(times)), 4), "tokens_per_s": round(1.0 / min(times), 4)}
+        sweep.append(cell)
+        log(f"cpu baseline: {threads} threads: {cell}")
+    best = max(sweep, key=lambda c: c["tokens_per_s"])
+    base1 = next((c for c in sweep if c["threads"] == 1), None)
+    for c in sweep:
+        if base1:
+            c["speedup_vs_1"] = round(c["tokens_per_s"] / base1["tokens_per_s"], 2)
+    return {"value": best["tokens_per_s"], "unit": "tokens/s", "cores": best["threads"],
+            "kind": "port",
+            "sample": (f"greedy decode tokens of the 48-layer model at context {pos0} on "
+                       f"oracle/libknj_oracle.so, best token time per cell, cells "
+                       f"{[(c['threads'], c['tokens']) for c in sweep]} (threads, tokens); the "
+                       f"headline is the best cell ({best['threads']} threads)"),
+            "host": {"cpu_model": cpus["model"], "logical_cpus": cpus["logical"],
+                     "physical_cores": cpus["physical"], "affinity_cpus": cpus["affinity"],
+                     "cpu_share": share,
+                     "note": "thread counts stop at the GPU box's CPU share per GPU; "
+                             "above it the oracle would compete with other jobs' CPUs"},
+            "sweep": sweep}
+
+
+def sweep_cells(spec: str, share: int) -> list[tuple[int, int]]:
+    """'1:3,4:8,16:8' -> [(threads, tokens)], thread counts capped at `share`."""
+    cells = []
+    for part in spec.split(","):
+        t, _, n = part.partition(":")
+        th = min(int(t), share)
+        if th >= 1 and th not in [c[0] for c in cells]:
+            cells.append((th, max(1, int(n or 8))))
+    return cells
 
 
 def main() -> int:
@@ -232,8 +294,10 @@ def main() -> int:
     ap.add_argument("--long-ctx", type=int, default=32768,
                     help="context of the config-5 leg (0 skips it)")
     ap.add_argument("--long-steps", type=int, default=32)
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
-    ap.add_argument("--cpu-tokens", type=int, default=4)
+    ap.add_argument("--cpu-sweep", default="1:3,4:8,16:8",
+                    help="CPU baseline cells threads:tokens (thread counts capped at --cpu-share)")
+    ap.add_argument("--cpu-share", type=int, default=16,
+                    help="host threads the GPU box grants one GPU's job")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
 
@@ -347,7 +411,8 @@ def main() -> int:
         "batched_decode": batched,
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(model, cfg, args.cpu_budget, args.cpu_tokens)
+        share = min(args.cpu_share, len(os.sched_getaffinity(0)))
+        result["cpu_baseline"] = cpu_baseline(model, cfg, sweep_cells(args.cpu_sweep, share), share)
     model.close()
     if args.long_ctx:
         result["long_context"] = long_ctx_leg(args.seed, args.long_ctx, args.long_steps)

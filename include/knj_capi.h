@@ -182,6 +182,11 @@ int knj_batch_fill_kv(knj_batch* b, int n_pos, uint64_t seed);
 int knj_batch_hidden(const knj_batch* b, int il, int seq, float* out);
 int knj_batch_topk(const knj_batch* b, int il, int seq, int32_t* idx, float* w);
 int knj_batch_kv_download(const knj_batch* b, int seq, uint16_t* k, uint16_t* v);
+/* One sequence's whole cache ([n_layer][n_head_kv][n_ctx][head_dim] f16, the
+ * batch's n_ctx) from the host, e.g. a cache a knj_model prompt pass wrote; and
+ * the lockstep position of every sequence. */
+int knj_batch_kv_upload(knj_batch* b, int seq, const uint16_t* k, const uint16_t* v);
+int knj_batch_set_pos(knj_batch* b, int pos);
 
 /* Byte offsets of layer `il`'s tensors inside the weight image of a model of
  * configuration `c` (the layout of knj_model.h); returns the image size, 0 on a

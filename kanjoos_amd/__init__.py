@@ -40,7 +40,7 @@ EXPORTS = (
     "knj_model_transfer_bytes", "knj_device_floor",
     "knj_batch_create", "knj_batch_free", "knj_batch_pos", "knj_batch_forward",
     "knj_batch_decode_greedy", "knj_batch_fill_kv", "knj_batch_hidden", "knj_batch_topk",
-    "knj_batch_kv_download",
+    "knj_batch_kv_download", "knj_batch_kv_upload", "knj_batch_set_pos",
 )
 
 
@@ -162,6 +162,8 @@ _SIGS = {
     "knj_batch_hidden": (_i, [_P, _i, _i, _P]),
     "knj_batch_topk": (_i, [_P, _i, _i, _P, _P]),
     "knj_batch_kv_download": (_i, [_P, _i, _P, _P]),
+    "knj_batch_kv_upload": (_i, [_P, _i, _P, _P]),
+    "knj_batch_set_pos": (_i, [_P, _i]),
 }
 
 _lib = None
@@ -528,6 +530,15 @@ class Batch:
         w = np.empty(k, dtype=np.float32)
         check(lib().knj_batch_topk(self.h, il, seq, _ptr(i), _ptr(w)))
         return i, w
+
+    def kv_upload(self, seq: int, k: np.ndarray, v: np.ndarray) -> None:
+        shape = (self.cfg.n_layer, self.cfg.n_head_kv, self.n_ctx, self.cfg.head_dim)
+        k = np.ascontiguousarray(k, dtype=np.uint16).reshape(shape)
+        v = np.ascontiguousarray(v, dtype=np.uint16).reshape(shape)
+        check(lib().knj_batch_kv_upload(self.h, seq, _ptr(k), _ptr(v)))
+
+    def set_pos(self, pos: int) -> None:
+        check(lib().knj_batch_set_pos(self.h, pos))
 
     def kv_download(self, seq: int):
         shape = (self.cfg.n_layer, self.cfg.n_head_kv, self.n_ctx, self.cfg.head_dim)

@@ -338,4 +338,18 @@ int knj_batch_kv_download(const knj_batch* b, int seq, uint16_t* k, uint16_t* v)
   return KNJ_OK;
 }
 
+int knj_batch_kv_upload(knj_batch* b, int seq, const uint16_t* k, const uint16_t* v) {
+  KNJ_CHECK_ARG(b && k && v && seq >= 0 && seq < b->n_seq, "bad arguments");
+  const uint64_t n = kv_seq_elems(b);
+  KNJ_HIP(hipMemcpy(b->kv_k + (uint64_t)seq * n, k, n * 2, hipMemcpyHostToDevice));
+  KNJ_HIP(hipMemcpy(b->kv_v + (uint64_t)seq * n, v, n * 2, hipMemcpyHostToDevice));
+  return KNJ_OK;
+}
+
+int knj_batch_set_pos(knj_batch* b, int pos) {
+  KNJ_CHECK_ARG(b && pos >= 0 && pos <= b->n_ctx, "position outside the context");
+  b->pos = pos;
+  return KNJ_OK;
+}
+
 }  // extern "C"

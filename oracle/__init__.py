@@ -134,6 +134,8 @@ def lib():
         L.knjo_model_set_pos.restype = C.c_int
         L.knjo_model_set_pos.argtypes = [_P, C.c_int]
         L.knjo_model_set_kv_source.argtypes = [_P, _P, _P]
+        L.knjo_model_kv_rms.argtypes = [_P, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        L.knjo_model_kv_rms.restype = None
         L.knjo_model_kv_stats.argtypes = [_P, C.POINTER(C.c_int64), C.POINTER(C.c_int64),
                                           C.POINTER(C.c_int), C.POINTER(C.c_float)]
         L.knjo_last_error.restype = C.c_char_p
@@ -300,7 +302,11 @@ class OracleModel:
     def kv_stats(self):
         a, d, u, mid = C.c_int64(), C.c_int64(), C.c_int(), C.c_float()
         lib().knjo_model_kv_stats(self.h, C.byref(a), C.byref(d), C.byref(u), C.byref(mid))
-        return dict(adopted=a.value, differing=d.value, max_ulp=u.value, max_mid_dist=mid.value)
+        d2, v2 = C.c_double(), C.c_double()
+        lib().knjo_model_kv_rms(self.h, C.byref(d2), C.byref(v2))
+        rel = (d2.value / v2.value) ** 0.5 if v2.value > 0 else 0.0
+        return dict(adopted=a.value, differing=d.value, max_ulp=u.value, max_mid_dist=mid.value,
+                    rel_rms_dist=rel)
 
     def set_pos(self, pos: int):
         if lib().knjo_model_set_pos(self.h, pos) != 0:

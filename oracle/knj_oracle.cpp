@@ -494,6 +494,7 @@ struct knjo_model {
   int64_t kv_adopted = 0, kv_diff = 0;
   int kv_max_ulp = 0;
   float kv_max_mid = 0.0f;
+  double kv_sum_d2 = 0.0, kv_sum_v2 = 0.0;  // squared distances, squared values
   std::vector<float> hidden;     // [n_layer][H], last token
   std::vector<int32_t> topk_idx; // [n_layer][K]
   std::vector<float> topk_w;     // [n_layer][K]
@@ -516,6 +517,7 @@ static uint16_t adopt_kv(knjo_model* m, float v, const uint16_t* src, size_t idx
   if (!src) return own;
   const uint16_t got = src[idx];
   m->kv_adopted += 1;
+  m->kv_sum_v2 += (double)v * (double)v;
   if (got == own) return own;
   m->kv_diff += 1;
   const int ulp = std::abs((int)(own & 0x7FFF) - (int)(got & 0x7FFF)) +
@@ -533,6 +535,7 @@ static uint16_t adopt_kv(knjo_model* m, float v, const uint16_t* src, size_t idx
   const double lo = 0.5 * ((double)g + (double)below), hi = 0.5 * ((double)g + (double)above);
   const double dist = v < lo ? lo - v : (v > hi ? v - hi : 0.0);
   m->kv_max_mid = std::max(m->kv_max_mid, (float)dist);
+  m->kv_sum_d2 += dist * dist;
   return got;
 }
 
@@ -544,6 +547,12 @@ void knjo_model_set_kv_source(knjo_model* m, const uint16_t* k, const uint16_t* 
   m->kv_adopted = m->kv_diff = 0;
   m->kv_max_ulp = 0;
   m->kv_max_mid = 0.0f;
+  m->kv_sum_d2 = m->kv_sum_v2 = 0.0;
+}
+
+void knjo_model_kv_rms(knjo_model* m, double* sum_d2, double* sum_v2) {
+  *sum_d2 = m->kv_sum_d2;
+  *sum_v2 = m->kv_sum_v2;
 }
 
 void knjo_model_kv_stats(knjo_model* m, int64_t* adopted, int64_t* differing, int* max_ulp,

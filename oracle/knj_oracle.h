@@ -95,6 +95,10 @@ int knjo_model_set_pos(knjo_model* m, int pos);
 void knjo_model_set_kv_source(knjo_model* m, const uint16_t* k, const uint16_t* v);
 void knjo_model_kv_stats(knjo_model* m, int64_t* adopted, int64_t* differing, int* max_ulp,
                          float* max_mid_dist);
+/* Sums over the adopted elements since knjo_model_set_kv_source: squared
+ * distance to the rounding interval of the adopted value, squared own value;
+ * sqrt(d2 / v2) is the relative RMS distance of the adopted cache writes. */
+void knjo_model_kv_rms(knjo_model* m, double* sum_d2, double* sum_v2);
 const char* knjo_last_error(void);
 
 #ifdef __cplusplus

@@ -33,3 +33,17 @@ def rel_rmse(got, want):
     nz = want != 0
     den = float(np.sum(want[nz] ** 2))
     return float(np.sqrt(np.sum((got[nz] - want[nz]) ** 2) / den)) if den > 0 else 0.0
+
+
+def progress(msg):
+    """A progress line for long GPU tests: printed, and appended to
+    gpurun_out/test_progress.log so a long test visibly makes progress even
+    while pytest captures its output."""
+    print(msg, flush=True)
+    try:
+        d = os.path.join(ROOT, "gpurun_out")
+        os.makedirs(d, exist_ok=True)
+        with open(os.path.join(d, "test_progress.log"), "a") as f:
+            f.write(msg + "\n")
+    except OSError:
+        pass
