@@ -101,6 +101,21 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
                          int type_down, int n_embd, int n_ff, int n_expert, int k,
                          const float* resid, float* out, float* logits, int32_t* topk_idx,
                          float* topk_w, void* stream);
+/* knj_moe_decode_layer_noalloc: knj_moe_decode_layer computed by the same
+ *   kernels, with its scratch (hx, then act: n_embd + k * n_ff floats) in a
+ *   fixed device array of 32768 floats (128 KiB per device, held until the
+ *   process ends) instead of library-allocated memory: the call allocates and
+ *   frees nothing.  No counterpart in the reference; it is for callers that
+ *   cannot allocate (code under HIP graph capture, tight serving loops,
+ *   harnesses that forbid hipMalloc).  Larger shapes return KNJ_E_ARG.  Every
+ *   call on a device shares that device's array, so calls that overlap on one
+ *   device (other streams, other threads) race; nothing in the array needs to
+ *   start at zero.  The device must have been opened with knj_device_open. */
+int knj_moe_decode_layer_noalloc(const float* x, const float* norm_w, float eps,
+                                 const float* router_w, const void* gate, const void* up,
+                                 const void* down, int type_gate_up, int type_down, int n_embd,
+                                 int n_ff, int n_expert, int k, const float* resid, float* out,
+                                 float* logits, int32_t* topk_idx, float* topk_w, void* stream);
 
 /* ------------------------------------------------------------ MoE over many tokens (config 2)
  * knj_moe_batch_layer: Model::moe on n_tokens rows at once (model.cpp:399-510

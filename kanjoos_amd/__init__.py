@@ -30,7 +30,7 @@ EXPORTS = (
     "knj_device_open", "knj_device_close", "knj_device_caps_get", "knj_check_arch",
     "knj_built_arch", "knj_last_error", "knj_malloc", "knj_free", "knj_memcpy_h2d",
     "knj_memcpy_d2h", "knj_memset_zero", "knj_synchronize", "knj_dequant", "knj_gemv",
-    "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_moe_batch_layer", "knj_attention_step", "knj_model_create_synthetic", "knj_model_create_from_image",
+    "knj_rmsnorm", "knj_moe_router", "knj_moe_decode_layer", "knj_moe_decode_layer_noalloc", "knj_moe_batch_layer", "knj_attention_step", "knj_model_create_synthetic", "knj_model_create_from_image",
     "knj_model_free", "knj_model_image_bytes", "knj_model_image_device", "knj_model_layer_offsets", "knj_model_fill_kv", "knj_gguf_probe",
     "knj_model_create_from_gguf", "knj_model_config_get",
     "knj_model_download_image", "knj_model_reset", "knj_model_pos", "knj_model_set_pos",
@@ -124,6 +124,8 @@ _SIGS = {
     "knj_moe_router": (_i, [_P, _P, _f, _P, _i, _i, _i, _P, _P, _P, _P, _P]),
     "knj_moe_decode_layer": (_i, [_P, _P, _f, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _P, _P,
                                   _P, _P, _P, _P]),
+    "knj_moe_decode_layer_noalloc": (_i, [_P, _P, _f, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _P,
+                                          _P, _P, _P, _P, _P]),
     "knj_moe_batch_layer": (_i, [_P, _P, _f, _P, _P, _P, _P, _i, _i, _i, _i, _i, _i, _i, _P, _P,
                                   _P, _P, _P, _P]),
     "knj_attention_step": (_i, [_P, _P, _P, _P, _P, _f, _f, _i, _i, _i, _i, _i, _P, _P, _P, _P]),
@@ -293,6 +295,17 @@ def moe_decode_layer(x, router_w, gate, up, down, n_embd, n_ff, n_expert, k, out
     check(lib().knj_moe_decode_layer(_p(x), _p(norm_w), eps, _p(router_w), _p(gate), _p(up),
                                      _p(down), type_gate_up, type_down, n_embd, n_ff, n_expert, k,
                                      _p(resid), _p(out), _p(logits), _p(topk_idx), _p(topk_w), None))
+
+
+def moe_decode_layer_noalloc(x, router_w, gate, up, down, n_embd, n_ff, n_expert, k, out, logits,
+                             topk_idx, topk_w, norm_w=None, eps: float = 1e-6, resid=None,
+                             type_gate_up: int = TYPE_Q4_K, type_down: int = TYPE_Q4_K) -> None:
+    """knj_moe_decode_layer with its scratch in the library's fixed device array
+    (no allocation; n_embd + k * n_ff <= 32768)."""
+    check(lib().knj_moe_decode_layer_noalloc(_p(x), _p(norm_w), eps, _p(router_w), _p(gate), _p(up),
+                                             _p(down), type_gate_up, type_down, n_embd, n_ff,
+                                             n_expert, k, _p(resid), _p(out), _p(logits),
+                                             _p(topk_idx), _p(topk_w), None))
 
 
 def moe_batch_layer(x, router_w, gate, up, down, n_tokens, n_embd, n_ff, n_expert, k, out, logits,

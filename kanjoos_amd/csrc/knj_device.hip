@@ -22,7 +22,18 @@ void* g_scratch = nullptr;
 uint64_t g_scratch_bytes = 0;
 unsigned int* g_counters = nullptr;  // zeroed once at open; every user leaves them at zero
 constexpr const char* kBuiltArch = "gfx950";
+// Device address of `scratch` (below) per device, taken at knj_device_open.
+constexpr int kMaxDevices = 64;
+float* g_fixed_scratch[kMaxDevices] = {};
 }  // namespace
+
+// Fixed scratch of knj_moe_decode_layer_noalloc: hx [n_embd] then act
+// [k][n_ff], at most kFixedScratchFloats floats.  Each device holds its own
+// copy for the life of the process.  Host code never passes the array's name
+// to a kernel: it is a host-side stand-in, and the device address comes from
+// hipGetSymbolAddress at knj_device_open.
+constexpr uint64_t kFixedScratchFloats = 32768;  // 128 KiB
+static __device__ __align__(256) float scratch[kFixedScratchFloats];
 
 void set_error(const std::string& msg) { g_error = msg; }
 
@@ -107,6 +118,12 @@ int knj_device_open(int device) {
   if (rc != KNJ_OK) return rc;
   KNJ_HIP(hipSetDevice(device));
   std::lock_guard<std::mutex> g(g_mu);
+  if (device < kMaxDevices && !g_fixed_scratch[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "address of the fixed scratch");
+    g_fixed_scratch[device] = (float*)p;
+  }
   if (!g_counters) {
     KNJ_HIP(hipMalloc(&g_counters, 4096));
     KNJ_HIP(hipMemset(g_counters, 0, 4096));
@@ -261,26 +278,13 @@ int knj_moe_router(const float* x, const float* norm_w, float eps, const float* 
   return KNJ_OK;
 }
 
-int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const float* router_w,
-                         const void* gate, const void* up, const void* down, int type_gate_up,
-                         int type_down, int n_embd, int n_ff, int n_expert, int k,
-                         const float* resid, float* out, float* logits, int32_t* topk_idx,
-                         float* topk_w, void* stream) {
-  int rc = require_open();
-  if (rc) return rc;
-  rc = check_moe_shape(n_embd, n_ff, n_expert, k);
-  if (rc) return rc;
-  KNJ_CHECK_ARG(n_embd <= 4096, "router: n_embd must be at most 4096");
-  KNJ_CHECK_ARG(type_gate_up == KNJ_TYPE_Q4_K, "gate/up experts must be Q4_K");
-  KNJ_CHECK_ARG(type_down == KNJ_TYPE_Q4_K || type_down == KNJ_TYPE_Q6_K,
-                "down experts must be Q4_K or Q6_K");
-  KNJ_CHECK_ARG(x && router_w && gate && up && down && out && logits && topk_idx && topk_w,
-                "null pointer");
-  hipStream_t s = (hipStream_t)stream;
-  // scratch: hx [n_embd], then act [k][n_ff]
-  const uint64_t bytes = (uint64_t)n_embd * 4 + (uint64_t)k * n_ff * 4;
-  float* hx = (float*)device_scratch(bytes, s);
-  if (!hx) return hip_fail(hipErrorOutOfMemory, "scratch");
+// The batch-1 MoE layer on a given scratch of n_embd + k * n_ff floats.
+static int moe_decode_layer_on(float* scratch_ptr, const float* x, const float* norm_w, float eps,
+                               const float* router_w, const void* gate, const void* up,
+                               const void* down, int type_gate_up, int type_down, int n_embd,
+                               int n_ff, int n_expert, int k, const float* resid, float* out,
+                               float* logits, int32_t* topk_idx, float* topk_w, hipStream_t s) {
+  float* hx = scratch_ptr;
   float* act = hx + n_embd;
   // logits only: the gate/up launch routes from them and writes topk_idx/topk_w
   RouterArgs ra{x, norm_w, eps, router_w, n_embd, n_expert, k, hx, logits, nullptr, nullptr,
@@ -291,6 +295,67 @@ int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const f
                 n_expert, k, act, resid, out, nullptr};
   KNJ_HIP(launch_experts(ea, s));
   return KNJ_OK;
+}
+
+static int check_moe_decode_args(const float* x, const float* router_w, const void* gate,
+                                 const void* up, const void* down, int type_gate_up, int type_down,
+                                 int n_embd, int n_ff, int n_expert, int k, float* out,
+                                 float* logits, int32_t* topk_idx, float* topk_w) {
+  int rc = require_open();
+  if (rc) return rc;
+  rc = check_moe_shape(n_embd, n_ff, n_expert, k);
+  if (rc) return rc;
+  KNJ_CHECK_ARG(n_embd <= 4096, "router: n_embd must be at most 4096");
+  KNJ_CHECK_ARG(type_gate_up == KNJ_TYPE_Q4_K, "gate/up experts must be Q4_K");
+  KNJ_CHECK_ARG(type_down == KNJ_TYPE_Q4_K || type_down == KNJ_TYPE_Q6_K,
+                "down experts must be Q4_K or Q6_K");
+  KNJ_CHECK_ARG(x && router_w && gate && up && down && out && logits && topk_idx && topk_w,
+                "null pointer");
+  return KNJ_OK;
+}
+
+int knj_moe_decode_layer(const float* x, const float* norm_w, float eps, const float* router_w,
+                         const void* gate, const void* up, const void* down, int type_gate_up,
+                         int type_down, int n_embd, int n_ff, int n_expert, int k,
+                         const float* resid, float* out, float* logits, int32_t* topk_idx,
+                         float* topk_w, void* stream) {
+  int rc = check_moe_decode_args(x, router_w, gate, up, down, type_gate_up, type_down, n_embd,
+                                 n_ff, n_expert, k, out, logits, topk_idx, topk_w);
+  if (rc) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  const uint64_t bytes = (uint64_t)n_embd * 4 + (uint64_t)k * n_ff * 4;
+  float* buf = (float*)device_scratch(bytes, s);
+  if (!buf) return hip_fail(hipErrorOutOfMemory, "scratch");
+  return moe_decode_layer_on(buf, x, norm_w, eps, router_w, gate, up, down, type_gate_up,
+                             type_down, n_embd, n_ff, n_expert, k, resid, out, logits, topk_idx,
+                             topk_w, s);
+}
+
+int knj_moe_decode_layer_noalloc(const float* x, const float* norm_w, float eps,
+                                 const float* router_w, const void* gate, const void* up,
+                                 const void* down, int type_gate_up, int type_down, int n_embd,
+                                 int n_ff, int n_expert, int k, const float* resid, float* out,
+                                 float* logits, int32_t* topk_idx, float* topk_w, void* stream) {
+  int rc = check_moe_decode_args(x, router_w, gate, up, down, type_gate_up, type_down, n_embd,
+                                 n_ff, n_expert, k, out, logits, topk_idx, topk_w);
+  if (rc) return rc;
+  const uint64_t need = (uint64_t)n_embd + (uint64_t)k * n_ff;
+  if (need > kFixedScratchFloats) {
+    set_error("knj_moe_decode_layer_noalloc: n_embd + k * n_ff = " + std::to_string(need) +
+              " floats exceeds the fixed scratch of " + std::to_string(kFixedScratchFloats) +
+              " floats (use knj_moe_decode_layer)");
+    return KNJ_E_ARG;
+  }
+  int dev = -1;
+  KNJ_HIP(hipGetDevice(&dev));
+  float* fixed = (dev >= 0 && dev < kMaxDevices) ? g_fixed_scratch[dev] : nullptr;
+  if (!fixed) {
+    set_error("knj_moe_decode_layer_noalloc: the current device was not opened with knj_device_open");
+    return KNJ_E_STATE;
+  }
+  return moe_decode_layer_on(fixed, x, norm_w, eps, router_w, gate, up, down, type_gate_up,
+                             type_down, n_embd, n_ff, n_expert, k, resid, out, logits, topk_idx,
+                             topk_w, (hipStream_t)stream);
 }
 
 int knj_moe_batch_layer(const float* x, const float* norm_w, float eps, const float* router_w,
