@@ -22,9 +22,19 @@ __device__ unsigned long long g_knj_stamps[64];
     if (threadIdx.x == 0 && blockIdx.x == 0 && blockIdx.y == 0)                      \
       g_knj_stamps[i] = __builtin_amdgcn_s_memrealtime();                            \
   } while (0)
+// per-workgroup start/end times (slot 0/1) of up to 4096 workgroups
+__device__ unsigned long long g_knj_wg[2][4096];
+#define KNJ_WG_STAMP(slot)                                                           \
+  do {                                                                               \
+    if (threadIdx.x == 0 && blockIdx.x < 4096)                                       \
+      g_knj_wg[slot][blockIdx.x] = __builtin_amdgcn_s_memrealtime();                 \
+  } while (0)
 #else
 #define KNJ_STAMP(i) \
   do {               \
+  } while (0)
+#define KNJ_WG_STAMP(slot) \
+  do {                     \
   } while (0)
 #endif
 
@@ -365,6 +375,15 @@ __device__ __forceinline__ void xslice_global(const float* __restrict__ x,
   xv.s1 = b;
 }
 
+// Byte n of a word as f32: one v_cvt_f32_ubyteN each (the compiler otherwise
+// extracts each nibble with a bit-field extract first).
+__device__ __forceinline__ float ub0(uint32_t v) { float r; asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(v)); return r; }
+__device__ __forceinline__ float ub1(uint32_t v) { float r; asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v)); return r; }
+__device__ __forceinline__ float ub2(uint32_t v) { float r; asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v)); return r; }
+__device__ __forceinline__ float ub3(uint32_t v) { float r; asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v)); return r; }
+
+// 16 code bytes: low nibbles against xlo (sub-block 2g), high nibbles against
+// xhi (sub-block 2g+1), each summed in element order.
 __device__ __forceinline__ void q4k_codes16(uint4 q, const float* xlo, const float* xhi, float& slo,
                                             float& shi) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
@@ -372,14 +391,14 @@ __device__ __forceinline__ void q4k_codes16(uint4 q, const float* xlo, const flo
   for (int k = 0; k < 4; ++k) {
     const uint32_t lo = w[k] & 0x0F0F0F0Fu;
     const uint32_t hi = (w[k] >> 4) & 0x0F0F0F0Fu;
-    slo += (float)(lo & 0xFFu) * xlo[4 * k];
-    slo += (float)((lo >> 8) & 0xFFu) * xlo[4 * k + 1];
-    slo += (float)((lo >> 16) & 0xFFu) * xlo[4 * k + 2];
-    slo += (float)(lo >> 24) * xlo[4 * k + 3];
-    shi += (float)(hi & 0xFFu) * xhi[4 * k];
-    shi += (float)((hi >> 8) & 0xFFu) * xhi[4 * k + 1];
-    shi += (float)((hi >> 16) & 0xFFu) * xhi[4 * k + 2];
-    shi += (float)(hi >> 24) * xhi[4 * k + 3];
+    slo += ub0(lo) * xlo[4 * k];
+    slo += ub1(lo) * xlo[4 * k + 1];
+    slo += ub2(lo) * xlo[4 * k + 2];
+    slo += ub3(lo) * xlo[4 * k + 3];
+    shi += ub0(hi) * xhi[4 * k];
+    shi += ub1(hi) * xhi[4 * k + 1];
+    shi += ub2(hi) * xhi[4 * k + 2];
+    shi += ub3(hi) * xhi[4 * k + 3];
   }
 }
 

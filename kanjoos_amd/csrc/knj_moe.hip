@@ -458,6 +458,7 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   const uint64_t rb = (uint64_t)(F >> 8) * KNJ_Q4K_BLOCK;
   const uint64_t slab = rb * (uint64_t)a.n_embd;
   KNJ_STAMP(8);
+  KNJ_WG_STAMP(0);
   const int row = min((int)(blockIdx.x * (kBlock / 64) + wave), a.n_embd - 1);
   const bool row_ok = (int)(blockIdx.x * (kBlock / 64) + wave) < a.n_embd;
   const int b = active ? (sub >> 2) : 0, g = sub & 3;
@@ -556,11 +557,111 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
     if (r < K) o = __fadd_rn(o, __fmul_rn(wr, dr));
   }
   KNJ_STAMP(11);
-  if (!row_ok || lane != 0) return;
-  const float v = a.resid ? __fadd_rn(resid, o) : o;
-  a.out[row] = v;
-  if (a.hidden_copy) a.hidden_copy[row] = v;
+  if (row_ok && lane == 0) {
+    const float v = a.resid ? __fadd_rn(resid, o) : o;
+    a.out[row] = v;
+    if (a.hidden_copy) a.hidden_copy[row] = v;
+  }
   KNJ_STAMP(12);
+  KNJ_WG_STAMP(1);
+}
+
+// ------------------------------------------------------------------ down (Q4_K, k <= 8)
+// Workgroup = 8 waves x 8 output rows; wave w takes expert slot w for all 8
+// rows (16-lane row groups, one 64-weight slice per lane, two rows per lane
+// so each staged activation slice serves two rows).  The loads are ordered so
+// no wait covers more than it needs: first the k activation vectors, the
+// routing and the residuals (one round trip), then this wave's expert rows;
+// the activations are staged in LDS while the weights are in flight.  The k
+// products of a row are folded in ascending expert index by one thread per row.
+constexpr int kDownRows = 8;
+
+__global__ __launch_bounds__(512) void k_expert_down8(ExpertArgs a) {
+  constexpr int KMAX = 8;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int rg = lane >> 4, sub = lane & 15;
+  const int F = a.n_ff, K = a.k, n = K * F;
+  const int nslices = F >> 6;
+  const bool active = sub < nslices && wave < K;
+  const uint64_t rb = (uint64_t)(F >> 8) * KNJ_Q4K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_embd;
+  const int r0 = blockIdx.x * kDownRows;
+  const int kk = min(wave, K - 1);
+  __shared__ float acts[KMAX * xpad_size(1024)];
+  __shared__ float sums[KMAX * 32];
+  __shared__ float dots[KMAX][kDownRows];
+  const int fpad = xpad_size(F);
+  // 1) activations (k * n_ff <= 8192 floats: four float4 per thread), routing, residuals
+  float4 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * (t + 512 * j);
+    v[j] = *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
+  }
+  int ids[KMAX];
+  float wts[KMAX];
+#pragma unroll
+  for (int q = 0; q < KMAX; ++q) {
+    ids[q] = q < K ? a.topk_idx[q] : 0x7FFFFFFF;
+    wts[q] = q < K ? a.topk_w[q] : 0.0f;
+  }
+  const bool own_row = t < kDownRows && r0 + t < a.n_embd;
+  const float resid = (own_row && a.resid) ? a.resid[r0 + t] : 0.0f;
+  // 2) this wave's expert rows (valid rows only; rows past n_embd read row n_embd - 1)
+  int e = ids[0];
+#pragma unroll
+  for (int q = 1; q < KMAX; ++q) e = kk == q ? ids[q] : e;
+  const int sl = active ? sub : 0;
+  const int b = sl >> 2, g = sl & 3;
+  const int ra = min(r0 + rg, a.n_embd - 1), rb2 = min(r0 + rg + 4, a.n_embd - 1);
+  const uint8_t* ex = a.down + (uint64_t)e * slab + (uint64_t)b * KNJ_Q4K_BLOCK;
+  const Q4Slice q0 = q4k_load(ex + (uint64_t)ra * rb, g);
+  const Q4Slice q1 = q4k_load(ex + (uint64_t)rb2 * rb, g);
+  __builtin_amdgcn_sched_barrier(0);
+  // 3) stage the activations with their 32-element sums (eight threads per sub-block)
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * (t + 512 * j);
+    const float sb = group_sum<8>((v[j].x + v[j].y) + (v[j].z + v[j].w));
+    if (i < n) {
+      const int k2 = i / F, c = i - k2 * F;
+      *reinterpret_cast<float4*>(acts + k2 * fpad + xpad(c)) = v[j];
+      if ((t & 7) == 0) sums[i >> 5] = sb;
+    }
+  }
+  __syncthreads();
+  // 4) the two rows of this lane's group
+  XSlice xv;
+  const int sb0 = kk * (F >> 5) + 2 * sl;
+  xslice_load_sums(acts + kk * fpad, sl, sums[sb0], sums[sb0 + 1], xv);
+  const float d0 = group_sum<16>(active ? q4k_dot(q0, g, xv) : 0.0f);
+  const float d1 = group_sum<16>(active ? q4k_dot(q1, g, xv) : 0.0f);
+  if (sub == 0 && wave < K) {
+    dots[wave][rg] = d0;
+    dots[wave][rg + 4] = d1;
+  }
+  __syncthreads();
+  if (!own_row) return;
+  // 5) ascending expert index: rank[q] = #{slots with a lower expert}
+  float o = 0.0f;
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    float wr = 0.0f, dr = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KMAX; ++q) {
+      int rank = 0;
+#pragma unroll
+      for (int q2 = 0; q2 < KMAX; ++q2) rank += ids[q2] < ids[q] ? 1 : 0;
+      const bool hit = rank == r;
+      wr = hit ? wts[q] : wr;
+      dr = hit ? dots[q][t] : dr;
+    }
+    if (r < K) o = __fadd_rn(o, __fmul_rn(wr, dr));
+  }
+  const int row = r0 + t;
+  const float out = a.resid ? __fadd_rn(resid, o) : o;
+  a.out[row] = out;
+  if (a.hidden_copy) a.hidden_copy[row] = out;
 }
 
 // ------------------------------------------------------------------ down (Q6_K, n_ff <= 1024)
@@ -778,6 +879,14 @@ hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t
 }
 
 hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+  if (a.type_down == KNJ_TYPE_Q4_K && a.n_ff <= 1024 && a.k <= 8) {
+    const int grid = (a.n_embd + kDownRows - 1) / kDownRows;
+    if (t0 || span_take("k_expert_down8", &t0, &t1))
+      hipExtLaunchKernelGGL(k_expert_down8, dim3(grid), dim3(512), 0u, s, t0, t1, 0u, a);
+    else
+      hipLaunchKernelGGL(k_expert_down8, dim3(grid), dim3(512), 0, s, a);
+    return hipGetLastError();
+  }
   if (a.type_down == KNJ_TYPE_Q4_K && a.n_ff <= 1024) {
     const int kpg = (a.k + 3) / 4;
     const int grid = (a.n_embd + 3) / 4;
