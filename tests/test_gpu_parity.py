@@ -445,18 +445,37 @@ def test_full_model_step_parity(full_pair):
 
 
 def test_full_model_greedy_golden(device):
-    """64 greedy tokens of the full model against the oracle's committed tokens."""
+    """64 greedy tokens of the full model against the oracle's committed run
+    (tests/golden/full_greedy.json, 7 distinct tokens, smallest top-1/top-2
+    margin 3.0e-3): identical tokens, and at every step the logits of the
+    oracle's 16 largest entries within 1e-2 of the largest logit.  Each side
+    keeps its own f16 cache here (nothing is adopted), so the two caches differ
+    by f16 rounding flips of single elements, and a flipped key element moves a
+    sharp attention score enough to move the logits: measured 1.2e-4 after the
+    12-token prompt, 1-2e-4 at most steps, up to 5e-3 at a few.  The 1e-5 bar
+    on logits and on every layer is held where the oracle adopts the GPU's
+    cache values (test_full_model_step_parity, tests/test_gpu_full_configs.py);
+    this test pins the free-running token sequence."""
     path = os.path.join(GOLDEN, "full_greedy.json")
-    if not os.path.exists(path):
-        pytest.skip("full_greedy.json not generated")
     want = json.load(open(path))
     gm = K.Model.synthetic(K.qwen3_30b_a3b(**full_config()), seed=want["seed"])
-    lg = gm.forward(want["prompt"])
-    first = int(np.argmax(lg))
-    assert first == want["tokens"][0]
-    got = [first] + list(gm.decode_greedy(first, len(want["tokens"]) - 1))
-    gm.close()
-    assert got == want["tokens"]
+    try:
+        lg = gm.forward(want["prompt"])
+        worst = []
+        for step, tok in enumerate(want["tokens"]):
+            ids = np.asarray(want["top16_ids"][step])
+            ref = np.asarray(want["top16_logits"][step], dtype=np.float64)
+            scale = float(np.max(np.abs(ref)))
+            err = float(np.max(np.abs(lg[ids].astype(np.float64) - ref))) / scale
+            worst.append(err)
+            assert int(np.argmax(lg)) == tok, (step, int(np.argmax(lg)), tok)
+            assert err <= 1e-2, (step, err)
+            if step + 1 < len(want["tokens"]):
+                lg = gm.forward([tok])
+        say(f"golden: {len(want['tokens'])} tokens ({want['distinct_tokens']} distinct, min margin "
+            f"{want['min_margin']:.3g}); logits vs oracle: step 0 {worst[0]:.2e}, max {max(worst):.2e}; all {[round(w * 1e6, 1) for w in worst]}")
+    finally:
+        gm.close()
 
 
 def _attn_ref(q, k, v, qn, kn, eps, base, pos, n_head, n_kv, D, kc, vc):
