@@ -294,7 +294,7 @@ def main() -> int:
     ap.add_argument("--long-ctx", type=int, default=32768,
                     help="context of the config-5 leg (0 skips it)")
     ap.add_argument("--long-steps", type=int, default=32)
-    ap.add_argument("--cpu-sweep", default="1:3,4:8,16:8",
+    ap.add_argument("--cpu-sweep", default="1:8,4:8,16:8",
                     help="CPU baseline cells threads:tokens (thread counts capped at --cpu-share)")
     ap.add_argument("--cpu-share", type=int, default=16,
                     help="host threads the GPU box grants one GPU's job")
