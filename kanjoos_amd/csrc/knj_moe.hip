@@ -664,6 +664,102 @@ __global__ __launch_bounds__(512) void k_expert_down8(ExpertArgs a) {
   if (a.hidden_copy) a.hidden_copy[row] = out;
 }
 
+// ------------------------------------------------------------------ down (Q6_K, k <= 8)
+// As k_expert_down8 for Q6_K experts: wave w takes expert slot w for the
+// workgroup's 8 rows; lane = one 32-weight unit of a row (32-lane halves take
+// rows 2i and 2i + 1, four rounds), read with q6_unit_load as in the one-row
+// kernel; activations and their 8-element sums staged once per workgroup.
+__global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
+  constexpr int KMAX = 8;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int F = a.n_ff, K = a.k, n = K * F;
+  const int nunits = F / 32;
+  const int half = lane >> 5, u = lane & 31;
+  const bool active = u < nunits && wave < K;
+  const int uu = u < nunits ? u : 0;
+  const int b = uu >> 3, hf = (uu >> 2) & 1, o = uu & 3;
+  const uint64_t rb = (uint64_t)(F / KNJ_QK) * KNJ_Q6K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_embd;
+  const int r0 = blockIdx.x * kDownRows;
+  const int kk = min(wave, K - 1);
+  __shared__ float acts[KMAX * 1024];
+  __shared__ float s8[KMAX * 1024 / 8];
+  __shared__ float dots[KMAX][kDownRows];
+  float4 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * (t + 512 * j);
+    v[j] = *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
+  }
+  int ids[KMAX];
+  float wts[KMAX];
+#pragma unroll
+  for (int q = 0; q < KMAX; ++q) {
+    ids[q] = q < K ? a.topk_idx[q] : 0x7FFFFFFF;
+    wts[q] = q < K ? a.topk_w[q] : 0.0f;
+  }
+  const bool own_row = t < kDownRows && r0 + t < a.n_embd;
+  const float resid = (own_row && a.resid) ? a.resid[r0 + t] : 0.0f;
+  int e = ids[0];
+#pragma unroll
+  for (int q = 1; q < KMAX; ++q) e = kk == q ? ids[q] : e;
+  const uint8_t* ex = a.down + (uint64_t)e * slab + (uint64_t)b * KNJ_Q6K_BLOCK;
+  Q6Unit qu[kDownRows / 2];
+#pragma unroll
+  for (int it = 0; it < kDownRows / 2; ++it) {
+    const int row = min(r0 + 2 * it + half, a.n_embd - 1);
+    qu[it] = q6_unit_load(ex + (uint64_t)row * rb, hf, o);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * (t + 512 * j);
+    if (i < n) *reinterpret_cast<float4*>(acts + i) = v[j];
+  }
+  __syncthreads();
+  for (int g = t; 8 * g < n; g += 512) {
+    const float4 x0 = *reinterpret_cast<const float4*>(acts + 8 * g);
+    const float4 x1 = *reinterpret_cast<const float4*>(acts + 8 * g + 4);
+    s8[g] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
+  }
+  __syncthreads();
+  float4 x8[4][2];
+  float sx[4];
+#pragma unroll
+  for (int tq = 0; tq < 4; ++tq) {
+    const int i = kk * F + 256 * b + 128 * hf + 32 * tq + 8 * o;
+    x8[tq][0] = *reinterpret_cast<const float4*>(acts + i);
+    x8[tq][1] = *reinterpret_cast<const float4*>(acts + i + 4);
+    sx[tq] = s8[i >> 3];
+  }
+#pragma unroll
+  for (int it = 0; it < kDownRows / 2; ++it) {
+    const float acc = group_sum<32>(active ? q6_unit_dot(qu[it], x8, sx) : 0.0f);
+    if (u == 0 && wave < K) dots[wave][2 * it + half] = acc;
+  }
+  __syncthreads();
+  if (!own_row) return;
+  float o_ = 0.0f;
+#pragma unroll
+  for (int r = 0; r < KMAX; ++r) {
+    float wr = 0.0f, dr = 0.0f;
+#pragma unroll
+    for (int q = 0; q < KMAX; ++q) {
+      int rank = 0;
+#pragma unroll
+      for (int q2 = 0; q2 < KMAX; ++q2) rank += ids[q2] < ids[q] ? 1 : 0;
+      const bool hit = rank == r;
+      wr = hit ? wts[q] : wr;
+      dr = hit ? dots[q][t] : dr;
+    }
+    if (r < K) o_ = __fadd_rn(o_, __fmul_rn(wr, dr));
+  }
+  const int row = r0 + t;
+  const float out = a.resid ? __fadd_rn(resid, o_) : o_;
+  a.out[row] = out;
+  if (a.hidden_copy) a.hidden_copy[row] = out;
+}
+
 // ------------------------------------------------------------------ down (Q6_K, n_ff <= 1024)
 // Wave = one output row for all k experts: 32-lane group gi takes expert slots
 // gi, gi+2, ..; lane = one 32-weight Q6_K unit of the row (n_ff / 32 <= 32
@@ -904,6 +1000,14 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
     return hipErrorInvalidValue;
   }
   if (a.type_down != KNJ_TYPE_Q6_K) return hipErrorInvalidValue;
+  if (a.n_ff <= 1024 && a.k <= 8) {
+    const int grid = (a.n_embd + kDownRows - 1) / kDownRows;
+    if (t0 || span_take("k_expert_down8_q6", &t0, &t1))
+      hipExtLaunchKernelGGL(k_expert_down8_q6, dim3(grid), dim3(512), 0u, s, t0, t1, 0u, a);
+    else
+      hipLaunchKernelGGL(k_expert_down8_q6, dim3(grid), dim3(512), 0, s, a);
+    return hipGetLastError();
+  }
   if (a.n_ff <= 1024 && a.k <= 16) {
     const int kpg = (a.k + 1) / 2;
     const int grid = (a.n_embd + 3) / 4;
