@@ -223,14 +223,14 @@ __global__ __launch_bounds__(kBlock) void k_route_batch(const float* __restrict_
 // One workgroup: pairs (token, slot) grouped by expert.  offsets[e] is the
 // first pair of expert e (offsets[E] = m*k); pair_tok[q] the token of pair q;
 // pair_of[t*k + s] the pair of token t's slot s; items the (expert, first
-// pair) of every tile of kTok pairs.  The order of pairs within an expert does
+// pair) of every tile of `tile` pairs.  The order of pairs within an expert does
 // not change any result: each pair's outputs depend only on its own row.
 __global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ topk_idx, int m,
                                                    int k, int n_expert, int* __restrict__ offsets,
                                                    int* __restrict__ pair_tok,
                                                    int* __restrict__ pair_of,
                                                    int2* __restrict__ items,
-                                                   int* __restrict__ n_items) {
+                                                   int* __restrict__ n_items, int tile) {
   __shared__ int cnt[256], cur[256];
   __shared__ int wsum[2][kBlock / 64];
   const int t = threadIdx.x, P = m * k, lane = t & 63, wave = t >> 6;
@@ -240,7 +240,7 @@ __global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ t
   __syncthreads();
   // exclusive prefix sums over the experts (thread t = expert t) of the pair
   // counts and the tile counts: a scan within each wave, then the wave totals
-  const int c = t < n_expert ? cnt[t] : 0, ct = (c + kTok - 1) / kTok;
+  const int c = t < n_expert ? cnt[t] : 0, ct = (c + tile - 1) / tile;
   int sc = c, st = ct;
   for (int d = 1; d < 64; d <<= 1) {
     const int yc = __shfl_up(sc, d, 64), yt = __shfl_up(st, d, 64);
@@ -262,7 +262,7 @@ __global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ t
   if (t < n_expert) {
     offsets[t] = oc;
     cur[t] = oc;
-    for (int i = 0; i < ct; ++i) items[ot + i] = make_int2(t, i * kTok);
+    for (int i = 0; i < ct; ++i) items[ot + i] = make_int2(t, i * tile);
     if (t == n_expert - 1) {
       offsets[n_expert] = oc + c;
       *n_items = ot + ct;
@@ -297,6 +297,7 @@ struct GroupArgs {
   // residual) and k_ksum adds the ranges in order.
   int ksplit = 1;
   float* partial = nullptr;
+  int tile = kTok;          // pairs per work item of the list (<= kTok)
 };
 
 // Workgroup = one tile of kTok pairs of one expert x kRowsWG weight rows; wave
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
     const int2 it = a.items[item];
     e = it.x;
     p0 = a.offsets[e] + it.y;
-    cnt = min(kTok, a.offsets[e + 1] - p0);
+    cnt = min(a.tile, a.offsets[e + 1] - p0);
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int rbase = blockIdx.x * kRowsWG + wave * 32;
@@ -480,6 +481,210 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
   }
 }
 
+// Grouped Q4_K product for lists whose experts hold few pairs (decode
+// batches: at 32 sequences x 8 slots over 128 experts about 2 pairs each),
+// where 32-pair tiles would be mostly padding.  Work item = up to kFew = 8
+// pairs of one expert.  One 16x16x32 f16 matrix-core step: the 16 A rows are
+// the 8 pairs x {high part, remainder} (A row 2 p + part), the 16 B columns
+// are 16 weight rows, so lane l's four results are pairs 2 (l/16) and
+// 2 (l/16) + 1 (high and remainder each) of weight row l % 16, and the two
+// parts are added in the lane at the end.  Lane group kq = l/16 owns code
+// group kq (32 bytes: sub-blocks 2 kq and 2 kq + 1) of its row's
+// super-block: step u takes bytes 8 (u/2) .. +7 of the group, nibble u % 2,
+// i.e. the 8-group 8 kq + 4 (u % 2) + u/2 of the super-block; the K order of
+// a step differs by lane group, and A is read to match.  The scales ride in B
+// (sc q is exact in f16); the min term is a ninth step per super-block whose
+// K slots 8 kq, 8 kq + 1 carry the sub-block sums (A) and mins (B) of
+// sub-blocks 2 kq, 2 kq + 1 and zeros elsewhere.  Per super-block:
+// acc += d cq - dmin cm.  A comes straight from global memory (the pairs'
+// rows are shared by every workgroup of the expert and stay in L2).
+constexpr int kFew = 8;
+constexpr int kFewBelow = 8;   // the few kernels when pairs < kFewBelow * experts
+
+__device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// (w & m) | c in one instruction (with the masks in registers; the
+// compiler splits it when they are literals)
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(m), "v"(c));
+  return r;
+}
+__device__ __forceinline__ half2v cvt_h2(float v) {
+  const _Float16 h = (_Float16)v;
+  return half2v{h, h};
+}
+constexpr uint32_t kNib = 0x000F000Fu;      // low nibbles of bytes 0 and 2
+constexpr uint32_t kF16Base = 0x64006400u;  // f16 1024 in both halves
+
+struct FewBlock {
+  uint4 h, c0, c1;  // header (d, dmin, scales), the lane's 32 code bytes
+};
+
+
+// Lane constants of the few-pair kernels: bit positions of the scale and min
+// of sub-blocks 2 kq and 2 kq + 1 in the 12 scale bytes (words 1..3 of a
+// Q4_K header): 6 bits at byte s of words 1 (scale) and 2 (min) for s < 4;
+// else the low (scale) / high (min) nibble of byte s - 4 of word 3 and the top
+// two bits of byte s - 4 of words 1 and 2.
+struct FewLane {
+  bool klo;
+  int oa, ob, oc;
+  __device__ explicit FewLane(int kq)
+      : klo(kq < 2),
+        oa(kq < 2 ? 16 * kq : 16 * kq - 32),
+        ob(kq < 2 ? 16 * kq + 4 : 16 * kq - 26),
+        oc(kq < 2 ? 16 * kq : 16 * kq - 28) {}
+};
+
+// One super-block of one (matrix, 16-row tile): the eight code steps and the
+// min-term step, acc += d cq - dmin cm.
+__device__ __forceinline__ void few_superblock(const FewBlock& b, const half8 (&x)[8], half8 xm,
+                                               const FewLane& L, f32x4& acc) {
+  const uint32_t X = L.klo ? b.h.y : b.h.w, Y = L.klo ? b.h.z : b.h.w;
+  const uint32_t sc0 = __builtin_amdgcn_ubfe(X, L.oa, 4) | (__builtin_amdgcn_ubfe(b.h.y, L.ob, 2) << 4);
+  const uint32_t sc1 = __builtin_amdgcn_ubfe(X, L.oa + 8, 4) | (__builtin_amdgcn_ubfe(b.h.y, L.ob + 8, 2) << 4);
+  const uint32_t mn0 = __builtin_amdgcn_ubfe(Y, L.oc, 4) | (__builtin_amdgcn_ubfe(b.h.z, L.ob, 2) << 4);
+  const uint32_t mn1 = __builtin_amdgcn_ubfe(Y, L.oc + 8, 4) | (__builtin_amdgcn_ubfe(b.h.z, L.ob + 8, 2) << 4);
+  const float fs0 = (float)sc0, fs1 = (float)sc1;
+  // low nibbles: (1024 + q) sc - 1024 sc; high nibbles, unshifted:
+  // (1024 + 16 q) sc / 16 - 64 sc (every value exact in f16)
+  const half2v s0 = cvt_h2(fs0), n0 = cvt_h2(-1024.0f * fs0);
+  const half2v s1 = cvt_h2(0.0625f * fs1), n1 = cvt_h2(-64.0f * fs1);
+  half8 bm = {};
+  bm[0] = (_Float16)(float)mn0;
+  bm[1] = (_Float16)(float)mn1;
+  const f32x4 cm = mfma16(xm, bm, f32x4{0.f, 0.f, 0.f, 0.f});
+  f32x4 cq = {0.f, 0.f, 0.f, 0.f};
+  const uint32_t wd[8] = {b.c0.x, b.c0.y, b.c0.z, b.c0.w, b.c1.x, b.c1.y, b.c1.z, b.c1.w};
+  const uint32_t mlo = kNib, mhi = kNib << 4;
+  auto cv = [&](uint32_t w, uint32_t m, half2v sc, half2v nc) {
+    return __builtin_elementwise_fma(as_h2(and_or(w, m, kF16Base)), sc, nc);
+  };
+#pragma unroll
+  for (int hw = 0; hw < 4; ++hw) {
+    // bytes 8 hw .. 8 hw + 7 of the lane's code group: bytes (0, 2), (1, 3),
+    // (4, 6), (5, 7) per half2, low nibbles then high nibbles
+    const uint32_t wa = wd[2 * hw], wb = wd[2 * hw + 1], sa = wa >> 8, sb = wb >> 8;
+    const half2v l0 = cv(wa, mlo, s0, n0), l1 = cv(sa, mlo, s0, n0);
+    const half2v l2 = cv(wb, mlo, s0, n0), l3 = cv(sb, mlo, s0, n0);
+    const half2v h0 = cv(wa, mhi, s1, n1), h1 = cv(sa, mhi, s1, n1);
+    const half2v h2 = cv(wb, mhi, s1, n1), h3 = cv(sb, mhi, s1, n1);
+    cq = mfma16(x[2 * hw], half8{l0.x, l0.y, l1.x, l1.y, l2.x, l2.y, l3.x, l3.y}, cq);
+    cq = mfma16(x[2 * hw + 1], half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y}, cq);
+  }
+  const float d = h2f(b.h.x), dmin = h2f(b.h.x >> 16);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] += d * cq[i] - dmin * cm[i];
+}
+
+// The few-pair grouped product with the reduction split over the waves of a
+// workgroup: workgroup = (FT 16-row tiles of every matrix) x (up to 8 pairs of
+// one expert); wave w takes super-blocks w, w + KS, ... (KS = waves, NSBW per
+// wave) and issues every load of them before any arithmetic, so a workgroup
+// asks for whole rows (all super-blocks) of its tiles at once.  The waves'
+// partial tiles meet in LDS and are added in wave order.
+template <bool GATEUP, int FT, int NSBW>
+__global__ __launch_bounds__(256) void k_group_fewk(GroupArgs a) {
+  constexpr int NM = GATEUP ? 2 : 1;
+  __shared__ f32x4 part[4][NM * FT][64];
+  const int item = blockIdx.y;
+  if (item >= *a.n_items) return;  // uniform over the workgroup
+  const int2 it = a.items[item];
+  const int e = it.x, p0 = a.offsets[e] + it.y;
+  const int cnt = min(kFew, a.offsets[e + 1] - p0);
+  const int KS = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, kq = lane >> 4;
+  const int rbase = blockIdx.x * 16 * FT;
+  const int nsb = a.n_in >> 8;
+  const uint64_t P = (uint64_t)a.P;
+  const uint64_t rb = (uint64_t)nsb * KNJ_Q4K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_out;
+  // A row of this lane: pair ap (clamped into the item), part apart
+  const int ap = p0 + min(col >> 1, cnt - 1), apart = col & 1;
+  const _Float16* abase = (apart ? a.al : a.ah) + (uint64_t)ap * 8;
+  const _Float16* sbase = (apart ? a.sl : a.sh) + (uint64_t)ap * 8 + 2 * kq;
+  const FewLane L(kq);
+  struct Buf {
+    FewBlock w[NM][FT];
+    half8 x[8];
+    uint32_t s2;
+  };
+  Buf B[NSBW];
+#pragma unroll
+  for (int i = 0; i < NSBW; ++i) {
+    const int sb = wave + KS * i;
+    if (sb < nsb) {  // uniform over the wave
+#pragma unroll
+      for (int mtx = 0; mtx < NM; ++mtx)
+#pragma unroll
+        for (int f = 0; f < FT; ++f) {
+          const int row = min(rbase + 16 * f + col, a.n_out - 1);
+          const uint8_t* p = (mtx ? a.w1 : a.w0) + (uint64_t)e * slab + (uint64_t)row * rb +
+                             (uint64_t)sb * KNJ_Q4K_BLOCK;
+          B[i].w[mtx][f].h = *reinterpret_cast<const uint4*>(p);
+          B[i].w[mtx][f].c0 = *reinterpret_cast<const uint4*>(p + KNJ_Q4K_QS + 32 * kq);
+          B[i].w[mtx][f].c1 = *reinterpret_cast<const uint4*>(p + KNJ_Q4K_QS + 32 * kq + 16);
+        }
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        B[i].x[u] = ld_h8(abase + (uint64_t)(32 * sb + 8 * kq + 4 * (u & 1) + (u >> 1)) * P * 8);
+      B[i].s2 = *reinterpret_cast<const uint32_t*>(sbase + (uint64_t)sb * P * 8);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc[NM][FT];
+#pragma unroll
+  for (int mtx = 0; mtx < NM; ++mtx)
+#pragma unroll
+    for (int f = 0; f < FT; ++f) acc[mtx][f] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < NSBW; ++i) {
+    if (wave + KS * i < nsb) {
+      half8 xm = {};
+      xm[0] = as_h2(B[i].s2).x;
+      xm[1] = as_h2(B[i].s2).y;
+#pragma unroll
+      for (int mtx = 0; mtx < NM; ++mtx)
+#pragma unroll
+        for (int f = 0; f < FT; ++f) few_superblock(B[i].w[mtx][f], B[i].x, xm, L, acc[mtx][f]);
+    }
+  }
+#pragma unroll
+  for (int mtx = 0; mtx < NM; ++mtx)
+#pragma unroll
+    for (int f = 0; f < FT; ++f) part[wave][mtx * FT + f][lane] = acc[mtx][f];
+  __syncthreads();
+  // wave w finishes tiles w, w + KS, ... of every matrix, the ranges added in
+  // wave order; lane's four values: pair 2 kq + i / 2, part i % 2, weight row
+  // 16 f + col
+  for (int f = wave; f < FT; f += KS) {
+    const int row = rbase + 16 * f + col;
+    if (row >= a.n_out) continue;
+    f32x4 s[NM];
+#pragma unroll
+    for (int mtx = 0; mtx < NM; ++mtx) {
+      s[mtx] = part[0][mtx * FT + f][lane];
+      for (int w = 1; w < KS; ++w) s[mtx] += part[w][mtx * FT + f][lane];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int pj = 2 * kq + h;
+      if (pj >= cnt) continue;
+      float v = s[0][2 * h] + s[0][2 * h + 1];
+      if constexpr (GATEUP) {
+        const float u = s[NM - 1][2 * h] + s[NM - 1][2 * h + 1];
+        v = (v / (1.0f + expf(-v))) * u;
+      }
+      const uint64_t o = (uint64_t)(p0 + pj) * a.n_out + row;
+      a.out[o] = a.resid ? a.resid[o] + v : v;
+    }
+  }
+}
+
 // Q6_K down projection of the grouped MoE (d * sc * (q - 32) per weight,
 // sc per 16 weights): the same workgroup tiling and A staging as
 // k_group_q4k, but one matrix-core step covers exactly one 16-weight scale
@@ -508,7 +713,7 @@ __global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
     const int2 it = a.items[item];
     e = it.x;
     p0 = a.offsets[e] + it.y;
-    cnt = min(kTok, a.offsets[e + 1] - p0);
+    cnt = min(a.tile, a.offsets[e + 1] - p0);
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int rbase = blockIdx.x * kRowsWG + wave * 32;
@@ -773,9 +978,9 @@ __global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
         ws[r] = wt[s];
       }
   }
-  // one float4 of columns per thread (blockIdx.y picks the 4 * kBlock-column
-  // range): every slot's load is issued before the first use
-  const int i = 4 * (blockIdx.y * kBlock + threadIdx.x);
+  // one float4 of columns per thread (blockIdx.y picks the 4 * blockDim.x-
+  // column range): every slot's load is issued before the first use
+  const int i = 4 * (blockIdx.y * blockDim.x + threadIdx.x);
   if (i >= n) return;
   float4 v[16];
 #pragma unroll
@@ -806,7 +1011,7 @@ __global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
 
 uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int k) {
   const uint64_t P = (uint64_t)m * k, H = n_embd, F = n_ff;
-  const uint64_t items = (uint64_t)n_expert + (P + kTok - 1) / kTok;
+  const uint64_t items = (uint64_t)n_expert + (P + kFew - 1) / kFew;  // the smaller tile bounds both lists
   uint64_t b = 0;
   auto add = [&](uint64_t bytes) { b += (bytes + 255) & ~255ull; };
   add(m * H * 4);                       // hx
@@ -838,6 +1043,19 @@ hipError_t group_lds_attr() {
   return e;
 }
 
+// The few-pair product over n_in: KS = min(4, super-blocks) waves per
+// workgroup, each with NSBW super-blocks; ft 16-row tiles per workgroup.
+template <bool GATEUP>
+hipError_t launch_fewk(const GroupArgs& g, int max_items, int ft, hipStream_t s) {
+  const int nsb = g.n_in >> 8, ks = std::min(4, nsb), nw = (nsb + ks - 1) / ks;
+  const dim3 grid((g.n_out + 16 * ft - 1) / (16 * ft), max_items), block(64 * ks);
+#define KNJ_FEWK(FT, NW) \
+  if (ft == FT && nw <= NW) { KNJ_LAUNCH((k_group_fewk<GATEUP, FT, NW>), grid, block, 0, s, g); return hipGetLastError(); }
+  KNJ_FEWK(2, 1) KNJ_FEWK(2, 2) KNJ_FEWK(2, 4) KNJ_FEWK(4, 1)
+#undef KNJ_FEWK
+  return hipErrorInvalidValue;
+}
+
 hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s) {
   if (hipError_t e = group_lds_attr()) return e;
   const int m = a.m, H = a.n_embd, F = a.n_ff, E = a.n_expert, K = a.k;
@@ -845,7 +1063,11 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
       (a.type_down != KNJ_TYPE_Q4_K && a.type_down != KNJ_TYPE_Q6_K))
     return hipErrorInvalidValue;
   const uint64_t P = (uint64_t)m * K;
-  const int max_items = E + (int)((P + kTok - 1) / kTok);
+  // few pairs per expert on average (decode batches): 8-pair items on the
+  // 16x16x32 kernels; else 32-pair items on the 32x32x16 kernels
+  const bool few = P < (uint64_t)kFewBelow * E;
+  const int tile = few ? kFew : kTok;
+  const int max_items = E + (int)((P + tile - 1) / tile);
   uint8_t* p = (uint8_t*)scratch;
   auto take = [&](uint64_t bytes) {
     uint8_t* q = p;
@@ -879,23 +1101,34 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   KNJ_LAUNCH(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, a.logits, m, E, K,
                      a.topk_idx, a.topk_w);
   KNJ_LAUNCH(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
-                     pair_of, items, n_items);
+                     pair_of, items, n_items, tile);
   KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), H / 256), dim3(kBlock), 0, s, xin,
              pair_tok, H, (int)P, xh, xl, sxh, sxl);
   GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, (int)P, offsets, items, n_items, act};
-  KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
-                     kGroupLds, s, gu);
+  gu.tile = tile;
+  // (measured at 32 sequences: 32 rows per workgroup for gate/up, whose
+  // super-blocks fill two per wave; 64 for down, one per wave)
+  if (few) {
+    if (hipError_t e = launch_fewk<true>(gu, max_items, 2, s)) return e;
+  } else
+    KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+               kGroupLds, s, gu);
   KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), F / 256), dim3(kBlock), 0, s, act,
              nullptr, F, (int)P, ah, al, sah, sal);
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
-  if (a.type_down == KNJ_TYPE_Q6_K)
+  dn.tile = tile;
+  if (few && a.type_down == KNJ_TYPE_Q4_K) {
+    if (hipError_t e = launch_fewk<false>(dn, max_items, (F >> 8) <= 4 ? 4 : 2, s)) return e;
+  } else if (a.type_down == KNJ_TYPE_Q6_K)
     KNJ_LAUNCH(k_group_q6k, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock), kGroupLds,
                s, dn);
   else
     KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                kGroupLds, s, dn);
-  KNJ_LAUNCH(k_combine, dim3(m, (H + 4 * kBlock - 1) / (4 * kBlock)), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K,
-                     H, a.resid, a.out, a.hidden_copy);
+  // one wave per 256 columns of a token: enough workgroups for the chip at
+  // decode batch sizes
+  KNJ_LAUNCH(k_combine, dim3(m, (H + 255) / 256), dim3(64), 0, s, y, pair_of, a.topk_idx,
+             a.topk_w, K, H, a.resid, a.out, a.hidden_copy);
   return hipGetLastError();
 }
 
