@@ -941,46 +941,32 @@ __global__ void k_argmax_final(const unsigned long long* __restrict__ keys, int 
 // ------------------------------------------------------------------ combine
 // out[t] = resid[t] + sum over token t's k slots, in ascending expert order,
 // of w * y[pair] (the scatter order of model.cpp:499-507).
-__global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
-                                                    const int* __restrict__ pair_of,
-                                                    const int32_t* __restrict__ topk_idx,
-                                                    const float* __restrict__ topk_w, int k,
-                                                    int n, const float* __restrict__ resid,
-                                                    float* __restrict__ out,
-                                                    float* __restrict__ out2) {
-  const int t = blockIdx.x;
-  int ids[16], pr[16], rank[16];
-  float wt[16];
-#pragma unroll
-  for (int s = 0; s < 16; ++s) {
-    ids[s] = s < k ? topk_idx[(uint64_t)t * k + s] : 0x7FFFFFFF;
-    wt[s] = s < k ? topk_w[(uint64_t)t * k + s] : 0.0f;
-    pr[s] = s < k ? pair_of[(uint64_t)t * k + s] : 0;
+__global__ __launch_bounds__(64) void k_combine(const float* __restrict__ y,
+                                                const int* __restrict__ pair_of,
+                                                const int32_t* __restrict__ topk_idx,
+                                                const float* __restrict__ topk_w, int k, int n,
+                                                const float* __restrict__ resid,
+                                                float* __restrict__ out,
+                                                float* __restrict__ out2) {
+  // one wave: lane s < k reads slot s, finds its rank among the token's
+  // experts (distinct ids) and files its pair and weight under that rank
+  __shared__ int ps[16];
+  __shared__ float ws[16];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const bool in = lane < k;
+  const int id = in ? topk_idx[(uint64_t)t * k + lane] : 0x7FFFFFFF;
+  const float wt = in ? topk_w[(uint64_t)t * k + lane] : 0.0f;
+  const int pr = in ? pair_of[(uint64_t)t * k + lane] : 0;
+  int rank = 0;
+  for (int q = 0; q < k; ++q) rank += __shfl(id, q, 64) < id ? 1 : 0;
+  if (in) {
+    ps[rank] = pr;
+    ws[rank] = wt;
   }
-#pragma unroll
-  for (int s = 0; s < 16; ++s) {
-    int r = 0;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) r += ids[q] < ids[s] ? 1 : 0;
-    rank[s] = r;
-  }
-  // the slots in ascending expert order, once for all columns
-  int ps[16];
-  float ws[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    ps[r] = 0;
-    ws[r] = 0.0f;
-#pragma unroll
-    for (int s = 0; s < 16; ++s)
-      if (rank[s] == r) {
-        ps[r] = pr[s];
-        ws[r] = wt[s];
-      }
-  }
-  // one float4 of columns per thread (blockIdx.y picks the 4 * blockDim.x-
-  // column range): every slot's load is issued before the first use
-  const int i = 4 * (blockIdx.y * blockDim.x + threadIdx.x);
+  __syncthreads();
+  // one float4 of columns per lane (blockIdx.y picks the 256-column range):
+  // every slot's load is issued before the first use
+  const int i = 4 * (blockIdx.y * 64 + lane);
   if (i >= n) return;
   float4 v[16];
 #pragma unroll
@@ -992,10 +978,11 @@ __global__ __launch_bounds__(kBlock) void k_combine(const float* __restrict__ y,
 #pragma unroll
   for (int r = 0; r < 16; ++r)
     if (r < k) {
-      o.x = __fadd_rn(o.x, __fmul_rn(ws[r], v[r].x));
-      o.y = __fadd_rn(o.y, __fmul_rn(ws[r], v[r].y));
-      o.z = __fadd_rn(o.z, __fmul_rn(ws[r], v[r].z));
-      o.w = __fadd_rn(o.w, __fmul_rn(ws[r], v[r].w));
+      const float w = ws[r];
+      o.x = __fadd_rn(o.x, __fmul_rn(w, v[r].x));
+      o.y = __fadd_rn(o.y, __fmul_rn(w, v[r].y));
+      o.z = __fadd_rn(o.z, __fmul_rn(w, v[r].z));
+      o.w = __fadd_rn(o.w, __fmul_rn(w, v[r].w));
     }
   if (resid) {
     o.x = __fadd_rn(rs.x, o.x);
