@@ -499,7 +499,9 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
 // acc += d cq - dmin cm.  A comes straight from global memory (the pairs'
 // rows are shared by every workgroup of the expert and stay in L2).
 constexpr int kFew = 8;
-constexpr int kFewBelow = 8;   // the few kernels when pairs < kFewBelow * experts
+// the few kernels when pairs < kFewBelow * experts (measured crossover with
+// the 32-pair kernels: between 8 and 12 pairs per expert)
+constexpr int kFewBelow = 10;
 
 __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
