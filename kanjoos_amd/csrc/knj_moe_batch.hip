@@ -52,6 +52,39 @@ __device__ __forceinline__ half8 q4_unpack(uint32_t w0, uint32_t w1, int shift, 
   return half8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
 }
 
+// (w & m) | c in one instruction (with the masks in registers; the
+// compiler splits it when they are literals)
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(m), "v"(c));
+  return r;
+}
+__device__ __forceinline__ half2v cvt_h2(float v) {
+  const _Float16 h = (_Float16)v;
+  return half2v{h, h};
+}
+constexpr uint32_t kNib = 0x000F000Fu;      // low nibbles of bytes 0 and 2
+constexpr uint32_t kF16Base = 0x64006400u;  // f16 1024 in both halves
+
+// The 16 weights of 8 code bytes (words wa, wb): low nibbles sc_lo q and high
+// nibbles sc_hi q, each in perm8 order.  Low: (1024 + q) sc - 1024 sc; high,
+// unshifted: (1024 + 16 q) sc / 16 - 64 sc (every value exact in f16); the
+// byte shift is shared by both halves.  s_lo/n_lo = sc_lo, -1024 sc_lo;
+// s_hi/n_hi = sc_hi / 16, -64 sc_hi.
+__device__ __forceinline__ void q4_unpack2(uint32_t wa, uint32_t wb, half2v s_lo, half2v n_lo,
+                                           half2v s_hi, half2v n_hi, half8& lo, half8& hi) {
+  const uint32_t mlo = kNib, mhi = kNib << 4, sa = wa >> 8, sb = wb >> 8;
+  auto cv = [&](uint32_t w, uint32_t m, half2v sc, half2v nc) {
+    return __builtin_elementwise_fma(as_h2(and_or(w, m, kF16Base)), sc, nc);
+  };
+  const half2v l0 = cv(wa, mlo, s_lo, n_lo), l1 = cv(sa, mlo, s_lo, n_lo);
+  const half2v l2 = cv(wb, mlo, s_lo, n_lo), l3 = cv(sb, mlo, s_lo, n_lo);
+  const half2v h0 = cv(wa, mhi, s_hi, n_hi), h1 = cv(sa, mhi, s_hi, n_hi);
+  const half2v h2 = cv(wb, mhi, s_hi, n_hi), h3 = cv(sb, mhi, s_hi, n_hi);
+  lo = half8{l0.x, l0.y, l1.x, l1.y, l2.x, l2.y, l3.x, l3.y};
+  hi = half8{h0.x, h0.y, h1.x, h1.y, h2.x, h2.y, h3.x, h3.y};
+}
+
 __device__ __forceinline__ half8 ld_h8(const _Float16* p) {
   return __builtin_bit_cast(half8, *reinterpret_cast<const uint4*>(p));
 }
@@ -310,7 +343,7 @@ struct GroupArgs {
 // (double-buffered LDS, one barrier per super-block).  Per code group: 8 steps
 // per matrix (hi/lo x and the two nibble sub-blocks x 2); one min-term step
 // per matrix per super-block.
-constexpr int kQStride = 33;                   // uint4 per 8-group row of 32 pairs (+1 pad)
+constexpr int kQStride = 32;                   // uint4 per 8-group row of 32 pairs
 constexpr int kPart = 32 * kQStride;           // uint4 per hi (or lo) part of a super-block
 constexpr int kBuf = 2 * kPart + 64;           // + the sums (hi 32, lo 32)
 constexpr size_t kGroupLds = 2 * kBuf * 16;    // double-buffered bytes
@@ -319,8 +352,15 @@ struct WBlock {
   uint4 h, c[4];
 };
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+
+// s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
+// memory operations are outstanding and does not wait on the other counters
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
 template <bool GATEUP>
-__global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_group_q4k(GroupArgs a) {
   extern __shared__ uint4 lds[];
   // grouped: work item blockIdx.y of the list; dense (no offsets): the
   // m rows are one expert, tile blockIdx.y
@@ -346,20 +386,21 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
   const uint64_t slab = rb * (uint64_t)a.n_out;
   const uint8_t* wr0 = a.w0 + (uint64_t)e * slab + (uint64_t)row * rb;
   const uint8_t* wr1 = GATEUP ? a.w1 + (uint64_t)e * slab + (uint64_t)row * rb : wr0;
-  // staging: thread t copies uint4 idx = t + 256 u (u < 8) of the hi/lo parts
-  // and, for t < 64, one sums uint4
-  auto a_src = [&](int sb, int u) -> const uint4* {
-    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
-    const _Float16* base = part ? a.al : a.ah;
-    return reinterpret_cast<const uint4*>(base + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8);
-  };
-  auto a_dst = [&](int buf, int u) -> uint4* {
-    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
-    return lds + buf * kBuf + part * kPart + q * kQStride + jj;
-  };
-  auto s_src = [&](int sb) -> const uint4* {  // threads >= 64 read a copy they do not store
-    const _Float16* base = ((t >> 5) & 1) ? a.sl : a.sh;
-    return reinterpret_cast<const uint4*>(base + ((uint64_t)sb * P + p0 + min(t & 31, cnt - 1)) * 8);
+  // staging by LDS DMA (no registers): wave w's instruction u fills entries
+  // e = (8 w + u) 64 + lane of the buffer's hi/lo parts ([part][8-group q]
+  // [pair]); wave 0 also fills the 64 sums entries (hi 32, lo 32)
+  auto stage = [&](int sb, int buf) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e0 = (8 * wave + u) * 64, e = e0 + lane;
+      const int part = e >> 10, r = e & 1023, q = r >> 5, jj = r & 31;
+      const _Float16* src = (part ? a.al : a.ah) + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8;
+      __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(lds + buf * kBuf + e0), 16, 0, 0);
+    }
+    if (wave == 0) {
+      const _Float16* src = ((lane >> 5) ? a.sl : a.sh) + ((uint64_t)sb * P + p0 + min(lane & 31, cnt - 1)) * 8;
+      __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(lds + buf * kBuf + 2 * kPart), 16, 0, 0);
+    }
   };
   auto w_load = [&](const uint8_t* wr, int sb, WBlock& w) {
     const uint8_t* b = wr + (uint64_t)sb * KNJ_Q4K_BLOCK;
@@ -367,53 +408,59 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) w.c[g] = *reinterpret_cast<const uint4*>(b + KNJ_Q4K_QS + 32 * g + 16 * kh);
   };
-  // (the staging registers are loaded and stored on every iteration, without
-  // branches: an array live across divergent code is placed in scratch)
-  uint4 st[8], ss;
   WBlock w0c, w1c, w0n, w1n;
   // prologue: the first super-block of the range
-#pragma unroll
-  for (int u = 0; u < 8; ++u) st[u] = *a_src(sbb, u);
-  ss = *s_src(sbb);
+  stage(sbb, 0);
   w_load(wr0, sbb, w0c);
   if constexpr (GATEUP) w_load(wr1, sbb, w1c);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) *a_dst(0, u) = st[u];
-  if (t < 64) lds[2 * kPart + t] = ss;
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   f32x16 acc0 = {}, acc1 = {};
   for (int sb = sbb; sb < nsb; ++sb) {
     const int buf = (sb - sbb) & 1;
     const int nx = min(sb + 1, nsb - 1);  // the last iteration reloads its own block, unused
-#pragma unroll
-    for (int u = 0; u < 8; ++u) st[u] = *a_src(nx, u);
-    ss = *s_src(nx);
+    const bool more = sb + 1 < nsb;
+    // every load of the next super-block is issued before this one's
+    // arithmetic, the staging first: the memory counter is in order, so the
+    // wait for the staging at the end does not wait for the weights
+    if (more) stage(nx, buf ^ 1);
     w_load(wr0, nx, w0n);
     if constexpr (GATEUP) w_load(wr1, nx, w1n);
+    __builtin_amdgcn_sched_barrier(0);
     const uint4* L = lds + buf * kBuf;
     const half8 am = __builtin_bit_cast(half8, L[2 * kPart + kh * 32 + j]);
     // scales and mins of this lane's row, and the min-term step
-    auto prep = [&](const uint4& h, half2v* sc2, half2v* nc2, f32x16& cm) {
+    // the mins of this lane's row and the min-term step; the scales are
+    // decoded per code group below
+    auto mins = [&](const uint4& h) {
       half8 bm;
 #pragma unroll
       for (int s2 = 0; s2 < 8; ++s2) {
         uint32_t sc, mn;
         q4k_scale_min(h.y, h.z, h.w, s2, sc, mn);
-        const _Float16 f = (_Float16)(float)sc;
-        const _Float16 nf = (_Float16)(-1024.0f * (float)sc);
-        sc2[s2] = half2v{f, f};
-        nc2[s2] = half2v{nf, nf};
         bm[s2] = (_Float16)(float)mn;
       }
-      cm = mfma32(am, bm, f32x16{});
+      return mfma32(am, bm, f32x16{});
     };
-    half2v sc0[8], nc0[8], sc1[8], nc1[8];
-    f32x16 cm0, cm1 = {};
-    prep(w0c.h, sc0, nc0, cm0);
-    if constexpr (GATEUP) prep(w1c.h, sc1, nc1, cm1);
+    auto scales = [&](const uint4& h, int g, half2v& sl, half2v& nl, half2v& sh, half2v& nh) {
+      uint32_t s0, s1, mn;
+      q4k_scale_min(h.y, h.z, h.w, 2 * g, s0, mn);
+      q4k_scale_min(h.y, h.z, h.w, 2 * g + 1, s1, mn);
+      const float f0 = (float)s0, f1 = (float)s1;
+      sl = cvt_h2(f0);
+      nl = cvt_h2(-1024.0f * f0);
+      sh = cvt_h2(0.0625f * f1);
+      nh = cvt_h2(-64.0f * f1);
+    };
+    const f32x16 cm0 = mins(w0c.h);
+    f32x16 cm1 = {};
+    if constexpr (GATEUP) cm1 = mins(w1c.h);
     f32x16 cqa = {}, cqb = {};  // gate (or even groups), up (or odd groups)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
+      half2v sl0, nl0, sh0, nh0, sl1, nl1, sh1, nh1;
+      scales(w0c.h, g, sl0, nl0, sh0, nh0);
+      if constexpr (GATEUP) scales(w1c.h, g, sl1, nl1, sh1, nh1);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const int q = 8 * g + 2 * kh + kk;
@@ -422,16 +469,16 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
         const half8 xh1 = __builtin_bit_cast(half8, L[(q + 4) * kQStride + j]);
         const half8 xl1 = __builtin_bit_cast(half8, L[kPart + (q + 4) * kQStride + j]);
         const uint32_t w0a = kk ? w0c.c[g].z : w0c.c[g].x, w0b = kk ? w0c.c[g].w : w0c.c[g].y;
-        const half8 blo = q4_unpack(w0a, w0b, 0, sc0[2 * g], nc0[2 * g]);
-        const half8 bhi = q4_unpack(w0a, w0b, 4, sc0[2 * g + 1], nc0[2 * g + 1]);
+        half8 blo, bhi;
+        q4_unpack2(w0a, w0b, sl0, nl0, sh0, nh0, blo, bhi);
         if constexpr (GATEUP) {
           cqa = mfma32(xh0, blo, cqa);
           cqa = mfma32(xl0, blo, cqa);
           cqa = mfma32(xh1, bhi, cqa);
           cqa = mfma32(xl1, bhi, cqa);
           const uint32_t w1a = kk ? w1c.c[g].z : w1c.c[g].x, w1b = kk ? w1c.c[g].w : w1c.c[g].y;
-          const half8 ulo = q4_unpack(w1a, w1b, 0, sc1[2 * g], nc1[2 * g]);
-          const half8 uhi = q4_unpack(w1a, w1b, 4, sc1[2 * g + 1], nc1[2 * g + 1]);
+          half8 ulo, uhi;
+          q4_unpack2(w1a, w1b, sl1, nl1, sh1, nh1, ulo, uhi);
           cqb = mfma32(xh0, ulo, cqb);
           cqb = mfma32(xl0, ulo, cqb);
           cqb = mfma32(xh1, uhi, cqb);
@@ -457,13 +504,14 @@ __global__ __launch_bounds__(kBlock) void k_group_q4k(GroupArgs a) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc0[i] += d0 * (cqa[i] + cqb[i]) - m0 * cm0[i];
     }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) *a_dst(buf ^ 1, u) = st[u];
-    if (t < 64) lds[(buf ^ 1) * kBuf + 2 * kPart + t] = ss;
     w0c = w0n;
     if constexpr (GATEUP) w1c = w1n;
+    // the staging done (at most the weight loads issued after it outstanding)
+    // before the barrier that hands the buffer over
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(GATEUP ? 10 : 5));
     __syncthreads();
   }
+  __builtin_amdgcn_s_waitcnt(0);
   if (!rows_ok || rbase + (lane & 31) >= a.n_out) return;
   // acc[i] = C[token 8*(i/4) + 4*kh + i%4][row]
 #pragma unroll
@@ -507,19 +555,6 @@ __device__ __forceinline__ f32x4 mfma16(half8 a, half8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
-// (w & m) | c in one instruction (with the masks in registers; the
-// compiler splits it when they are literals)
-__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "v"(m), "v"(c));
-  return r;
-}
-__device__ __forceinline__ half2v cvt_h2(float v) {
-  const _Float16 h = (_Float16)v;
-  return half2v{h, h};
-}
-constexpr uint32_t kNib = 0x000F000Fu;      // low nibbles of bytes 0 and 2
-constexpr uint32_t kF16Base = 0x64006400u;  // f16 1024 in both halves
 
 struct FewBlock {
   uint4 h, c0, c1;  // header (d, dmin, scales), the lane's 32 code bytes
