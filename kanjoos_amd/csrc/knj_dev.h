@@ -533,12 +533,23 @@ __device__ __forceinline__ int argmax_index(unsigned long long key) {
 // ties to the lower index, model.cpp:442-451).  Lane q < k returns selection
 // q: its expert and its weight p / sum of the kept p, the sum taken in
 // selection order (model.cpp:452-458).  n_expert <= 256.
+// The same from logits already in registers: lane holds experts lane + 64 j
+// (-inf past n_expert).
+__device__ __forceinline__ void wave_route_lg(const float (&lg)[4], int n_expert, int k, int& my_idx,
+                                              float& my_w);
+
 __device__ __forceinline__ void wave_route(const float* __restrict__ logits, int n_expert, int k,
                                            int& my_idx, float& my_w) {
   const int lane = threadIdx.x & 63;
   float lg[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) lg[j] = lane + 64 * j < n_expert ? logits[lane + 64 * j] : -INFINITY;
+  wave_route_lg(lg, n_expert, k, my_idx, my_w);
+}
+
+__device__ __forceinline__ void wave_route_lg(const float (&lg)[4], int n_expert, int k, int& my_idx,
+                                              float& my_w) {
+  const int lane = threadIdx.x & 63;
   float mx = fmaxf(fmaxf(lg[0], lg[1]), fmaxf(lg[2], lg[3]));
   mx = group_max<64>(mx);
   float ex[4], s = 0.0f;

@@ -185,26 +185,29 @@ __global__ __launch_bounds__(kBlock) void k_split_tile(const float* __restrict__
 }
 
 // ------------------------------------------------------------------ router
-// logits[t][e] = sum_i hx[t][i] W[e][i] on the f32 matrix cores: workgroup =
-// 16 tokens x 16 experts with kRouterWaves waves, wave w taking the w-th
-// slice of n_embd (n_embd % (16 kRouterWaves) == 0); the partial tiles are
-// added in wave order.  Lane (r, kq) takes the float4 at 16 s + 4 kq of its
-// slice, so a row's four lanes read 64 contiguous bytes, eight float4 of each
-// operand in flight per round, and four accumulation chains (one per float4
-// component) are added at the end.
-constexpr int kRouterWaves = 16;
-__global__ __launch_bounds__(64 * kRouterWaves) void k_router_batch(const float* __restrict__ hx,
-                                                                    const float* __restrict__ w,
-                                                                    int m, int n, int n_expert,
-                                                                    float* __restrict__ logits) {
-  __shared__ float part[kRouterWaves][256];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// logits[t][e] = sum_i hx[t][i] W[e][i] on the f32 matrix cores.  The
+// reduction is cut into 16 slices of n_embd / 16 (n_embd % 256 == 0); tile
+// (16 tokens x 16 experts) x slice-group z (blockIdx.z, kz groups of 16 / kz
+// consecutive slices): one wave per slice, the group's waves added in slice
+// order into out[z][t][e].  With kz = 1 out is the logits; with kz > 1 the
+// routing below adds the kz groups in order, so the sum is the same
+// sequence of additions either way.  Lane (r, kq) takes the float4 at
+// 16 s + 4 kq of its slice, so a row's four lanes read 64 contiguous bytes,
+// eight float4 of each operand in flight per round, and four accumulation
+// chains (one per float4 component) are added at the end.
+constexpr int kRouterSlices = 16;
+__global__ __launch_bounds__(64 * kRouterSlices) void k_router_batch(const float* __restrict__ hx,
+                                                                     const float* __restrict__ w,
+                                                                     int m, int n, int n_expert,
+                                                                     float* __restrict__ out) {
+  __shared__ float part[kRouterSlices][256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
   const int r = lane & 15, kq = lane >> 4;
   const int t0 = blockIdx.x * 16, e0 = blockIdx.y * 16;
   const int tok = min(t0 + r, m - 1), ex = min(e0 + r, n_expert - 1);
-  const int q = n / kRouterWaves;
-  const float* ap = hx + (uint64_t)tok * n + wave * q + 4 * kq;
-  const float* bp = w + (uint64_t)ex * n + wave * q + 4 * kq;
+  const int q = n / kRouterSlices, slice = blockIdx.z * W + wave;
+  const float* ap = hx + (uint64_t)tok * n + slice * q + 4 * kq;
+  const float* bp = w + (uint64_t)ex * n + slice * q + 4 * kq;
   f32x4 c0 = {0.0f, 0.0f, 0.0f, 0.0f}, c1 = c0, c2 = c0, c3 = c0;
   for (int s = 0; s < q; s += 128) {
     float4 a[8], b[8];
@@ -226,26 +229,57 @@ __global__ __launch_bounds__(64 * kRouterWaves) void k_router_batch(const float*
 #pragma unroll
   for (int i = 0; i < 4; ++i) part[wave][(4 * kq + i) * 16 + r] = (c0[i] + c1[i]) + (c2[i] + c3[i]);
   __syncthreads();
-  if (threadIdx.x < 256) {
-    const int tt = threadIdx.x >> 4, ee = threadIdx.x & 15;
+  for (int i = threadIdx.x; i < 256; i += blockDim.x) {  // the 16 x 16 tile
+    const int tt = i >> 4, ee = i & 15;
     if (t0 + tt < m && e0 + ee < n_expert) {
-      float v = part[0][threadIdx.x];
-      for (int ww = 1; ww < kRouterWaves; ++ww) v += part[ww][threadIdx.x];
-      logits[(uint64_t)(t0 + tt) * n_expert + e0 + ee] = v;
+      float v = part[0][i];
+      for (int ww = 1; ww < W; ++ww) v += part[ww][i];
+      out[((uint64_t)blockIdx.z * m + t0 + tt) * n_expert + e0 + ee] = v;
     }
   }
 }
 
-// Softmax + top-k of every token: one wave per token.
-__global__ __launch_bounds__(kBlock) void k_route_batch(const float* __restrict__ logits, int m,
-                                                        int n_expert, int k,
+// Slice groups of the router: enough workgroups to spread its loads over
+// the chip at decode batch sizes (a power of two <= 16).
+int router_groups(int m, int n_expert) {
+  const int tiles = ((m + 15) / 16) * ((n_expert + 15) / 16);
+  int kz = 1;
+  while (kz < kRouterSlices && tiles * kz * 2 <= 256) kz *= 2;
+  return kz;
+}
+
+// Softmax + top-k of every token: one wave per token.  With kz > 1 the
+// router's slice groups are added first, in order, and written as the logits.
+__global__ __launch_bounds__(kBlock) void k_route_batch(const float* __restrict__ part, int kz,
+                                                        int m, int n_expert, int k,
+                                                        float* __restrict__ logits,
                                                         int32_t* __restrict__ topk_idx,
                                                         float* __restrict__ topk_w) {
   const int t = blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (t >= m) return;
+  // every group's value is loaded before the first addition
+  float pv[4][kRouterSlices];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = min(lane + 64 * j, n_expert - 1);
+#pragma unroll
+    for (int z = 0; z < kRouterSlices; ++z)
+      pv[j][z] = z < kz ? part[((uint64_t)z * m + t) * n_expert + e] : 0.0f;
+  }
+  float lg[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int e = lane + 64 * j;
+    float v = pv[j][0];
+#pragma unroll
+    for (int z = 1; z < kRouterSlices; ++z)
+      if (z < kz) v += pv[j][z];
+    if (e < n_expert && kz > 1) logits[(uint64_t)t * n_expert + e] = v;
+    lg[j] = e < n_expert ? v : -INFINITY;
+  }
   int idx;
   float wt;
-  wave_route(logits + (uint64_t)t * n_expert, n_expert, k, idx, wt);
+  wave_route_lg(lg, n_expert, k, idx, wt);
   if (lane < k) {
     topk_idx[(uint64_t)t * k + lane] = idx;
     topk_w[(uint64_t)t * k + lane] = wt;
@@ -1048,6 +1082,8 @@ uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int 
   add(P * F * 2); add(P * F * 2);       // act hi/lo
   add(P * F / 16); add(P * F / 16);     // act sums hi/lo
   add(P * H * 4);                       // y
+  const int kz = router_groups(m, n_expert);
+  if (kz > 1) add((uint64_t)kz * m * n_expert * 4);  // router slice-group sums
   return b;
 }
 
@@ -1114,16 +1150,18 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   _Float16* sah = (_Float16*)take(P * F / 16);
   _Float16* sal = (_Float16*)take(P * F / 16);
   float* y = (float*)take(P * H * 4);
+  const int kz = router_groups(m, E);
+  float* rpart = kz > 1 ? (float*)take((uint64_t)kz * m * E * 4) : a.logits;
 
   const float* xin = a.x;
   if (a.norm_w) {
     KNJ_LAUNCH(k_norm_rows, dim3(m), dim3(kBlock), 0, s, a.x, a.norm_w, a.eps, H, hx);
     xin = hx;
   }
-  KNJ_LAUNCH(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16), dim3(64 * kRouterWaves), 0, s, xin,
-                     a.router_w, m, H, E, a.logits);
-  KNJ_LAUNCH(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, a.logits, m, E, K,
-                     a.topk_idx, a.topk_w);
+  KNJ_LAUNCH(k_router_batch, dim3((m + 15) / 16, (E + 15) / 16, kz), dim3(64 * kRouterSlices / kz), 0,
+             s, xin, a.router_w, m, H, E, rpart);
+  KNJ_LAUNCH(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, rpart, kz, m, E, K, a.logits,
+             a.topk_idx, a.topk_w);
   KNJ_LAUNCH(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
                      pair_of, items, n_items, tile);
   KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), H / 256), dim3(kBlock), 0, s, xin,
