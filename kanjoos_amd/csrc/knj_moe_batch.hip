@@ -365,6 +365,10 @@ struct GroupArgs {
   int ksplit = 1;
   float* partial = nullptr;
   int tile = kTok;          // pairs per work item of the list (<= kTok)
+  // gate/up of the few-pair kernel with 32 rows per workgroup: the output in
+  // k_split_tile's layout (f16 high parts, remainders, per-32 sums) instead
+  // of f32 rows, when oh is set
+  _Float16 *oh = nullptr, *ol = nullptr, *osh = nullptr, *osl = nullptr;
 };
 
 // Workgroup = one tile of kTok pairs of one expert x kRowsWG weight rows; wave
@@ -657,10 +661,12 @@ __device__ __forceinline__ void few_superblock(const FewBlock& b, const half8 (&
 // wave) and issues every load of them before any arithmetic, so a workgroup
 // asks for whole rows (all super-blocks) of its tiles at once.  The waves'
 // partial tiles meet in LDS and are added in wave order.
-template <bool GATEUP, int FT, int NSBW>
+template <bool GATEUP, int FT, int NSBW, bool SPLIT = false>
 __global__ __launch_bounds__(256) void k_group_fewk(GroupArgs a) {
+  static_assert(!SPLIT || (GATEUP && FT == 2), "split output: gate/up over 32 rows");
   constexpr int NM = GATEUP ? 2 : 1;
   __shared__ f32x4 part[4][NM * FT][64];
+  __shared__ float vs[SPLIT ? 32 : 1][kFew];  // the workgroup's outputs (split form)
   const int item = blockIdx.y;
   if (item >= *a.n_items) return;  // uniform over the workgroup
   const int2 it = a.items[item];
@@ -750,8 +756,46 @@ __global__ __launch_bounds__(256) void k_group_fewk(GroupArgs a) {
         const float u = s[NM - 1][2 * h] + s[NM - 1][2 * h + 1];
         v = (v / (1.0f + expf(-v))) * u;
       }
-      const uint64_t o = (uint64_t)(p0 + pj) * a.n_out + row;
-      a.out[o] = a.resid ? a.resid[o] + v : v;
+      if (SPLIT) {
+        vs[16 * f + col][pj] = v;
+      } else {
+        const uint64_t o = (uint64_t)(p0 + pj) * a.n_out + row;
+        a.out[o] = a.resid ? a.resid[o] + v : v;
+      }
+    }
+  }
+  if constexpr (SPLIT) {
+    // the 32 rows [rbase, rbase + 32) of every pair in k_split_tile's layout:
+    // thread (pair p, 8-group g) the group's high parts and remainders in
+    // perm8 order; the 32-row sum, split the same way, per pair
+    __syncthreads();
+    const int P = a.P, t = threadIdx.x;
+    if (t < 32) {
+      const int pp = t & 7, g = t >> 3;
+      if (pp < cnt) {
+        half8 h, l;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+          const float x = vs[8 * g + perm8(jj)][pp];
+          h[jj] = (_Float16)x;
+          l[jj] = (_Float16)(x - (float)h[jj]);
+        }
+        const uint64_t o = ((uint64_t)(rbase / 8 + g) * P + p0 + pp) * 8;
+        *reinterpret_cast<half8*>(a.oh + o) = h;
+        *reinterpret_cast<half8*>(a.ol + o) = l;
+      }
+    } else if (t < 40) {
+      const int pp = t - 32;
+      if (pp < cnt) {
+        float sum = 0.0f;
+#pragma unroll
+        for (int r = 0; r < 32; ++r) sum += vs[r][pp];
+        const _Float16 sh = (_Float16)sum;
+        const int b = rbase / 32;
+        const uint64_t o = ((uint64_t)(b / 8) * P + p0 + pp) * 8 + b % 8;
+        a.osh[o] = sh;
+        a.osl[o] = (_Float16)(sum - (float)sh);
+      }
     }
   }
 }
@@ -1111,6 +1155,15 @@ hipError_t launch_fewk(const GroupArgs& g, int max_items, int ft, hipStream_t s)
   const dim3 grid((g.n_out + 16 * ft - 1) / (16 * ft), max_items), block(64 * ks);
 #define KNJ_FEWK(FT, NW) \
   if (ft == FT && nw <= NW) { KNJ_LAUNCH((k_group_fewk<GATEUP, FT, NW>), grid, block, 0, s, g); return hipGetLastError(); }
+  if constexpr (GATEUP) {
+    if (g.oh) {  // the split output (32 rows per workgroup)
+      if (ft != 2 || g.n_out % 32) return hipErrorInvalidValue;
+      if (nw <= 1) { KNJ_LAUNCH((k_group_fewk<GATEUP, 2, 1, true>), grid, block, 0, s, g); return hipGetLastError(); }
+      if (nw <= 2) { KNJ_LAUNCH((k_group_fewk<GATEUP, 2, 2, true>), grid, block, 0, s, g); return hipGetLastError(); }
+      if (nw <= 4) { KNJ_LAUNCH((k_group_fewk<GATEUP, 2, 4, true>), grid, block, 0, s, g); return hipGetLastError(); }
+      return hipErrorInvalidValue;
+    }
+  }
   KNJ_FEWK(2, 1) KNJ_FEWK(2, 2) KNJ_FEWK(2, 4) KNJ_FEWK(4, 1)
 #undef KNJ_FEWK
   return hipErrorInvalidValue;
@@ -1171,12 +1224,18 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   // (measured at 32 sequences: 32 rows per workgroup for gate/up, whose
   // super-blocks fill two per wave; 64 for down, one per wave)
   if (few) {
+    // SwiGLU written straight in the down product's operand layout
+    gu.oh = ah;
+    gu.ol = al;
+    gu.osh = sah;
+    gu.osl = sal;
     if (hipError_t e = launch_fewk<true>(gu, max_items, 2, s)) return e;
-  } else
+  } else {
     KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                kGroupLds, s, gu);
-  KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), F / 256), dim3(kBlock), 0, s, act,
-             nullptr, F, (int)P, ah, al, sah, sal);
+    KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), F / 256), dim3(kBlock), 0, s, act,
+               nullptr, F, (int)P, ah, al, sah, sal);
+  }
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
   dn.tile = tile;
   if (few && a.type_down == KNJ_TYPE_Q4_K) {
