@@ -358,7 +358,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
 template <int D>
 __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) {
   constexpr int NP = kBlock / 32;  // parts
-  constexpr int PMAX = 16;         // splits per part (n_split <= 128)
+  constexpr int PMAX = 32;         // splits per part (n_split <= 256)
   __shared__ float pm[NP], pl[NP];
   __shared__ float pacc[NP][32];
   const int h = blockIdx.x / (D / 32), d0 = 32 * (blockIdx.x % (D / 32));
@@ -755,16 +755,21 @@ __global__ __launch_bounds__(kBlock) void k_prefill_merge(PrefillAttnArgs a, int
 
 int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
 
+// splits of one head: one 64-slot chunk per workgroup up to 256 chunks (the
+// merge folds 8 parts x 32 splits; measured at 32K slots, 256 splits of 2-3
+// chunks beat 128 of 4-5 by 2% per token)
+constexpr int kMaxSplit = 256;
+
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
-  // one 64-slot chunk per workgroup up to 128 chunks; beyond, several chunks
-  // per workgroup so the merge sees at most 128 partials per head
+  // one 64-slot chunk per workgroup up to kMaxSplit chunks; beyond, several
+  // chunks per workgroup so the merge sees at most kMaxSplit partials per head
   const int chunks = attn_splits(a.n_ctx);
   // several sequences fill the chip with their own splits: two chunks per
   // workgroup there (measured 2% faster at 32 sequences x 2048 slots; one
   // chunk is faster at batch 1)
-  const int cpw = std::max((chunks + 127) / 128, a.n_seq > 1 ? 2 : 1);
+  const int cpw = std::max((chunks + kMaxSplit - 1) / kMaxSplit, a.n_seq > 1 ? 2 : 1);
   const int n_split = (chunks + cpw - 1) / cpw;
-  if (n_split > 128) return hipErrorInvalidValue;  // the merge folds at most 8 x 16 splits
+  if (n_split > kMaxSplit) return hipErrorInvalidValue;  // the merge folds at most 8 x 32 splits
   const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
     KNJ_LAUNCH(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
