@@ -685,12 +685,12 @@ __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
   __shared__ float acts[KMAX * 1024];
   __shared__ float s8[KMAX * 1024 / 8];
   __shared__ float dots[KMAX][kDownRows];
-  float4 v[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  // (named registers: an array here was placed in scratch memory)
+  auto act4 = [&](int j) {
     const int i = 4 * (t + 512 * j);
-    v[j] = *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
-  }
+    return *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
+  };
+  const float4 v0 = act4(0), v1 = act4(1), v2 = act4(2), v3 = act4(3);
   int ids[KMAX];
   float wts[KMAX];
 #pragma unroll
@@ -711,11 +711,14 @@ __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
     qu[it] = q6_unit_load(ex + (uint64_t)row * rb, hf, o);
   }
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  auto stage4 = [&](int j, const float4& v) {
     const int i = 4 * (t + 512 * j);
-    if (i < n) *reinterpret_cast<float4*>(acts + i) = v[j];
-  }
+    if (i < n) *reinterpret_cast<float4*>(acts + i) = v;
+  };
+  stage4(0, v0);
+  stage4(1, v1);
+  stage4(2, v2);
+  stage4(3, v3);
   __syncthreads();
   for (int g = t; 8 * g < n; g += 512) {
     const float4 x0 = *reinterpret_cast<const float4*>(acts + 8 * g);
