@@ -355,10 +355,9 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
 // load waits on the position.  Thread (dim j, part p) folds the splits of part
 // p (8 contiguous ranges, in order); every load of a thread is issued before
 // the first use, and the parts are added in order.
-template <int D>
+template <int D, int PMAX>  // PMAX splits per part: n_split <= 8 PMAX
 __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) {
   constexpr int NP = kBlock / 32;  // parts
-  constexpr int PMAX = 32;         // splits per part (n_split <= 256)
   __shared__ float pm[NP], pl[NP];
   __shared__ float pacc[NP][32];
   const int h = blockIdx.x / (D / 32), d0 = 32 * (blockIdx.x % (D / 32));
@@ -773,14 +772,18 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
     KNJ_LAUNCH(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    if (z == 1)
-      KNJ_LAUNCH(k_attn_merge<128>, dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+    if (z == 1 && n_split <= 128)  // (the loads a part holds cost at short contexts)
+      KNJ_LAUNCH((k_attn_merge<128, 16>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+    else if (z == 1)
+      KNJ_LAUNCH((k_attn_merge<128, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
     KNJ_LAUNCH(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    if (z == 1)
-      KNJ_LAUNCH(k_attn_merge<64>, dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+    if (z == 1 && n_split <= 128)
+      KNJ_LAUNCH((k_attn_merge<64, 16>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+    else if (z == 1)
+      KNJ_LAUNCH((k_attn_merge<64, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
