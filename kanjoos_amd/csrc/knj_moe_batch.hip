@@ -839,14 +839,15 @@ __global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
   const uint64_t P = (uint64_t)a.P;
   const uint64_t rb = (uint64_t)nsb * KNJ_Q6K_BLOCK;
   const uint8_t* wr = a.w0 + (uint64_t)e * rb * (uint64_t)a.n_out + (uint64_t)row * rb;
-  auto a_src = [&](int sb, int u) -> const uint4* {
-    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
-    const _Float16* base = part ? a.al : a.ah;
-    return reinterpret_cast<const uint4*>(base + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8);
-  };
-  auto a_dst = [&](int buf, int u) -> uint4* {
-    const int idx = t + kBlock * u, part = idx >> 10, r = idx & 1023, q = r >> 5, jj = r & 31;
-    return lds + buf * kBuf + part * kPart + q * kQStride + jj;
+  // staging by LDS DMA, as in k_group_q4k (no sums: no min term here)
+  auto stage = [&](int sb, int buf) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e0 = (8 * wave + u) * 64, ee = e0 + lane;
+      const int part = ee >> 10, r = ee & 1023, q = r >> 5, jj = r & 31;
+      const _Float16* src = (part ? a.al : a.ah) + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8;
+      __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(lds + buf * kBuf + e0), 16, 0, 0);
+    }
   };
   auto w_load = [&](int sb, Q6WBlock& w) {
     const uint8_t* b = wr + (uint64_t)sb * KNJ_Q6K_BLOCK;
@@ -863,13 +864,10 @@ __global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
     ld8_u2(b + KNJ_Q6K_SC + 8, w.sc[2], w.sc[3]);
     w.d = *reinterpret_cast<const uint16_t*>(b + KNJ_Q6K_D);
   };
-  uint4 st[8];
   Q6WBlock wc, wn;
-#pragma unroll
-  for (int u = 0; u < 8; ++u) st[u] = *a_src(0, u);
+  stage(0, 0);
   w_load(0, wc);
-#pragma unroll
-  for (int u = 0; u < 8; ++u) *a_dst(0, u) = st[u];
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   f32x16 acc = {};
   const half2v bias = half2v{(_Float16)1056.0f, (_Float16)1056.0f};  // 1024 + 32
@@ -877,9 +875,10 @@ __global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
   for (int sb = 0; sb < nsb; ++sb) {
     const int buf = sb & 1;
     const int nx = min(sb + 1, nsb - 1);  // the last iteration reloads its own block, unused
-#pragma unroll
-    for (int u = 0; u < 8; ++u) st[u] = *a_src(nx, u);
+    // the staging first, then the weights, all before this block's arithmetic
+    if (sb + 1 < nsb) stage(nx, buf ^ 1);
     w_load(nx, wn);
+    __builtin_amdgcn_sched_barrier(0);
     const uint4* L = lds + buf * kBuf;
     const float d = h2f(wc.d);
 #pragma unroll
@@ -903,9 +902,8 @@ __global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
 #pragma unroll
           for (int i = 0; i < 16; ++i) acc[i] += sg * c[i];
         }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) *a_dst(buf ^ 1, u) = st[u];
     wc = wn;
+    __builtin_amdgcn_s_waitcnt(0);  // the staging landed before the barrier hands it over
     __syncthreads();
   }
   if (!rows_ok || rbase + (lane & 31) >= a.n_out) return;
