@@ -514,7 +514,11 @@ def _attn_ref(q, k, v, qn, kn, eps, base, pos, n_head, n_kv, D, kc, vc):
 
 @pytest.mark.parametrize("n_head,n_kv,D,pos,n_ctx", [
     (nh, nkv, d, p, 200) for (nh, nkv, d) in [(32, 4, 128), (16, 2, 64), (12, 4, 128), (8, 8, 64)]
-    for p in [0, 63, 64, 130, 199]] + [(32, 4, 128, 20000, 32768), (32, 4, 128, 32767, 32768)])
+    for p in [0, 63, 64, 130, 199]] + [(32, 4, 128, 20000, 32768), (32, 4, 128, 32767, 32768)] +
+    # three 64-slot chunks per workgroup (two in flight), with splits past the
+    # position and one holding it part-way; five chunks per workgroup
+    [(32, 4, 128, 39999, 40000), (32, 4, 128, 160, 40000), (32, 4, 128, 30100, 40000),
+     (16, 2, 64, 39000, 40000), (32, 4, 128, 69999, 70000)])
 def test_attention_step(device, n_head, n_kv, D, pos, n_ctx):
     """knj_attention_step against a float64 reference: cache append and output
     (the last two cases are config 5's 32K context)."""
