@@ -292,18 +292,19 @@ __global__ __launch_bounds__(kBlock) void k_route_batch(const float* __restrict_
 // pair_of[t*k + s] the pair of token t's slot s; items the (expert, first
 // pair) of every tile of `tile` pairs.  The order of pairs within an expert does
 // not change any result: each pair's outputs depend only on its own row.
-__global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ topk_idx, int m,
+constexpr int kBucketThreads = 1024;  // (the counting and scattering atomics spread wider)
+__global__ __launch_bounds__(kBucketThreads) void k_bucket(const int32_t* __restrict__ topk_idx, int m,
                                                    int k, int n_expert, int* __restrict__ offsets,
                                                    int* __restrict__ pair_tok,
                                                    int* __restrict__ pair_of,
                                                    int2* __restrict__ items,
                                                    int* __restrict__ n_items, int tile) {
   __shared__ int cnt[256], cur[256];
-  __shared__ int wsum[2][kBlock / 64];
+  __shared__ int wsum[2][kBucketThreads / 64];
   const int t = threadIdx.x, P = m * k, lane = t & 63, wave = t >> 6;
   if (t < n_expert) cnt[t] = 0;
   __syncthreads();
-  for (int p = t; p < P; p += kBlock) atomicAdd(&cnt[topk_idx[p]], 1);
+  for (int p = t; p < P; p += kBucketThreads) atomicAdd(&cnt[topk_idx[p]], 1);
   __syncthreads();
   // exclusive prefix sums over the experts (thread t = expert t) of the pair
   // counts and the tile counts: a scan within each wave, then the wave totals
@@ -336,7 +337,7 @@ __global__ __launch_bounds__(kBlock) void k_bucket(const int32_t* __restrict__ t
     }
   }
   __syncthreads();
-  for (int p = t; p < P; p += kBlock) {
+  for (int p = t; p < P; p += kBucketThreads) {
     const int q = atomicAdd(&cur[topk_idx[p]], 1);
     pair_tok[q] = p / k;
     pair_of[p] = q;
@@ -1213,7 +1214,7 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
              s, xin, a.router_w, m, H, E, rpart);
   KNJ_LAUNCH(k_route_batch, dim3((m + 3) / 4), dim3(kBlock), 0, s, rpart, kz, m, E, K, a.logits,
              a.topk_idx, a.topk_w);
-  KNJ_LAUNCH(k_bucket, dim3(1), dim3(kBlock), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
+  KNJ_LAUNCH(k_bucket, dim3(1), dim3(kBucketThreads), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
                      pair_of, items, n_items, tile);
   KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), H / 256), dim3(kBlock), 0, s, xin,
              pair_tok, H, (int)P, xh, xl, sxh, sxl);
