@@ -61,6 +61,10 @@ __device__ __forceinline__ float4 norm_rope4(float4 v, int c, float4 w, float ep
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h16x8 __attribute__((ext_vector_type(8)));
 
+// The 8-weight order of the grouped GEMMs' operands (knj_moe_batch.hip):
+// position j of an 8-group holds element perm8_a(j) (bits 0 and 1 swapped).
+__host__ __device__ constexpr int perm8_a(int j) { return (j & 4) | ((j & 1) << 1) | ((j & 2) >> 1); }
+
 // One 16x16x32 f16 matrix-core step: acc[i] += sum_k A[4*(l/16)+i][k] B[k][l%16]
 // where lane l supplies A[l%16][8*(l/16) + j] and B[8*(l/16) + j][l%16], j < 8.
 __device__ __forceinline__ f32x4 mfma16(h16x8 a, h16x8 b, f32x4 acc) {
@@ -477,10 +481,46 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge_head(AttnArgs a, int n_sp
   // fold the ranges in order: part 0 + part 1 (+ 2 + 3)
   parts[tid] = acc;
   __syncthreads();
+  float res = 0.0f;
   if (tid < D) {
     float o = parts[tid];
     for (int q = 1; q < NP; ++q) o += parts[tid + q * D];
-    a.out[z * a.out_stride + (uint64_t)h * D + tid] = o / L;
+    res = o / L;
+    a.out[z * a.out_stride + (uint64_t)h * D + tid] = res;
+  }
+  if (!a.split_hi) return;  // uniform
+  // the row's D columns h D .. h D + D - 1 in k_split_tile's layout, with its
+  // arithmetic: f16 high part and remainder, each 8-group in perm8 order; each
+  // 32-column sum as eight sequential additions per 8-group, the four groups
+  // added pairwise
+  __syncthreads();  // parts[] is read above
+  if (tid < D) fs[tid] = res;
+  __syncthreads();
+  const int P = a.n_seq, c0 = h * D;
+  if (tid < D / 8) {
+    const int g = tid, q = (c0 >> 3) + g;
+    _Float16 hv[8], lv[8];
+    float s8 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = fs[8 * g + perm8_a(j)];
+      hv[j] = (_Float16)x;
+      lv[j] = (_Float16)(x - (float)hv[j]);
+      s8 += fs[8 * g + j];
+    }
+    const uint64_t o = ((uint64_t)q * P + z) * 8;
+    *reinterpret_cast<uint4*>(a.split_hi + o) = *reinterpret_cast<const uint4*>(hv);
+    *reinterpret_cast<uint4*>(a.split_lo + o) = *reinterpret_cast<const uint4*>(lv);
+    parts[g] = s8;
+  }
+  __syncthreads();
+  if (tid < D / 32) {
+    const int b = (c0 >> 5) + tid;
+    const float sum = (parts[4 * tid] + parts[4 * tid + 1]) + (parts[4 * tid + 2] + parts[4 * tid + 3]);
+    const _Float16 sh = (_Float16)sum;
+    const uint64_t o = ((uint64_t)(b >> 3) * P + z) * 8 + (b & 7);
+    a.split_shi[o] = sh;
+    a.split_slo[o] = (_Float16)(sum - (float)sh);
   }
 }
 
@@ -786,9 +826,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH((k_attention<128, true>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     else
       KNJ_LAUNCH((k_attention<128, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    if (z == 1 && n_split <= 128)  // (the loads a part holds cost at short contexts)
+    if (z == 1 && !a.split_hi && n_split <= 128)  // (the loads a part holds cost at short contexts)
       KNJ_LAUNCH((k_attn_merge<128, 16>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
-    else if (z == 1)
+    else if (z == 1 && !a.split_hi)
       KNJ_LAUNCH((k_attn_merge<128, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
@@ -797,9 +837,9 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH((k_attention<64, true>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     else
       KNJ_LAUNCH((k_attention<64, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    if (z == 1 && n_split <= 128)
+    if (z == 1 && !a.split_hi && n_split <= 128)
       KNJ_LAUNCH((k_attn_merge<64, 16>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
-    else if (z == 1)
+    else if (z == 1 && !a.split_hi)
       KNJ_LAUNCH((k_attn_merge<64, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);

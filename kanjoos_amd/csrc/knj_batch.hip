@@ -79,6 +79,8 @@ struct knj_batch {
   unsigned long long* keys = nullptr;  // argmax partial keys
   uint16_t *kv_k = nullptr, *kv_v = nullptr;
   void* scratch = nullptr;
+  _Float16* osplit[4] = {};  // the attention output in the O product's operand layout
+  _Float16* qsplit[4] = {};  // the attn-normalised rows in the QKV product's operand layout
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
   bool use_graph = true;
@@ -108,11 +110,24 @@ int enqueue_batch_step(knj_batch* b, hipStream_t s) {
                      img + m->off_embd, H, b->tokens, b->dpos, m->rope_cos, m->rope_sin, half, b->x,
                      b->rope);
   KNJ_HIP(hipGetLastError());
+  // layer 0's QKV operand; every later one comes from the previous layer's
+  // combine, and the last combine writes the output-normalised rows
+  const bool fused_norms = H <= 4096 && H % 256 == 0;  // (always, for a valid model)
+  if (fused_norms)
+    KNJ_HIP(launch_norm_split(b->x, reinterpret_cast<const float*>(img + m->lo[0].attn_norm), c.rms_eps,
+                              B, H, nullptr, b->qsplit, s));
   for (int il = 0; il < c.n_layer; ++il) {
     const knj_layer_offsets& lo = m->lo[il];
-    KNJ_HIP(launch_norm_rows(b->x, reinterpret_cast<const float*>(img + lo.attn_norm), c.rms_eps, B,
-                             H, b->hx, s));
-    KNJ_HIP(launch_dense_q4k(img + lo.wqkv, H, QKV, B, b->hx, nullptr, b->qkv, b->scratch, s));
+    if (fused_norms) {
+      const _Float16* pre[4] = {b->qsplit[0], b->qsplit[1], b->qsplit[2], b->qsplit[3]};
+      DenseQ4Extra qx;
+      qx.pre = pre;
+      KNJ_HIP(launch_dense_q4k_ex(img + lo.wqkv, H, QKV, B, nullptr, nullptr, b->qkv, b->scratch, qx, s));
+    } else {
+      KNJ_HIP(launch_norm_rows(b->x, reinterpret_cast<const float*>(img + lo.attn_norm), c.rms_eps, B,
+                               H, b->hx, s));
+      KNJ_HIP(launch_dense_q4k(img + lo.wqkv, H, QKV, B, b->hx, nullptr, b->qkv, b->scratch, s));
+    }
     AttnArgs at{b->qkv, b->qkv + QD, b->qkv + QD + KVD,
                 reinterpret_cast<const float*>(img + lo.q_norm),
                 reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, b->rope, b->rope + half,
@@ -124,9 +139,21 @@ int enqueue_batch_step(knj_batch* b, hipStream_t s) {
     at.kv_stride = kv_seq_elems(b);
     at.out_stride = (uint64_t)QD;
     at.rope_stride = D;
+    // the merge writes the O product's split operand too; the O product's
+    // last launch also writes the ffn-normalised rows the MoE takes
+    at.split_hi = b->osplit[0];
+    at.split_lo = b->osplit[1];
+    at.split_shi = b->osplit[2];
+    at.split_slo = b->osplit[3];
     KNJ_HIP(launch_attention(at, s));
-    KNJ_HIP(launch_dense_q4k(img + lo.wo, QD, H, B, b->ctx, b->x, b->x, b->scratch, s));
-    MoeBatchArgs ma{b->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
+    const _Float16* pre[4] = {b->osplit[0], b->osplit[1], b->osplit[2], b->osplit[3]};
+    DenseQ4Extra ox;
+    ox.pre = pre;
+    ox.norm_w = reinterpret_cast<const float*>(img + lo.ffn_norm);
+    ox.eps = c.rms_eps;
+    ox.norm_out = b->hx;
+    KNJ_HIP(launch_dense_q4k_ex(img + lo.wo, QD, H, B, b->ctx, b->x, b->x, b->scratch, ox, s));
+    MoeBatchArgs ma{b->hx, nullptr, c.rms_eps,
                     reinterpret_cast<const float*>(img + lo.router), img + lo.gate, img + lo.up,
                     img + lo.down, B, H, c.n_ff, c.n_expert, c.n_expert_used, b->x, b->x,
                     b->router_logits + (uint64_t)il * B * c.n_expert,
@@ -134,10 +161,18 @@ int enqueue_batch_step(knj_batch* b, hipStream_t s) {
                     b->topk_w + (uint64_t)il * B * c.n_expert_used};
     ma.hidden_copy = b->hidden + (uint64_t)il * B * H;
     ma.type_down = c.type_down;
+    if (fused_norms) {
+      const bool last = il + 1 == c.n_layer;
+      ma.next_norm_w = reinterpret_cast<const float*>(img + (last ? m->off_onorm : m->lo[il + 1].attn_norm));
+      ma.next_eps = c.rms_eps;
+      ma.next_hx = last ? b->hx : nullptr;
+      ma.next_split = last ? nullptr : b->qsplit;
+    }
     KNJ_HIP(launch_moe_batch(ma, b->scratch, s));
   }
-  KNJ_HIP(launch_norm_rows(b->x, reinterpret_cast<const float*>(img + m->off_onorm), c.rms_eps, B,
-                           H, b->hx, s));
+  if (!fused_norms)
+    KNJ_HIP(launch_norm_rows(b->x, reinterpret_cast<const float*>(img + m->off_onorm), c.rms_eps, B,
+                             H, b->hx, s));
   if (c.type_head == KNJ_TYPE_Q6_K)
     KNJ_HIP(launch_dense_q6k(img + m->off_head, H, c.n_vocab, B, b->hx, b->logits, b->scratch, s));
   else
@@ -250,6 +285,21 @@ int knj_batch_create(knj_model* m, int n_seq, int n_ctx, knj_batch** out) {
                                  dense_scratch_bytes(B, H, QKV), dense_scratch_bytes(B, QD, H),
                                  dense_scratch_bytes(B, H, 0)});
   A(&b->scratch, scr);
+  // [hi | lo | sums hi | sums lo] of B rows x n columns, as split_operand_bytes lays them out
+  auto split_buf = [&](int n, _Float16** sp) {
+    void* os = nullptr;
+    A(&os, split_operand_bytes(B, n));
+    if (!rc) {
+      uint8_t* q = (uint8_t*)os;
+      const uint64_t hb = ((uint64_t)B * n * 2 + 255) & ~255ull, sb = ((uint64_t)B * n / 16 + 255) & ~255ull;
+      sp[0] = (_Float16*)q;
+      sp[1] = (_Float16*)(q + hb);
+      sp[2] = (_Float16*)(q + 2 * hb);
+      sp[3] = (_Float16*)(q + 2 * hb + sb);
+    }
+  };
+  split_buf(QD, b->osplit);
+  split_buf(H, b->qsplit);
   if (!rc && (hipMemset(b->kv_k, 0, kv) != hipSuccess || hipMemset(b->kv_v, 0, kv) != hipSuccess))
     rc = KNJ_E_HIP;
   if (!rc) rc = batch_graph(b);

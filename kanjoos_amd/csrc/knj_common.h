@@ -129,9 +129,20 @@ struct MoeBatchArgs {
   float* topk_w;           // [m][k]
   float* hidden_copy = nullptr;  // optional second destination of out
   int type_down = KNJ_TYPE_Q4_K;  // Q4_K or Q6_K
+  // Optional, the next step's input from the combine's rows: out RMS-normalised
+  // with next_norm_w into next_hx (f32, may be
+  // null) and/or next_split (k_split_tile's layout: hi, lo, sums hi, sums lo)
+  const float* next_norm_w = nullptr;
+  float next_eps = 1e-6f;
+  float* next_hx = nullptr;
+  _Float16* const* next_split = nullptr;
 };
 uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int k);
 hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s);
+// Rows of x RMS-normalised with nw into hx (may be null) and/or split (k_split_tile's
+// layout); n <= 4096, n % 256 == 0.
+hipError_t launch_norm_split(const float* x, const float* nw, float eps, int m, int n, float* hx,
+                             _Float16* const* split, hipStream_t s);
 
 // Dense GEMMs over m rows at once (the batched decode step), on the matrix
 // cores with split-f16 (Q4_K) or split-bf16 (bf16 weights) activations:
@@ -143,6 +154,23 @@ hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, i
                             hipStream_t s);
 hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const float* x,
                             const float* resid, float* out, void* scratch, hipStream_t s);
+// The same with two fusions a batched layer step uses: `pre` (hi, lo, sums hi,
+// sums lo in k_split_tile's layout, or null) is the activation operand already
+// split, so x is not read; with `norm_w`, the rows of out are also written
+// RMS-normalised with norm_w into norm_out (the next product's input), by the
+// launch that adds the reduction ranges when there is one.
+struct DenseQ4Extra {
+  const _Float16* const* pre = nullptr;  // [4]
+  const float* norm_w = nullptr;
+  float eps = 1e-6f;
+  float* norm_out = nullptr;
+};
+hipError_t launch_dense_q4k_ex(const uint8_t* w, int n_in, int n_out, int m, const float* x,
+                               const float* resid, float* out, void* scratch,
+                               const DenseQ4Extra& ex, hipStream_t s);
+// Bytes of the split operand of m rows of n floats (k_split_tile's layout:
+// hi, lo, sums hi, sums lo, each 256-byte aligned).
+uint64_t split_operand_bytes(int m, int n);
 hipError_t launch_dense_bf16(const uint16_t* w, int n_in, int n_out, int m, const float* x,
                              float* out, void* scratch, hipStream_t s);
 // Q6_K (no residual, no reduction split): scratch dense_scratch_bytes(m, n_in, 0).
@@ -177,6 +205,10 @@ struct AttnArgs {
   int n_seq = 1;
   uint64_t qkv_stride = 0, kv_stride = 0, out_stride = 0;
   int rope_stride = 0;
+  // With several sequences: the output also (split_hi set) in k_split_tile's
+  // layout over the n_seq rows of n_head * D columns (hi, lo, sums hi, sums
+  // lo), the next product's operand
+  _Float16 *split_hi = nullptr, *split_lo = nullptr, *split_shi = nullptr, *split_slo = nullptr;
 };
 int attn_splits(int n_ctx);
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s);

@@ -938,6 +938,54 @@ __global__ __launch_bounds__(kBlock) void k_ksum(const float* __restrict__ parti
   *reinterpret_cast<float4*>(out + i4) = r;
 }
 
+// k_ksum and k_norm_rows in one launch, one workgroup per row (n <= 4096,
+// n % 256 == 0): out = resid + the ranges in order (k_ksum's additions), then
+// norm_out = out * scale * w with k_norm_rows's thread mapping and block sum,
+// so both are the bits the two launches give.
+__global__ __launch_bounds__(kBlock) void k_ksum_norm(const float* __restrict__ partial, int ksplit,
+                                                      uint64_t total, int n, const float* resid,
+                                                      float* out, const float* __restrict__ nw,
+                                                      float eps, float* __restrict__ norm_out) {
+  __shared__ float red[8];
+  const uint64_t row = blockIdx.x;
+  float4 r[4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * threadIdx.x + 4 * kBlock * u;
+    if (i < n) {
+      const uint64_t e = row * n + i;
+      float4 v[16];
+#pragma unroll
+      for (int z = 0; z < 16; ++z)
+        if (z < ksplit) v[z] = *reinterpret_cast<const float4*>(partial + (uint64_t)z * total + e);
+      float4 a = resid ? *reinterpret_cast<const float4*>(resid + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int z = 0; z < 16; ++z)
+        if (z < ksplit) {
+          a.x += v[z].x;
+          a.y += v[z].y;
+          a.z += v[z].z;
+          a.w += v[z].w;
+        }
+      *reinterpret_cast<float4*>(out + e) = a;
+      ss += a.x * a.x + a.y * a.y + a.z * a.z + a.w * a.w;
+      r[u] = a;
+    }
+  }
+  ss = block_sum(ss, red);
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * threadIdx.x + 4 * kBlock * u;
+    if (i < n) {
+      const float4 w = *reinterpret_cast<const float4*>(nw + i);
+      *reinterpret_cast<float4*>(norm_out + row * n + i) =
+          make_float4(r[u].x * scale * w.x, r[u].y * scale * w.y, r[u].z * scale * w.z, r[u].w * scale * w.w);
+    }
+  }
+}
+
 // ------------------------------------------------------------------ bf16 weights (LM head)
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
@@ -1108,6 +1156,111 @@ __global__ __launch_bounds__(64) void k_combine(const float* __restrict__ y,
   if (out2) *reinterpret_cast<float4*>(out2 + (uint64_t)t * n + i) = o;
 }
 
+// k_combine over whole rows, then the next step's input from them: one
+// workgroup per token, thread t on the float4 at 4 t + 1024 u (k_norm_rows's
+// mapping).  The weighted sum is k_combine's (ascending expert, the same
+// roundings); with nw, the row's RMS norm as k_norm_rows computes it into hx
+// and/or the split operand as k_split_tile computes it (8-groups in perm8
+// order through LDS, sequential sums per 8-group, pairwise per 32).  k = 0:
+// out = resid (the norm and split of a row alone).
+__global__ __launch_bounds__(kBlock) void k_combine_norm(
+    const float* __restrict__ y, const int* __restrict__ pair_of, const int32_t* __restrict__ topk_idx,
+    const float* __restrict__ topk_w, int k, int n, int P, const float* resid, float* out,
+    float* __restrict__ out2, const float* __restrict__ nw, float eps, float* __restrict__ hx,
+    _Float16* __restrict__ shi, _Float16* __restrict__ slo, _Float16* __restrict__ sshi,
+    _Float16* __restrict__ sslo) {
+  __shared__ int ps[16];
+  __shared__ float ws[16];
+  __shared__ float red[8];
+  __shared__ float row[4096];
+  const int t = blockIdx.x, tid = threadIdx.x;
+  if (tid < 64) {
+    const bool in = tid < k;
+    const int id = in ? topk_idx[(uint64_t)t * k + tid] : 0x7FFFFFFF;
+    const float wt = in ? topk_w[(uint64_t)t * k + tid] : 0.0f;
+    const int pr = in ? pair_of[(uint64_t)t * k + tid] : 0;
+    int rank = 0;
+    for (int q = 0; q < k; ++q) rank += __shfl(id, q, 64) < id ? 1 : 0;
+    if (in) {
+      ps[rank] = pr;
+      ws[rank] = wt;
+    }
+  }
+  __syncthreads();
+  float4 o4[4];
+  float ss = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * tid + 4 * kBlock * u;
+    if (i < n) {
+      float4 v[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (r < k) v[r] = *reinterpret_cast<const float4*>(y + (uint64_t)ps[r] * n + i);
+      const float4 rs = resid ? *reinterpret_cast<const float4*>(resid + (uint64_t)t * n + i)
+                              : make_float4(0.f, 0.f, 0.f, 0.f);
+      float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (r < k) {
+          const float w = ws[r];
+          o.x = __fadd_rn(o.x, __fmul_rn(w, v[r].x));
+          o.y = __fadd_rn(o.y, __fmul_rn(w, v[r].y));
+          o.z = __fadd_rn(o.z, __fmul_rn(w, v[r].z));
+          o.w = __fadd_rn(o.w, __fmul_rn(w, v[r].w));
+        }
+      if (resid) {
+        o.x = __fadd_rn(rs.x, o.x);
+        o.y = __fadd_rn(rs.y, o.y);
+        o.z = __fadd_rn(rs.z, o.z);
+        o.w = __fadd_rn(rs.w, o.w);
+      }
+      *reinterpret_cast<float4*>(out + (uint64_t)t * n + i) = o;
+      if (out2) *reinterpret_cast<float4*>(out2 + (uint64_t)t * n + i) = o;
+      ss += o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+      o4[u] = o;
+    }
+  }
+  if (!nw) return;  // uniform
+  ss = block_sum(ss, red);
+  const float scale = 1.0f / sqrtf(ss / (float)n + eps);
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int i = 4 * tid + 4 * kBlock * u;
+    if (i < n) {
+      const float4 w = *reinterpret_cast<const float4*>(nw + i);
+      const float4 h = make_float4(o4[u].x * scale * w.x, o4[u].y * scale * w.y,
+                                   o4[u].z * scale * w.z, o4[u].w * scale * w.w);
+      if (hx) *reinterpret_cast<float4*>(hx + (uint64_t)t * n + i) = h;
+      *reinterpret_cast<float4*>(row + i) = h;
+    }
+  }
+  if (!shi) return;  // uniform
+  __syncthreads();
+  for (int g = tid; 8 * g < n; g += kBlock) {  // 8-group g of the row
+    half8 hv, lv;
+    float s8 = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float x = row[8 * g + perm8(j)];
+      hv[j] = (_Float16)x;
+      lv[j] = (_Float16)(x - (float)hv[j]);
+      s8 += row[8 * g + j];
+    }
+    const uint64_t o = ((uint64_t)g * P + t) * 8;
+    *reinterpret_cast<half8*>(shi + o) = hv;
+    *reinterpret_cast<half8*>(slo + o) = lv;
+    const float sum = group_sum<4>(s8);  // the four 8-groups of 32-sub-block g / 4
+    if ((g & 3) == 0) {
+      const int b = g >> 2;
+      const _Float16 sv = (_Float16)sum;
+      const uint64_t so = ((uint64_t)(b >> 3) * P + t) * 8 + (b & 7);
+      sshi[so] = sv;
+      sslo[so] = (_Float16)(sum - (float)sv);
+    }
+  }
+}
+
 }  // namespace
 
 uint64_t moe_batch_scratch_bytes(int m, int n_embd, int n_ff, int n_expert, int k) {
@@ -1245,10 +1398,17 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   else
     KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                kGroupLds, s, dn);
-  // one wave per 256 columns of a token: enough workgroups for the chip at
-  // decode batch sizes
-  KNJ_LAUNCH(k_combine, dim3(m, (H + 255) / 256), dim3(64), 0, s, y, pair_of, a.topk_idx,
-             a.topk_w, K, H, a.resid, a.out, a.hidden_copy);
+  if (a.next_norm_w) {
+    _Float16* const* sp = a.next_split;
+    KNJ_LAUNCH(k_combine_norm, dim3(m), dim3(kBlock), 0, s, y, pair_of, a.topk_idx, a.topk_w, K, H, m,
+               a.resid, a.out, a.hidden_copy, a.next_norm_w, a.next_eps, a.next_hx,
+               sp ? sp[0] : nullptr, sp ? sp[1] : nullptr, sp ? sp[2] : nullptr, sp ? sp[3] : nullptr);
+  } else {
+    // one wave per 256 columns of a token: enough workgroups for the chip at
+    // decode batch sizes
+    KNJ_LAUNCH(k_combine, dim3(m, (H + 255) / 256), dim3(64), 0, s, y, pair_of, a.topk_idx,
+               a.topk_w, K, H, a.resid, a.out, a.hidden_copy);
+  }
   return hipGetLastError();
 }
 
@@ -1273,6 +1433,15 @@ uint64_t dense_scratch_bytes(int m, int n_in, int n_out) {
          ((part + 255) & ~255ull);
 }
 
+hipError_t launch_norm_split(const float* x, const float* nw, float eps, int m, int n, float* hx,
+                             _Float16* const* split, hipStream_t s) {
+  if (n > 4096 || n % 256) return hipErrorInvalidValue;
+  KNJ_LAUNCH(k_combine_norm, dim3(m), dim3(kBlock), 0, s, nullptr, nullptr, nullptr, nullptr, 0, n,
+             m, x, const_cast<float*>(x), nullptr, nw, eps, hx, split ? split[0] : nullptr,
+             split ? split[1] : nullptr, split ? split[2] : nullptr, split ? split[3] : nullptr);
+  return hipGetLastError();
+}
+
 hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, int n, float* out,
                             hipStream_t s) {
   if (n > 4096 || n % 256) return hipErrorInvalidValue;
@@ -1280,8 +1449,19 @@ hipError_t launch_norm_rows(const float* x, const float* nw, float eps, int m, i
   return hipGetLastError();
 }
 
+uint64_t split_operand_bytes(int m, int n) {
+  const uint64_t P = (uint64_t)m;
+  return 2 * ((P * n * 2 + 255) & ~255ull) + 2 * ((P * n / 16 + 255) & ~255ull);
+}
+
 hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const float* x,
                             const float* resid, float* out, void* scratch, hipStream_t s) {
+  return launch_dense_q4k_ex(w, n_in, n_out, m, x, resid, out, scratch, DenseQ4Extra{}, s);
+}
+
+hipError_t launch_dense_q4k_ex(const uint8_t* w, int n_in, int n_out, int m, const float* x,
+                               const float* resid, float* out, void* scratch,
+                               const DenseQ4Extra& ex, hipStream_t s) {
   if (hipError_t e = group_lds_attr()) return e;
   if (n_in > 4096 || n_in % 256 || n_out % 32 || m > 1024) return hipErrorInvalidValue;
   const uint64_t P = (uint64_t)m;
@@ -1291,25 +1471,39 @@ hipError_t launch_dense_q4k(const uint8_t* w, int n_in, int n_out, int m, const 
     p += (bytes + 255) & ~255ull;
     return q;
   };
-  _Float16* xh = (_Float16*)take(P * n_in * 2);
-  _Float16* xl = (_Float16*)take(P * n_in * 2);
-  _Float16* sh = (_Float16*)take(P * n_in / 16);
-  _Float16* sl = (_Float16*)take(P * n_in / 16);
+  const _Float16* xh = (_Float16*)take(P * n_in * 2);
+  const _Float16* xl = (_Float16*)take(P * n_in * 2);
+  const _Float16* sh = (_Float16*)take(P * n_in / 16);
+  const _Float16* sl = (_Float16*)take(P * n_in / 16);
   const int ks = dense_ksplit(m, n_in, n_out);
   float* part = ks > 1 ? (float*)take((uint64_t)ks * P * n_out * 4) : nullptr;
-  KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 256), dim3(kBlock), 0, s, x, nullptr,
-             n_in, m, xh, xl, sh, sl);
+  if (ex.pre) {
+    xh = ex.pre[0];
+    xl = ex.pre[1];
+    sh = ex.pre[2];
+    sl = ex.pre[3];
+  } else {
+    KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 256), dim3(kBlock), 0, s, x, nullptr,
+               n_in, m, const_cast<_Float16*>(xh), const_cast<_Float16*>(xl),
+               const_cast<_Float16*>(sh), const_cast<_Float16*>(sl));
+  }
   GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, nullptr, nullptr, nullptr, out, resid};
   g.ksplit = ks;
   g.partial = part;
   const int tiles = (m + kTok - 1) / kTok;
   KNJ_LAUNCH(k_group_q4k<false>, dim3((n_out + kRowsWG - 1) / kRowsWG, tiles, ks),
                      dim3(kBlock), kGroupLds, s, g);
-  if (ks > 1) {
+  const bool fuse = ex.norm_w && ks > 1 && n_out <= 4096 && n_out % 256 == 0;
+  if (fuse) {
+    KNJ_LAUNCH(k_ksum_norm, dim3(m), dim3(kBlock), 0, s, part, ks, P * n_out, n_out, resid, out,
+               ex.norm_w, ex.eps, ex.norm_out);
+  } else if (ks > 1) {
     const uint64_t n = P * n_out;
     KNJ_LAUNCH(k_ksum, dim3((unsigned)((n / 4 + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, part, ks,
                n, resid, out);
   }
+  if (ex.norm_w && !fuse)
+    KNJ_LAUNCH(k_norm_rows, dim3(m), dim3(kBlock), 0, s, out, ex.norm_w, ex.eps, n_out, ex.norm_out);
   return hipGetLastError();
 }
 

@@ -113,8 +113,13 @@ int prefill_chunk(knj_model* m, const int32_t* tokens, int n, bool last) {
                        c.n_head_kv, D, c.n_ctx, 1.0f / std::sqrt((float)D), b.ctx, b.attn_part,
                        prefill_partial_bytes(c.n_head, c.n_head_kv, D, b.cap)};
     KNJ_HIP(launch_prefill_attention(pa, s));
-    KNJ_HIP(launch_dense_q4k(img + lo.wo, QD, H, n, b.ctx, b.x, b.x, b.scratch, s));
-    MoeBatchArgs ma{b.x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
+    // the O product's last launch also writes the ffn-normalised rows the MoE takes
+    DenseQ4Extra ox;
+    ox.norm_w = reinterpret_cast<const float*>(img + lo.ffn_norm);
+    ox.eps = c.rms_eps;
+    ox.norm_out = b.hx;
+    KNJ_HIP(launch_dense_q4k_ex(img + lo.wo, QD, H, n, b.ctx, b.x, b.x, b.scratch, ox, s));
+    MoeBatchArgs ma{b.hx, nullptr, c.rms_eps,
                     reinterpret_cast<const float*>(img + lo.router), img + lo.gate, img + lo.up,
                     img + lo.down, n, H, c.n_ff, E, K, b.x, b.x, b.router_logits, b.topk_idx,
                     b.topk_w};

@@ -738,18 +738,20 @@ def test_runs_are_bit_identical(device, config1_weights):
     finally:
         a.close()
         b.close()
-    n_embd, n_ff, n_expert, k, m = 2048, 768, 128, 8, 96
+    n_embd, n_ff, n_expert, k = 2048, 768, 128, 8
     _, router, gate, up, down = config1_weights
-    x = np.random.default_rng(6).standard_normal((m, n_embd)).astype(np.float32)
-    d = {nm: K.DeviceBuffer.from_array(v) for nm, v in
-         dict(x=x, router=router, gate=gate, up=up, down=down).items()}
-    outs = []
-    for _ in range(2):
-        out = K.DeviceBuffer(4 * m * n_embd)
-        logits = K.DeviceBuffer(4 * m * n_expert)
-        ti = K.DeviceBuffer(4 * m * k)
-        tw = K.DeviceBuffer(4 * m * k)
-        K.moe_batch_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], m, n_embd, n_ff,
-                          n_expert, k, out, logits, ti, tw)
-        outs.append(out.download(np.float32))
-    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    # 96 tokens: the few-pair kernels (8-pair items); 512: the 32-pair kernels
+    for m in (96, 512):
+        x = np.random.default_rng(6).standard_normal((m, n_embd)).astype(np.float32)
+        d = {nm: K.DeviceBuffer.from_array(v) for nm, v in
+             dict(x=x, router=router, gate=gate, up=up, down=down).items()}
+        outs = []
+        for _ in range(2):
+            out = K.DeviceBuffer(4 * m * n_embd)
+            logits = K.DeviceBuffer(4 * m * n_expert)
+            ti = K.DeviceBuffer(4 * m * k)
+            tw = K.DeviceBuffer(4 * m * k)
+            K.moe_batch_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], m, n_embd, n_ff,
+                              n_expert, k, out, logits, ti, tw)
+            outs.append(out.download(np.float32))
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), m
