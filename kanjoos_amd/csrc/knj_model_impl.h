@@ -19,6 +19,7 @@ struct knj_prefill_bufs {
   int32_t *topk_idx = nullptr, *tokens = nullptr;
   float* attn_part = nullptr;  // split-KV partials of the prompt-pass attention
   void* scratch = nullptr;
+  _Float16* qsplit[4] = {};  // the attn-normalised rows in the QKV product's operand layout
 };
 
 struct knj_model {

@@ -82,6 +82,19 @@ int ensure_bufs(knj_model* m) {
   A((void**)&b.attn_part, prefill_partial_bytes(c.n_head, c.n_head_kv, c.head_dim, R));
   A(&b.scratch, std::max({moe_batch_scratch_bytes(R, H, c.n_ff, c.n_expert, c.n_expert_used),
                           dense_scratch_bytes(R, H, QKV), dense_scratch_bytes(R, QD, H)}));
+  {
+    // [hi | lo | sums hi | sums lo] as split_operand_bytes lays them out
+    void* os = nullptr;
+    A(&os, split_operand_bytes(R, H));
+    if (!rc) {
+      uint8_t* q = (uint8_t*)os;
+      const uint64_t hb = ((uint64_t)R * H * 2 + 255) & ~255ull, sb = ((uint64_t)R * H / 16 + 255) & ~255ull;
+      b.qsplit[0] = (_Float16*)q;
+      b.qsplit[1] = (_Float16*)(q + hb);
+      b.qsplit[2] = (_Float16*)(q + 2 * hb);
+      b.qsplit[3] = (_Float16*)(q + 2 * hb + sb);
+    }
+  }
   if (!rc) b.cap = R;
   return rc;
 }
@@ -100,12 +113,19 @@ int prefill_chunk(knj_model* m, const int32_t* tokens, int n, bool last) {
                                                              b.tokens, b.x);
   KNJ_HIP(hipGetLastError());
   const float* lastx = b.x + (uint64_t)(n - 1) * H;
+  // layer 0's QKV operand; every later one comes from the previous layer's
+  // MoE combine (split operand of the split rows, in place of x's norm and split)
+  KNJ_HIP(launch_norm_split(b.x, reinterpret_cast<const float*>(img + m->lo[0].attn_norm), c.rms_eps,
+                            n, H, nullptr, b.qsplit, s));
   for (int il = 0; il < c.n_layer; ++il) {
     const knj_layer_offsets& lo = m->lo[il];
     const uint64_t kv_layer = (uint64_t)il * c.n_head_kv * c.n_ctx * D;
-    KNJ_HIP(launch_norm_rows(b.x, reinterpret_cast<const float*>(img + lo.attn_norm), c.rms_eps, n,
-                             H, b.hx, s));
-    KNJ_HIP(launch_dense_q4k(img + lo.wqkv, H, QKV, n, b.hx, nullptr, b.qkv, b.scratch, s));
+    {
+      const _Float16* pre[4] = {b.qsplit[0], b.qsplit[1], b.qsplit[2], b.qsplit[3]};
+      DenseQ4Extra qx;
+      qx.pre = pre;
+      KNJ_HIP(launch_dense_q4k_ex(img + lo.wqkv, H, QKV, n, nullptr, nullptr, b.qkv, b.scratch, qx, s));
+    }
     PrefillAttnArgs pa{b.qkv, QKV,
                        reinterpret_cast<const float*>(img + lo.q_norm),
                        reinterpret_cast<const float*>(img + lo.k_norm), c.rms_eps, m->rope_cos,
@@ -124,6 +144,11 @@ int prefill_chunk(knj_model* m, const int32_t* tokens, int n, bool last) {
                     img + lo.down, n, H, c.n_ff, E, K, b.x, b.x, b.router_logits, b.topk_idx,
                     b.topk_w};
     ma.type_down = c.type_down;
+    if (il + 1 < c.n_layer) {
+      ma.next_norm_w = reinterpret_cast<const float*>(img + m->lo[il + 1].attn_norm);
+      ma.next_eps = c.rms_eps;
+      ma.next_split = b.qsplit;
+    }
     KNJ_HIP(launch_moe_batch(ma, b.scratch, s));
     if (last) {
       const uint64_t r = (uint64_t)(n - 1);
