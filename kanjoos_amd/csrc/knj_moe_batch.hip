@@ -397,8 +397,27 @@ typedef __attribute__((address_space(1))) void glb_void;
 // s_waitcnt immediate (gfx9 encoding) that waits until at most n vector
 // memory operations are outstanding and does not wait on the other counters
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+// ... and that also waits for every LDS access of this wave
+constexpr int vm_lds_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
 
-template <bool GATEUP>
+// Workgroup barrier once at most N vector memory operations of this wave
+// remain outstanding (and no LDS access).  __syncthreads() is a release fence
+// plus the barrier, and the fence waits for every outstanding load (the
+// LDS-DMA staging makes them count as LDS writes), which would empty the
+// weight look-ahead at every barrier; the staging a barrier hands over is
+// covered by the explicit count instead.  The asm's memory clobber keeps the
+// compiler from moving memory accesses across it.
+#define KNJ_BARRIER_VM(N)                      \
+  do {                                         \
+    __builtin_amdgcn_s_waitcnt(vm_lds_imm(N)); \
+    __builtin_amdgcn_sched_barrier(0);         \
+    asm volatile("s_barrier" ::: "memory");    \
+    __builtin_amdgcn_sched_barrier(0);         \
+  } while (0)
+
+// NSBT > 0: the super-block range of every workgroup is exactly NSBT long
+// (the fully unrolled form below).
+template <bool GATEUP, int NSBT = 0>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_group_q4k(GroupArgs a) {
   extern __shared__ uint4 lds[];
   // grouped: work item blockIdx.y of the list; dense (no offsets): the
@@ -427,7 +446,10 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
   const uint8_t* wr1 = GATEUP ? a.w1 + (uint64_t)e * slab + (uint64_t)row * rb : wr0;
   // staging by LDS DMA (no registers): wave w's instruction u fills entries
   // e = (8 w + u) 64 + lane of the buffer's hi/lo parts ([part][8-group q]
-  // [pair]); wave 0 also fills the 64 sums entries (hi 32, lo 32)
+  // [pair]); wave 0 also fills the 64 sums entries (hi 32, lo 32), and in the
+  // unrolled form every wave does, the same bytes, so that all waves issue
+  // the same number of loads and the compiler's count of outstanding loads
+  // stays exact along the straight line
   auto stage = [&](int sb, int buf) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
@@ -436,7 +458,7 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
       const _Float16* src = (part ? a.al : a.ah) + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8;
       __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(lds + buf * kBuf + e0), 16, 0, 0);
     }
-    if (wave == 0) {
+    if (NSBT > 0 || wave == 0) {
       const _Float16* src = ((lane >> 5) ? a.sl : a.sh) + ((uint64_t)sb * P + p0 + min(lane & 31, cnt - 1)) * 8;
       __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(lds + buf * kBuf + 2 * kPart), 16, 0, 0);
     }
@@ -447,28 +469,46 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
 #pragma unroll
     for (int g = 0; g < 4; ++g) w.c[g] = *reinterpret_cast<const uint4*>(b + KNJ_Q4K_QS + 32 * g + 16 * kh);
   };
-  WBlock w0c, w1c, w0n, w1n;
-  // prologue: the first super-block of the range
-  stage(sbb, 0);
-  w_load(wr0, sbb, w0c);
-  if constexpr (GATEUP) w_load(wr1, sbb, w1c);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
   f32x16 acc0 = {}, acc1 = {};
-  for (int sb = sbb; sb < nsb; ++sb) {
-    const int buf = (sb - sbb) & 1;
-    const int nx = min(sb + 1, nsb - 1);  // the last iteration reloads its own block, unused
-    const bool more = sb + 1 < nsb;
-    // every load of the next super-block is issued before this one's
-    // arithmetic, the staging first: the memory counter is in order, so the
-    // wait for the staging at the end does not wait for the weights
-    if (more) stage(nx, buf ^ 1);
-    w_load(wr0, nx, w0n);
-    if constexpr (GATEUP) w_load(wr1, nx, w1n);
+  constexpr int WN = GATEUP ? 10 : 5;  // weight loads of one super-block
+  // Weight register sets.  Fixed range (NSBT > 0, fully unrolled): three sets
+  // in rotation, the weights of super-block i + 2 loaded while i is computed;
+  // a straight line, so no register copies wait for loads and the compiler's
+  // wait counts are exact.  Any range: the weights of i + 1 go to set 1 while
+  // set 0 is computed, then are copied over.
+  WBlock w0s[3], w1s[3];
+  const int n_it = NSBT > 0 ? NSBT : nsb - sbb;
+  stage(sbb, 0);
+  w_load(wr0, sbb, w0s[0]);
+  if constexpr (GATEUP) w_load(wr1, sbb, w1s[0]);
+  if constexpr (NSBT > 1) {
+    w_load(wr0, sbb + 1, w0s[1]);
+    if constexpr (GATEUP) w_load(wr1, sbb + 1, w1s[1]);
+    KNJ_BARRIER_VM(WN);
+  } else {
+    KNJ_BARRIER_VM(0);
+  }
+  constexpr int kUnroll = NSBT > 0 ? NSBT : 1;
+#pragma unroll kUnroll
+  for (int i = 0; i < n_it; ++i) {
+    const int buf = i & 1;
+    const int ci = NSBT > 0 ? i % 3 : 0, ni = NSBT > 0 ? (i + 2) % 3 : 1;
+    // every load of a later super-block is issued before this one's
+    // arithmetic, the staging first: the memory counter is in order, so
+    // the wait for the staging at the end leaves the weights in flight
+    if (i + 1 < n_it) stage(sbb + i + 1, buf ^ 1);
+    const bool load_next = NSBT == 0 || i + 2 < NSBT;
+    if (load_next) {
+      // any range: the last iteration reloads its own block, unused
+      const int nx = NSBT > 0 ? sbb + i + 2 : min(sbb + i + 1, nsb - 1);
+      w_load(wr0, nx, w0s[ni]);
+      if constexpr (GATEUP) w_load(wr1, nx, w1s[ni]);
+    }
     __builtin_amdgcn_sched_barrier(0);
+    const WBlock& w0c = w0s[ci];
+    const WBlock& w1c = w1s[ci];
     const uint4* L = lds + buf * kBuf;
     const half8 am = __builtin_bit_cast(half8, L[2 * kPart + kh * 32 + j]);
-    // scales and mins of this lane's row, and the min-term step
     // the mins of this lane's row and the min-term step; the scales are
     // decoded per code group below
     auto mins = [&](const uint4& h) {
@@ -535,20 +575,24 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     if constexpr (GATEUP) {
       const float d1 = h2f(w1c.h.x), m1 = h2f(w1c.h.x >> 16);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        acc0[i] += d0 * cqa[i] - m0 * cm0[i];
-        acc1[i] += d1 * cqb[i] - m1 * cm1[i];
+      for (int r = 0; r < 16; ++r) {
+        acc0[r] += d0 * cqa[r] - m0 * cm0[r];
+        acc1[r] += d1 * cqb[r] - m1 * cm1[r];
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc0[i] += d0 * (cqa[i] + cqb[i]) - m0 * cm0[i];
+      for (int r = 0; r < 16; ++r) acc0[r] += d0 * (cqa[r] + cqb[r]) - m0 * cm0[r];
     }
-    w0c = w0n;
-    if constexpr (GATEUP) w1c = w1n;
-    // the staging done (at most the weight loads issued after it outstanding)
-    // before the barrier that hands the buffer over
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(GATEUP ? 10 : 5));
-    __syncthreads();
+    if constexpr (NSBT == 0) {
+      w0s[0] = w0s[1];
+      if constexpr (GATEUP) w1s[0] = w1s[1];
+    }
+    // the staging done (at most the weight loads issued after it
+    // outstanding) before the barrier that hands the buffer over
+    if (load_next)
+      KNJ_BARRIER_VM(WN);
+    else
+      KNJ_BARRIER_VM(0);
   }
   __builtin_amdgcn_s_waitcnt(0);
   if (!rows_ok || rbase + (lane & 31) >= a.n_out) return;
@@ -1292,6 +1336,9 @@ hipError_t group_lds_attr() {
       r = hipFuncSetAttribute((const void*)k_group_q4k<false>,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGroupLds);
     if (r == hipSuccess)
+      r = hipFuncSetAttribute((const void*)k_group_q4k<false, 3>,
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGroupLds);
+    if (r == hipSuccess)
       r = hipFuncSetAttribute((const void*)k_group_q6k,
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGroupLds);
     return r;
@@ -1395,6 +1442,9 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   } else if (a.type_down == KNJ_TYPE_Q6_K)
     KNJ_LAUNCH(k_group_q6k, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock), kGroupLds,
                s, dn);
+  else if (F == 3 * 256)  // the model's 768-wide expert rows: the unrolled form
+    KNJ_LAUNCH((k_group_q4k<false, 3>), dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+               kGroupLds, s, dn);
   else
     KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
                kGroupLds, s, dn);
