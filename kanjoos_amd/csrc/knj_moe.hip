@@ -669,8 +669,37 @@ __global__ __launch_bounds__(512) void k_expert_down8(ExpertArgs a) {
 // workgroup's 8 rows; lane = one 32-weight unit of a row (32-lane halves take
 // rows 2i and 2i + 1, four rounds), read with q6_unit_load as in the one-row
 // kernel; activations and their 8-element sums staged once per workgroup.
+// STAGED: the 8 rows of a wave's expert are one contiguous, 16-byte aligned
+// run (8 x 630 bytes at n_ff = 768), fetched with 16-byte loads into LDS and
+// decoded from there, instead of three unaligned 8-byte runs, four scale
+// bytes and d per 32-weight unit straight from memory.
+constexpr int kQ6StageLoads = 7;  // 16-byte loads per lane: 8 rows of n_ff <= 1024
+
+// q6_unit_load from a Q6_K block at byte `blk` of an LDS region (2-byte
+// aligned blocks): the 8-byte runs as three aligned words and a funnel shift
+__device__ __forceinline__ void lds_ld8(const uint32_t* w4, uint32_t off, uint32_t& x, uint32_t& y) {
+  const uint32_t* w = w4 + (off >> 2);
+  const uint32_t w0 = w[0], w1 = w[1], w2 = w[2];
+  const uint32_t sh = (off & 3) * 8;
+  x = sh ? __builtin_amdgcn_alignbit(w1, w0, sh) : w0;
+  y = sh ? __builtin_amdgcn_alignbit(w2, w1, sh) : w1;
+}
+__device__ __forceinline__ Q6Unit q6_unit_load_lds(const uint8_t* region, uint32_t blk, int hf, int o) {
+  const uint32_t* w4 = reinterpret_cast<const uint32_t*>(region);
+  Q6Unit u;
+  lds_ld8(w4, blk + KNJ_Q6K_QL + 64 * hf + 8 * o, u.l0a, u.l0b);
+  lds_ld8(w4, blk + KNJ_Q6K_QL + 64 * hf + 32 + 8 * o, u.l1a, u.l1b);
+  lds_ld8(w4, blk + KNJ_Q6K_QH + 32 * hf + 8 * o, u.ha, u.hb);
+  const int8_t* sp = reinterpret_cast<const int8_t*>(region + blk + KNJ_Q6K_SC + 8 * hf + (o >> 1));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) u.sc[t] = sp[2 * t];
+  u.d = *reinterpret_cast<const uint16_t*>(region + blk + KNJ_Q6K_D);
+  return u;
+}
+template <bool STAGED>
 __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
   constexpr int KMAX = 8;
+  extern __shared__ uint4 wstage[];  // STAGED: [wave][8 rows x rb / 16]
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int F = a.n_ff, K = a.k, n = K * F;
   const int nunits = F / 32;
@@ -705,10 +734,18 @@ __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
   for (int q = 1; q < KMAX; ++q) e = kk == q ? ids[q] : e;
   const uint8_t* ex = a.down + (uint64_t)e * slab + (uint64_t)b * KNJ_Q6K_BLOCK;
   Q6Unit qu[kDownRows / 2];
+  const int nch = (int)(kDownRows * rb / 16);  // 16-byte chunks of the 8 rows
+  uint4 w0, w1, w2, w3, w4, w5, w6;  // (named registers, as above)
+  if constexpr (STAGED) {
+    const uint4* src = reinterpret_cast<const uint4*>(a.down + (uint64_t)e * slab + (uint64_t)r0 * rb);
+    auto ldc = [&](int j) { return src[min(lane + 64 * j, nch - 1)]; };
+    w0 = ldc(0); w1 = ldc(1); w2 = ldc(2); w3 = ldc(3); w4 = ldc(4); w5 = ldc(5); w6 = ldc(6);
+  } else {
 #pragma unroll
-  for (int it = 0; it < kDownRows / 2; ++it) {
-    const int row = min(r0 + 2 * it + half, a.n_embd - 1);
-    qu[it] = q6_unit_load(ex + (uint64_t)row * rb, hf, o);
+    for (int it = 0; it < kDownRows / 2; ++it) {
+      const int row = min(r0 + 2 * it + half, a.n_embd - 1);
+      qu[it] = q6_unit_load(ex + (uint64_t)row * rb, hf, o);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   auto stage4 = [&](int j, const float4& v) {
@@ -726,6 +763,20 @@ __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
     s8[g] = ((x0.x + x0.y) + (x0.z + x0.w)) + ((x1.x + x1.y) + (x1.z + x1.w));
   }
   __syncthreads();
+  if constexpr (STAGED) {
+    // this wave's rows into its own LDS range and back: one wave's LDS
+    // accesses complete in order, so no barrier
+    uint4* mine = wstage + wave * nch;
+    auto stc = [&](int j, const uint4& v) {
+      if (lane + 64 * j < nch) mine[lane + 64 * j] = v;
+    };
+    stc(0, w0); stc(1, w1); stc(2, w2); stc(3, w3); stc(4, w4); stc(5, w5); stc(6, w6);
+    asm volatile("" ::: "memory");
+    const uint8_t* wl = reinterpret_cast<const uint8_t*>(mine);
+#pragma unroll
+    for (int it = 0; it < kDownRows / 2; ++it)
+      qu[it] = q6_unit_load_lds(wl, (uint32_t)((2 * it + half) * rb + b * KNJ_Q6K_BLOCK), hf, o);
+  }
   float4 x8[4][2];
   float sx[4];
 #pragma unroll
@@ -1005,10 +1056,24 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
   if (a.type_down != KNJ_TYPE_Q6_K) return hipErrorInvalidValue;
   if (a.n_ff <= 1024 && a.k <= 8) {
     const int grid = (a.n_embd + kDownRows - 1) / kDownRows;
-    if (t0 || span_take("k_expert_down8_q6", &t0, &t1))
-      hipExtLaunchKernelGGL(k_expert_down8_q6, dim3(grid), dim3(512), 0u, s, t0, t1, 0u, a);
-    else
-      hipLaunchKernelGGL(k_expert_down8_q6, dim3(grid), dim3(512), 0, s, a);
+    const uint64_t rb = (uint64_t)(a.n_ff / KNJ_QK) * KNJ_Q6K_BLOCK;
+    const bool staged = a.n_embd % kDownRows == 0 && (kDownRows * rb) % 16 == 0 &&
+                        (rb * a.n_embd) % 16 == 0 && (reinterpret_cast<uintptr_t>(a.down) & 15) == 0;
+    if (staged) {
+      const unsigned lds = (unsigned)(8 * kDownRows * rb);  // 8 waves x 8 rows
+      static const hipError_t attr = hipFuncSetAttribute(
+          (const void*)k_expert_down8_q6<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
+          (int)(8 * kDownRows * 4 * KNJ_Q6K_BLOCK));
+      if (attr != hipSuccess) return attr;
+      if (t0 || span_take("k_expert_down8_q6", &t0, &t1))
+        hipExtLaunchKernelGGL(k_expert_down8_q6<true>, dim3(grid), dim3(512), lds, s, t0, t1, 0u, a);
+      else
+        hipLaunchKernelGGL(k_expert_down8_q6<true>, dim3(grid), dim3(512), lds, s, a);
+    } else if (t0 || span_take("k_expert_down8_q6", &t0, &t1)) {
+      hipExtLaunchKernelGGL(k_expert_down8_q6<false>, dim3(grid), dim3(512), 0u, s, t0, t1, 0u, a);
+    } else {
+      hipLaunchKernelGGL(k_expert_down8_q6<false>, dim3(grid), dim3(512), 0, s, a);
+    }
     return hipGetLastError();
   }
   if (a.n_ff <= 1024 && a.k <= 16) {
