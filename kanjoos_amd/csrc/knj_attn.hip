@@ -805,10 +805,12 @@ __global__ __launch_bounds__(kBlock) void k_prefill_merge(PrefillAttnArgs a, int
 
 int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
 
-// splits of one head: one 64-slot chunk per workgroup up to 256 chunks (the
-// merge folds 8 parts x 32 splits; measured at 32K slots, 256 splits of 2-3
-// chunks beat 128 of 4-5 by 2% per token)
-constexpr int kMaxSplit = 256;
+// splits of one head: one 64-slot chunk per workgroup up to kMaxSplit1
+// chunks at one sequence (the merge folds 8 parts x 40 splits; measured at 32K
+// slots, 256 splits of 2-3 chunks beat 128 of 4-5 by 2% per token, and the
+// 40-split parts keep 2 chunks per workgroup just past 32768 slots), up to
+// kMaxSplit with several sequences (the per-head merge)
+constexpr int kMaxSplit = 256, kMaxSplit1 = 320;
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   // one 64-slot chunk per workgroup up to kMaxSplit chunks; beyond, several
@@ -817,9 +819,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   // several sequences fill the chip with their own splits: two chunks per
   // workgroup there (measured 2% faster at 32 sequences x 2048 slots; one
   // chunk is faster at batch 1)
-  const int cpw = std::max((chunks + kMaxSplit - 1) / kMaxSplit, a.n_seq > 1 ? 2 : 1);
+  const int max_split = a.n_seq > 1 ? kMaxSplit : kMaxSplit1;
+  const int cpw = std::max((chunks + max_split - 1) / max_split, a.n_seq > 1 ? 2 : 1);
   const int n_split = (chunks + cpw - 1) / cpw;
-  if (n_split > kMaxSplit) return hipErrorInvalidValue;  // the merge folds at most 8 x 32 splits
+  if (n_split > max_split) return hipErrorInvalidValue;
   const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
     if (cpw <= 2)
@@ -828,8 +831,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH((k_attention<128, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     if (z == 1 && !a.split_hi && n_split <= 128)  // (the loads a part holds cost at short contexts)
       KNJ_LAUNCH((k_attn_merge<128, 16>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
-    else if (z == 1 && !a.split_hi)
+    else if (z == 1 && !a.split_hi && n_split <= 256)
       KNJ_LAUNCH((k_attn_merge<128, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+    else if (z == 1 && !a.split_hi)
+      KNJ_LAUNCH((k_attn_merge<128, 40>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
@@ -839,8 +844,10 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH((k_attention<64, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     if (z == 1 && !a.split_hi && n_split <= 128)
       KNJ_LAUNCH((k_attn_merge<64, 16>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
-    else if (z == 1 && !a.split_hi)
+    else if (z == 1 && !a.split_hi && n_split <= 256)
       KNJ_LAUNCH((k_attn_merge<64, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+    else if (z == 1 && !a.split_hi)
+      KNJ_LAUNCH((k_attn_merge<64, 40>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
