@@ -415,24 +415,42 @@ constexpr int vm_lds_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4);
     __builtin_amdgcn_sched_barrier(0);         \
   } while (0)
 
+// XCD-aware work mapping of a grouped launch (grid nrb row blocks x at least
+// 8 * ceil(n_items / 8) items): workgroups are dispatched to the eight XCDs
+// in turn by linear index, so XCD x runs linear indices x, x + 8, ...; this
+// gives XCD x the contiguous run of items [x * ipx, (x + 1) * ipx) with all
+// their row blocks.  The row blocks of one item share its activation tile,
+// and an expert's items are adjacent in the list and share its weight rows:
+// both are then read once into that XCD's L2 instead of once per XCD.
+// False: no work for this workgroup.
+__device__ __forceinline__ bool xcd_item(int nrb, int n_items, int& rblock, int& item) {
+  const int L = blockIdx.x + nrb * blockIdx.y;
+  const int xcd = L & 7, k = L >> 3;
+  const int ipx = (n_items + 7) >> 3;
+  const int ii = k / nrb;
+  rblock = k - ii * nrb;
+  item = xcd * ipx + ii;
+  return ii < ipx && item < n_items;
+}
+
 // NSBT > 0: the super-block range of every workgroup is exactly NSBT long
 // (the fully unrolled form below).
 template <bool GATEUP, int NSBT = 0>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) void k_group_q4k(GroupArgs a) {
   extern __shared__ uint4 lds[];
-  // grouped: work item blockIdx.y of the list; dense (no offsets): the
-  // m rows are one expert, tile blockIdx.y
-  int e = 0, p0 = blockIdx.y * kTok, cnt = min(kTok, a.P - p0);
+  // grouped: a work item of the list and a row block (xcd_item); dense (no
+  // offsets): the m rows are one expert, tile blockIdx.y, row block blockIdx.x
+  int e = 0, p0 = blockIdx.y * kTok, cnt = min(kTok, a.P - p0), rblock = blockIdx.x;
   if (a.offsets) {
-    const int item = blockIdx.y;
-    if (item >= *a.n_items) return;  // uniform over the workgroup
+    int item;
+    if (!xcd_item(gridDim.x, *a.n_items, rblock, item)) return;  // uniform over the workgroup
     const int2 it = a.items[item];
     e = it.x;
     p0 = a.offsets[e] + it.y;
     cnt = min(a.tile, a.offsets[e + 1] - p0);
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int rbase = blockIdx.x * kRowsWG + wave * 32;
+  const int rbase = rblock * kRowsWG + wave * 32;
   const bool rows_ok = rbase < a.n_out;  // waves past the last row still stage and sync
   const int row = min(rbase + (lane & 31), a.n_out - 1), kh = lane >> 5;
   const int j = lane & 31;
@@ -712,7 +730,9 @@ __global__ __launch_bounds__(256) void k_group_fewk(GroupArgs a) {
   constexpr int NM = GATEUP ? 2 : 1;
   __shared__ f32x4 part[4][NM * FT][64];
   __shared__ float vs[SPLIT ? 32 : 1][kFew];  // the workgroup's outputs (split form)
-  const int item = blockIdx.y;
+  // (the plain order: the XCD-aware mapping of the 32-pair kernels measured
+  // slower here, where an expert rarely has more than one item)
+  const int item = blockIdx.y, rblock = blockIdx.x;
   if (item >= *a.n_items) return;  // uniform over the workgroup
   const int2 it = a.items[item];
   const int e = it.x, p0 = a.offsets[e] + it.y;
@@ -720,7 +740,7 @@ __global__ __launch_bounds__(256) void k_group_fewk(GroupArgs a) {
   const int KS = blockDim.x >> 6;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, kq = lane >> 4;
-  const int rbase = blockIdx.x * 16 * FT;
+  const int rbase = rblock * 16 * FT;
   const int nsb = a.n_in >> 8;
   const uint64_t P = (uint64_t)a.P;
   const uint64_t rb = (uint64_t)nsb * KNJ_Q4K_BLOCK;
@@ -866,17 +886,17 @@ __global__ __launch_bounds__(kBlock) void k_group_q6k(GroupArgs a) {
   extern __shared__ uint4 lds[];
   // grouped: work item blockIdx.y; dense (no offsets): tile blockIdx.y of the
   // P rows seen as one expert
-  int e = 0, p0 = blockIdx.y * kTok, cnt = min(kTok, a.P - p0);
+  int e = 0, p0 = blockIdx.y * kTok, cnt = min(kTok, a.P - p0), rblock = blockIdx.x;
   if (a.offsets) {
-    const int item = blockIdx.y;
-    if (item >= *a.n_items) return;  // uniform over the workgroup
+    int item;
+    if (!xcd_item(gridDim.x, *a.n_items, rblock, item)) return;  // uniform over the workgroup
     const int2 it = a.items[item];
     e = it.x;
     p0 = a.offsets[e] + it.y;
     cnt = min(a.tile, a.offsets[e + 1] - p0);
   }
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int rbase = blockIdx.x * kRowsWG + wave * 32;
+  const int rbase = rblock * kRowsWG + wave * 32;
   const bool rows_ok = rbase < a.n_out;
   const int row = min(rbase + (lane & 31), a.n_out - 1), kh = lane >> 5;
   const int j = lane & 31;
@@ -1430,7 +1450,7 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
     gu.osl = sal;
     if (hipError_t e = launch_fewk<true>(gu, max_items, 2, s)) return e;
   } else {
-    KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+    KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items + 8), dim3(kBlock),
                kGroupLds, s, gu);
     KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), F / 256), dim3(kBlock), 0, s, act,
                nullptr, F, (int)P, ah, al, sah, sal);
@@ -1440,13 +1460,13 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
   if (few && a.type_down == KNJ_TYPE_Q4_K) {
     if (hipError_t e = launch_fewk<false>(dn, max_items, (F >> 8) <= 4 ? 4 : 2, s)) return e;
   } else if (a.type_down == KNJ_TYPE_Q6_K)
-    KNJ_LAUNCH(k_group_q6k, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock), kGroupLds,
+    KNJ_LAUNCH(k_group_q6k, dim3((H + kRowsWG - 1) / kRowsWG, max_items + 8), dim3(kBlock), kGroupLds,
                s, dn);
   else if (F == 3 * 256)  // the model's 768-wide expert rows: the unrolled form
-    KNJ_LAUNCH((k_group_q4k<false, 3>), dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+    KNJ_LAUNCH((k_group_q4k<false, 3>), dim3((H + kRowsWG - 1) / kRowsWG, max_items + 8), dim3(kBlock),
                kGroupLds, s, dn);
   else
-    KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items), dim3(kBlock),
+    KNJ_LAUNCH(k_group_q4k<false>, dim3((H + kRowsWG - 1) / kRowsWG, max_items + 8), dim3(kBlock),
                kGroupLds, s, dn);
   if (a.next_norm_w) {
     _Float16* const* sp = a.next_split;
