@@ -613,6 +613,54 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
       KNJ_BARRIER_VM(0);
   }
   __builtin_amdgcn_s_waitcnt(0);
+  if constexpr (GATEUP) {
+    if (a.oh) {
+      // SwiGLU written straight as the down product's operand, the same
+      // values, order and roundings as k_split_tile over the f32 rows: the
+      // wave's 32 x 32 tile goes through its own LDS range (free after the
+      // last barrier) as [pair][row]; lane (pair, 8-group g of the wave's 32
+      // rows) then forms the perm8 high parts and remainders and the
+      // group's sequential sum, four consecutive lanes the 32-row sum
+      if (!rows_ok) return;
+      float* vs = reinterpret_cast<float*>(lds) + wave * 32 * 33;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int tj = 8 * (i / 4) + 4 * kh + (i % 4);
+        const float g = acc0[i];
+        vs[tj * 33 + j] = (g / (1.0f + expf(-g))) * acc1[i];
+      }
+      const int b = rbase >> 5;  // the 32-row sub-block of the wave
+#pragma unroll
+      for (int r = 0; r < 2; ++r) {
+        const int pr = 16 * r + (lane >> 2), g = lane & 3;
+        float v[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) v[q] = vs[pr * 33 + 8 * g + q];
+        half8 h, l;
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const float x = v[perm8(q)];
+          h[q] = (_Float16)x;
+          l[q] = (_Float16)(x - (float)h[q]);
+          sum += v[q];
+        }
+        sum = group_sum<4>(sum);
+        if (pr < cnt) {
+          const uint64_t o = ((uint64_t)((rbase >> 3) + g) * P + p0 + pr) * 8;
+          *reinterpret_cast<half8*>(a.oh + o) = h;
+          *reinterpret_cast<half8*>(a.ol + o) = l;
+          if (g == 0) {
+            const _Float16 sv = (_Float16)sum;
+            const uint64_t so = ((uint64_t)(b >> 3) * P + p0 + pr) * 8 + (b & 7);
+            a.osh[so] = sv;
+            a.osl[so] = (_Float16)(sum - (float)sv);
+          }
+        }
+      }
+      return;
+    }
+  }
   if (!rows_ok || rbase + (lane & 31) >= a.n_out) return;
   // acc[i] = C[token 8*(i/4) + 4*kh + i%4][row]
 #pragma unroll
@@ -1450,10 +1498,13 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
     gu.osl = sal;
     if (hipError_t e = launch_fewk<true>(gu, max_items, 2, s)) return e;
   } else {
+    // SwiGLU written straight in the down product's operand layout
+    gu.oh = ah;
+    gu.ol = al;
+    gu.osh = sah;
+    gu.osl = sal;
     KNJ_LAUNCH(k_group_q4k<true>, dim3((F + kRowsWG - 1) / kRowsWG, max_items + 8), dim3(kBlock),
                kGroupLds, s, gu);
-    KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), F / 256), dim3(kBlock), 0, s, act,
-               nullptr, F, (int)P, ah, al, sah, sal);
   }
   GroupArgs dn{a.down, nullptr, F, H, ah, al, sah, sal, (int)P, offsets, items, n_items, y};
   dn.tile = tile;
