@@ -158,6 +158,51 @@ def test_moe_batch_layer(device, config1_weights, q6_down_weights, m, type_down)
     assert worst <= 1e-5
 
 
+@pytest.mark.parametrize("m,seed", [(64, 764), (512, 1213)])
+def test_moe_batch_layer_skewed(device, config1_weights, m, seed):
+    """Routing concentrated on a few experts: every token is one shared
+    direction plus small noise, so most experts get no pair and a handful get
+    about m pairs each (many 32-pair or 8-pair work items per expert, the
+    grouped kernels' XCD-ordered items of one expert side by side).  Same bar
+    as test_moe_batch_layer.  With tokens this alike, some seeds give a token
+    two top-9 logits within one float32 ulp, whose selection order then
+    depends on the summation order of the logit (not a fixed property of
+    either side); the seeds here keep every top-9 gap above 1e-5 relative,
+    and the test checks that premise."""
+    n_embd, n_ff, n_expert, k = 2048, 768, 128, 8
+    say(f"moe batch layer skewed m={m}")
+    _, router, gate, up, down = config1_weights
+    rng = np.random.default_rng(seed)
+    base = rng.standard_normal(n_embd).astype(np.float32)
+    x = (base[None, :] + 0.05 * rng.standard_normal((m, n_embd))).astype(np.float32)
+    resid = rng.standard_normal((m, n_embd)).astype(np.float32)
+    ones = np.ones(n_embd, np.float32)
+    hx = np.stack([O.rmsnorm(x[t], ones, 1e-6) for t in range(m)])
+    out_w, logits_w, ti_w, tw_w = O.moe(hx, router, gate, up, down, n_embd, n_ff, n_expert, k)
+    counts = np.bincount(ti_w.reshape(-1), minlength=n_expert)
+    say(f"  experts used {np.count_nonzero(counts)}, most pairs on one expert {counts.max()}")
+    assert counts.max() >= m // 2  # the routing is skewed as intended
+    top9 = -np.sort(-logits_w.reshape(m, n_expert), axis=1)[:, :9]
+    gap = (np.abs(np.diff(top9, axis=1)) / np.abs(top9[:, :-1])).min()
+    assert gap > 1e-5, f"inputs hold a near-tie in the top-9 logits ({gap:.3g})"
+    d = {nm: K.DeviceBuffer.from_array(a) for nm, a in
+         dict(x=x, resid=resid, router=router, gate=gate, up=up, down=down, ones=ones).items()}
+    out = K.DeviceBuffer(4 * m * n_embd)
+    logits = K.DeviceBuffer(4 * m * n_expert)
+    ti = K.DeviceBuffer(4 * m * k)
+    tw = K.DeviceBuffer(4 * m * k)
+    K.moe_batch_layer(d["x"], d["router"], d["gate"], d["up"], d["down"], m, n_embd, n_ff, n_expert,
+                      k, out, logits, ti, tw, norm_w=d["ones"], eps=1e-6, resid=d["resid"])
+    got_ti = ti.download(np.int32).reshape(m, k)
+    bad = np.flatnonzero((got_ti != ti_w).any(axis=1))
+    assert bad.size == 0, f"top-k differs for tokens {bad[:8]}"
+    assert np.allclose(tw.download(np.float32).reshape(m, k), tw_w, rtol=1e-5, atol=1e-7)
+    got = out.download(np.float32).reshape(m, n_embd) - resid
+    worst = max(rel_rmse(got[t], out_w[t]) for t in range(m))
+    say(f"  worst per-token rel-RMSE {worst:.3g}")
+    assert worst <= 1e-5
+
+
 def small_config(**kw):
     base = dict(n_layer=3, n_embd=512, n_head=8, n_head_kv=2, head_dim=64, n_ff=256,
                 n_expert=16, n_expert_used=4, n_vocab=4096, n_ctx=160)
