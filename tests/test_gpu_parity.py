@@ -121,8 +121,8 @@ def q6_down_weights():
 
 
 @pytest.mark.parametrize("m,type_down", [(1, K.TYPE_Q4_K), (7, K.TYPE_Q4_K), (64, K.TYPE_Q4_K),
-                                         (512, K.TYPE_Q4_K), (7, K.TYPE_Q6_K), (64, K.TYPE_Q6_K),
-                                         (512, K.TYPE_Q6_K)])
+                                         (300, K.TYPE_Q4_K), (512, K.TYPE_Q4_K), (7, K.TYPE_Q6_K),
+                                         (64, K.TYPE_Q6_K), (512, K.TYPE_Q6_K)])
 def test_moe_batch_layer(device, config1_weights, q6_down_weights, m, type_down):
     """Config 2 (m = 512) and smaller batches: the batched MoE layer against the
     oracle's Model::moe on the same m rows (top-k bit-exact, out <= 1e-5), with
