@@ -363,20 +363,21 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   KNJ_STAMP(5);
 }
 
-// Merge of the split partials of one query head over 32 of its dims (one
-// workgroup per (head, 32 dims)): M = max m_s, f_s = exp(m_s - M),
+// Merge of the split partials of one query head over DW of its dims (one
+// workgroup per (head, DW dims)): M = max m_s, f_s = exp(m_s - M),
 // out = sum_s acc_s f_s / sum_s l_s f_s.  Every split's record is written on
 // every call (splits past the position hold m = -inf, l = 0, acc = 0), so no
 // load waits on the position.  Thread (dim j, part p) folds the splits of part
-// p (8 contiguous ranges, in order); every load of a thread is issued before
-// the first use, and the parts are added in order.
-template <int D, int PMAX>  // PMAX splits per part: n_split <= 8 PMAX
+// p (kBlock / DW contiguous ranges, in order); every load of a thread is
+// issued before the first use ({m, l} as one 8-byte load), and the parts are
+// added in order.
+template <int D, int PMAX, int DW>  // PMAX splits per part: n_split <= (kBlock / DW) PMAX
 __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) {
-  constexpr int NP = kBlock / 32;  // parts
+  constexpr int NP = kBlock / DW;  // parts
   __shared__ float pm[NP], pl[NP];
-  __shared__ float pacc[NP][32];
-  const int h = blockIdx.x / (D / 32), d0 = 32 * (blockIdx.x % (D / 32));
-  const int z = blockIdx.y, tid = threadIdx.x, j = tid & 31, part = tid >> 5;
+  __shared__ float pacc[NP][DW];
+  const int h = blockIdx.x / (D / DW), d0 = DW * (blockIdx.x % (D / DW));
+  const int z = blockIdx.y, tid = threadIdx.x, j = tid % DW, part = tid / DW;
   const float* ph = a.partial + ((uint64_t)z * a.n_head + h) * n_split * (D + 2);
   const int per = (n_split + NP - 1) / NP;
   const int s0 = part * per, s1 = min(n_split, s0 + per);
@@ -385,8 +386,9 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
   for (int i = 0; i < PMAX; ++i) {
     const bool ok = s0 + i < s1;
     const float* rec = ph + (uint64_t)(ok ? s0 + i : 0) * (D + 2);
-    m[i] = ok ? rec[0] : -INFINITY;
-    l[i] = ok ? rec[1] : 0.0f;
+    const float2 ml = *reinterpret_cast<const float2*>(rec);  // records are 8-byte aligned
+    m[i] = ok ? ml.x : -INFINITY;
+    l[i] = ok ? ml.y : 0.0f;
     v[i] = ok ? rec[2 + d0 + j] : 0.0f;
   }
   float mx = -INFINITY;
@@ -407,7 +409,7 @@ __global__ __launch_bounds__(kBlock) void k_attn_merge(AttnArgs a, int n_split) 
   if (j == 0) pl[part] = ls;
   pacc[part][j] = acc;
   __syncthreads();
-  if (tid < 32) {
+  if (tid < DW) {
     float L = pl[0], o = pacc[0][tid];
 #pragma unroll
     for (int q = 1; q < NP; ++q) {
@@ -563,6 +565,19 @@ __global__ __launch_bounds__(kBlock) void k_prefill_rope_append(PrefillAttnArgs 
   *reinterpret_cast<uint2*>(a.v_cache + slot) = vv;
 }
 
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Four f16 of a transposed LDS read (ds_read_b64_tr_b16).  Within each group
+// of 16 lanes, lane 4q + e receives element e of the 8-byte pieces addressed
+// by lanes q, 4 + q, 8 + q and 12 + q, in that order: a 4 x 16 block of a
+// row-major matrix read one piece per lane arrives as its columns.
+__device__ __forceinline__ uint2 lds_tr16(const uint8_t* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
 // Prefill, step 2: causal attention of a tile of prompt rows.  Workgroup
 // (kv head, tile) takes 64 query columns, column = (row t0 + c / G, head
 // kvh*G + c % G), so every K/V chunk staged in LDS serves 64 queries.  Wave w
@@ -577,20 +592,32 @@ __global__ __launch_bounds__(kBlock) void k_prefill_rope_append(PrefillAttnArgs 
 //            A step's 32 reduction indices are the slots the lane already
 //            holds (32c + 4kq + i and 32c + 16 + 4kq + i), so the softmax
 //            weights feed the matrix cores without leaving the lane; the V^T
-//            operand reads the same slots from the transposed V rows.
-// Online softmax over 64-slot chunks as in the decode kernel, in base 2 (the
-// scores scaled by log2 e, the exponentials 2^x on the hardware's exp2); slot
-// s counts for the row at position qp when s <= qp.  Grid z splits the KV
+//            operand comes from V's row-major rows by transposed LDS reads.
+// K/V chunks of 64 slots reach LDS by DMA (no registers, no staging
+// arithmetic), row-major with the 16-byte slots of a row permuted by an XOR
+// of the row index, so the operand reads of 16 (K) or 8 (V) rows fall on
+// distinct banks; two stages, the next chunk's DMA in flight while the
+// current one is computed, one barrier per chunk.  Slots past the tile's last
+// position are fetched from that last position (finite values under a weight
+// of 0).  Online softmax over the chunks as in the decode kernel, in base 2
+// (the scores scaled by log2 e, the exponentials 2^x on the hardware's exp2);
+// slot s counts for the row at position qp when s <= qp.  Grid z splits the KV
 // range: split z walks chunks [z cps, (z + 1) cps) and, when there are
 // several, leaves a partial record per column for k_prefill_merge.
 template <int D>
 __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int cps) {
   constexpr int NT = kBlock, NC = 64;  // query columns: 16 per wave
-  constexpr int ROWH = D + 8;
-  constexpr int VTS = kChunk + 8;
-  auto vti = [](int d, int p) { return d * VTS + ((((p >> 3) ^ (d >> 3)) & 7) << 3) + (p & 7); };
-  __shared__ __align__(16) uint16_t ks[kChunk * ROWH];
-  __shared__ __align__(16) uint16_t vt[D * VTS];
+  constexpr int RB = 2 * D;            // bytes of one K or V row
+  constexpr int RPB = 256 / RB;        // rows per 256 bytes (the 64 banks)
+  constexpr int NSLOT = RB / 16, NPAIR = RB / 32;
+  constexpr int CB = kChunk * RB;      // bytes of one matrix's chunk
+  constexpr int NI = CB / 1024 / (NT / 64);  // 1 KB DMA instructions per wave per matrix
+  static_assert(NI >= 1 && CB % (1024 * (NT / 64)) == 0, "head_dim 64 or 128");
+  // K: 16-byte slot s of row p at s ^ (p / RPB mod NSLOT); V: 32-byte pair at
+  // pair ^ (p / RPB mod NPAIR).  Both are involutions.
+  auto kslot = [](int p, int sl) { return sl ^ ((p / RPB) & (NSLOT - 1)); };
+  auto vslot = [](int p, int sl) { return sl ^ (((p / RPB) & (NPAIR - 1)) << 1); };
+  __shared__ __align__(16) uint8_t kvs[2][2][CB];  // [stage][K, V][chunk]
   const int kvh = blockIdx.x;
   const int G = a.n_head / a.n_head_kv, QT = NC / G;
   const int t0 = blockIdx.y * QT;
@@ -604,26 +631,22 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int 
   // split z of gridDim.z walks chunks [c0, c1) of the tile's range
   const int c0 = blockIdx.z * cps;
   const int c1 = min((n_kv + kChunk - 1) / kChunk, c0 + cps);
-  const uint16_t* kc = a.k_cache + (uint64_t)kvh * a.n_ctx * D;
-  const uint16_t* vc = a.v_cache + (uint64_t)kvh * a.n_ctx * D;
-  constexpr int PER = (kChunk * D * 2) / (16 * NT);
-  static_assert(PER == 1 || PER == 2 || PER == 4, "head_dim 64 or 128");
-  uint4 k0, k1, k2, k3, v0, v1, v2, v3;
-  auto ld = [&](int p0, int j, uint4& kk, uint4& vv) {
-    const int c16 = tid + NT * j;
-    const int p = min(p0 + (c16 * 8) / D, a.n_ctx - 1), off = (c16 * 8) % D;
-    kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)p * D + off);
-    vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)p * D + off);
-  };
-  auto ld_chunk = [&](int p0) {
-    ld(p0, 0, k0, v0);
-    if constexpr (PER > 1) ld(p0, 1, k1, v1);
-    if constexpr (PER > 2) {
-      ld(p0, 2, k2, v2);
-      ld(p0, 3, k3, v3);
+  const uint8_t* kc = reinterpret_cast<const uint8_t*>(a.k_cache + (uint64_t)kvh * a.n_ctx * D);
+  const uint8_t* vc = reinterpret_cast<const uint8_t*>(a.v_cache + (uint64_t)kvh * a.n_ctx * D);
+  // wave w's DMA instruction i fills bytes (w NI + i) KB .. +1 KB of the
+  // chunk's K and V, lane l the 16 bytes at 16 l: slot sl of row p there
+  // holds the row's logical slot kslot(p, sl) (K) or vslot(p, sl) (V)
+  auto dma = [&](int p0, int st) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int o0 = (wave * NI + i) * 1024, o = o0 + 16 * lane;
+      const int p = o / RB, sl = (o % RB) / 16;
+      const uint64_t row = (uint64_t)min(p0 + p, n_kv - 1) * RB;
+      __builtin_amdgcn_global_load_lds((glb_void*)(kc + row + 16 * kslot(p, sl)), (lds_void*)(&kvs[st][0][o0]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((glb_void*)(vc + row + 16 * vslot(p, sl)), (lds_void*)(&kvs[st][1][o0]), 16, 0, 0);
     }
   };
-  if (c0 < c1) ld_chunk(c0 * kChunk);
+  if (c0 < c1) dma(c0 * kChunk, 0);
   // this lane's query column: dims 32c + 8kq .. +7 of every 32-dim step
   h16x8 qhi[D / 32], qlo[D / 32];
   const float* qrow = a.qkv + (uint64_t)t * a.qkv_stride + (uint64_t)(kvh * G + g) * D;
@@ -640,54 +663,25 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int 
 #pragma unroll
   for (int dt = 0; dt < D / 16; ++dt) acc[dt] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   for (int j = c0; j < c1; ++j) {
-    const int p0 = j * kChunk;
-    const int cnt = min(kChunk, n_kv - p0);
-    // stage the chunk: K rows, V transposed; slots past the tile's last
-    // position become zeros (a weight of 0 times a stale value stays 0)
-    // V goes in as (slot p, slot p + 1) pairs of one dim, 32 bits per write:
-    // the lanes staging slots p (even) and p + 1 hold the same 8 dims D/8
-    // lanes apart and swap half of them, the even lane then writing dims
-    // off .. off+3 and the odd lane dims off+4 .. off+7 of both slots
-    auto st = [&](int jj, const uint4& kk, const uint4& vv) {
-      const int c16 = tid + NT * jj;
-      const int p = (c16 * 8) / D, off = (c16 * 8) % D;
-      const bool dead = p >= cnt;
-      const uint4 k4 = dead ? make_uint4(0u, 0u, 0u, 0u) : kk;
-      const uint4 v4 = dead ? make_uint4(0u, 0u, 0u, 0u) : vv;
-      *reinterpret_cast<uint4*>(ks + p * ROWH + off) = k4;
-      const bool even = (p & 1) == 0;
-      auto swap = [](uint32_t x) {
-        if constexpr (D == 128) return xor16_u32(x);
-        else return dpp_u32<kDppRor8>(x);
-      };
-      const uint32_t r0 = swap(even ? v4.z : v4.x), r1 = swap(even ? v4.w : v4.y);
-      // own and partner words of the four dims this lane writes
-      const uint32_t o0 = even ? v4.x : v4.z, o1 = even ? v4.y : v4.w;
-      const uint32_t lo0 = even ? o0 : r0, hi0 = even ? r0 : o0;  // slot p&~1, slot p|1
-      const uint32_t lo1 = even ? o1 : r1, hi1 = even ? r1 : o1;
-      const int d0 = off + (even ? 0 : 4), pe = p & ~1;
-      *reinterpret_cast<uint32_t*>(vt + vti(d0, pe)) = (lo0 & 0xFFFFu) | (hi0 << 16);
-      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 1, pe)) = (lo0 >> 16) | (hi0 & 0xFFFF0000u);
-      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 2, pe)) = (lo1 & 0xFFFFu) | (hi1 << 16);
-      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 3, pe)) = (lo1 >> 16) | (hi1 & 0xFFFF0000u);
-    };
-    st(0, k0, v0);
-    if constexpr (PER > 1) st(1, k1, v1);
-    if constexpr (PER > 2) {
-      st(2, k2, v2);
-      st(3, k3, v3);
-    }
-    if (j + 1 < c1) ld_chunk(p0 + kChunk);
+    const int p0 = j * kChunk, st = (j - c0) & 1;
+    // this wave's DMA of chunk j has landed (the only loads outstanding);
+    // the barrier hands every wave's part over and also ends every wave's
+    // reads of the other stage, which the next chunk's DMA then refills
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    if (j + 1 < c1) dma(p0 + kChunk, st ^ 1);
+    const uint8_t* ks = kvs[st][0];
+    const uint8_t* vs = kvs[st][1];
     // scores of this lane's column over the chunk's 64 slots
     f32x4 sc[4];
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
       f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f};
-      const uint16_t* krow = ks + (16 * s4 + r) * ROWH + 8 * kq;
+      const int p = 16 * s4 + r;
+      const uint8_t* krow = ks + p * RB;
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
-        const h16x8 ka = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(krow + 32 * c));
+        const h16x8 ka = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(krow + 16 * kslot(p, 4 * c + kq)));
         sa = mfma16(ka, qhi[c], sa);
         sa = mfma16(ka, qlo[c], sa);
       }
@@ -730,24 +724,27 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int 
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
     }
-    // values: step c covers slots 32c + 4kq + i (j < 4) and 32c + 16 + 4kq + i
+    // values: step c covers slots 32c + 4kq + i (i < 4) and 32c + 16 + 4kq + i;
+    // lane r's transposed read takes row 32c (+16) + 4kq + r/4, dims
+    // 16dt + 4(r%4) .. +3, and receives dim 16dt + r of the four rows
+    const int pa = 4 * kq + (r >> 2), sub = 8 * (r & 3);  // row in the 16-slot step, byte in 32-dim block
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const float4 ea = make_float4(sc[2 * c][0], sc[2 * c][1], sc[2 * c][2], sc[2 * c][3]);
       const float4 eb = make_float4(sc[2 * c + 1][0], sc[2 * c + 1][1], sc[2 * c + 1][2], sc[2 * c + 1][3]);
       h16x8 eh, el;
       split_h8(ea, eb, eh, el);
+      const int pA = 32 * c + pa, pB = pA + 16;
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
-        const int d = 16 * dt + r;
-        const uint2 va = *reinterpret_cast<const uint2*>(vt + vti(d, 32 * c + 4 * kq));
-        const uint2 vb = *reinterpret_cast<const uint2*>(vt + vti(d, 32 * c + 16 + 4 * kq));
+        const int bo = 32 * dt + sub;  // byte of the piece in the row
+        const uint2 va = lds_tr16(vs + pA * RB + 16 * vslot(pA, bo >> 4) + (bo & 15));
+        const uint2 vb = lds_tr16(vs + pB * RB + 16 * vslot(pB, bo >> 4) + (bo & 15));
         const h16x8 vv = __builtin_bit_cast(h16x8, make_uint4(va.x, va.y, vb.x, vb.y));
         acc[dt] = mfma16(vv, eh, acc[dt]);
         acc[dt] = mfma16(vv, el, acc[dt]);
       }
     }
-    __syncthreads();  // the next chunk overwrites ks / vt
   }
   if (gridDim.z > 1) {
     // partial record {max, sum, sum e*v} of this column for the merge (a
@@ -829,12 +826,14 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH((k_attention<128, true>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     else
       KNJ_LAUNCH((k_attention<128, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    if (z == 1 && !a.split_hi && n_split <= 128)  // (the loads a part holds cost at short contexts)
-      KNJ_LAUNCH((k_attn_merge<128, 16>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+    // up to 128 splits: 16 dims per workgroup, 16 parts of at most 8 splits
+    // (the loads a part holds cost at short contexts)
+    if (z == 1 && !a.split_hi && n_split <= 128)
+      KNJ_LAUNCH((k_attn_merge<128, 8, 16>), dim3(a.n_head * 8, z), dim3(kBlock), 0, s, a, n_split);
     else if (z == 1 && !a.split_hi && n_split <= 256)
-      KNJ_LAUNCH((k_attn_merge<128, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+      KNJ_LAUNCH((k_attn_merge<128, 32, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
     else if (z == 1 && !a.split_hi)
-      KNJ_LAUNCH((k_attn_merge<128, 40>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
+      KNJ_LAUNCH((k_attn_merge<128, 40, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
@@ -843,11 +842,11 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     else
       KNJ_LAUNCH((k_attention<64, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     if (z == 1 && !a.split_hi && n_split <= 128)
-      KNJ_LAUNCH((k_attn_merge<64, 16>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+      KNJ_LAUNCH((k_attn_merge<64, 16, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else if (z == 1 && !a.split_hi && n_split <= 256)
-      KNJ_LAUNCH((k_attn_merge<64, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+      KNJ_LAUNCH((k_attn_merge<64, 32, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else if (z == 1 && !a.split_hi)
-      KNJ_LAUNCH((k_attn_merge<64, 40>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
+      KNJ_LAUNCH((k_attn_merge<64, 40, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
