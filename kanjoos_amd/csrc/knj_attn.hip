@@ -569,13 +569,34 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(1))) void glb_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// 32-bit LDS address of a pointer into shared memory
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
 // Four f16 of a transposed LDS read (ds_read_b64_tr_b16).  Within each group
 // of 16 lanes, lane 4q + e receives element e of the 8-byte pieces addressed
 // by lanes q, 4 + q, 8 + q and 12 + q, in that order: a 4 x 16 block of a
-// row-major matrix read one piece per lane arrives as its columns.
-__device__ __forceinline__ uint2 lds_tr16(const uint8_t* p) {
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
-  return __builtin_bit_cast(uint2, v);
+// row-major matrix read one piece per lane arrives as its columns.  Issued as
+// asm: the compiler's wait placement treats the builtin as aliasing every
+// LDS DMA in flight and would wait for the next chunk's DMA before it; the
+// caller waits for the reads itself (lds_wait8) before using the values.
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+// every LDS access of this wave complete; the eight values are tied to the
+// wait so that no use moves above it
+__device__ __forceinline__ void lds_wait8(u32x2* v) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+}
+__device__ __forceinline__ void lds_tie8(u32x2* v) {
+  asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
 }
 
 // Prefill, step 2: causal attention of a tile of prompt rows.  Workgroup
@@ -728,19 +749,26 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int 
     // lane r's transposed read takes row 32c (+16) + 4kq + r/4, dims
     // 16dt + 4(r%4) .. +3, and receives dim 16dt + r of the four rows
     const int pa = 4 * kq + (r >> 2), sub = 8 * (r & 3);  // row in the 16-slot step, byte in 32-dim block
+    // rows pa + 32c and pa + 32c + 16 share the swizzle of row pa
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       const float4 ea = make_float4(sc[2 * c][0], sc[2 * c][1], sc[2 * c][2], sc[2 * c][3]);
       const float4 eb = make_float4(sc[2 * c + 1][0], sc[2 * c + 1][1], sc[2 * c + 1][2], sc[2 * c + 1][3]);
       h16x8 eh, el;
       split_h8(ea, eb, eh, el);
-      const int pA = 32 * c + pa, pB = pA + 16;
+      const uint32_t vrow = lds_addr(vs) + (32 * c + pa) * RB + (sub & 15);
+      u32x2 va[8], vb[8];
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
-        const int bo = 32 * dt + sub;  // byte of the piece in the row
-        const uint2 va = lds_tr16(vs + pA * RB + 16 * vslot(pA, bo >> 4) + (bo & 15));
-        const uint2 vb = lds_tr16(vs + pB * RB + 16 * vslot(pB, bo >> 4) + (bo & 15));
-        const h16x8 vv = __builtin_bit_cast(h16x8, make_uint4(va.x, va.y, vb.x, vb.y));
+        const uint32_t ad = vrow + 16 * vslot(pa, (32 * dt + sub) >> 4);
+        va[dt] = lds_tr16<0>(ad);
+        vb[dt] = lds_tr16<16 * RB>(ad);
+      }
+      lds_wait8(va);
+      lds_tie8(vb);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        const h16x8 vv = __builtin_bit_cast(h16x8, make_uint4(va[dt].x, va[dt].y, vb[dt].x, vb[dt].y));
         acc[dt] = mfma16(vv, eh, acc[dt]);
         acc[dt] = mfma16(vv, el, acc[dt]);
       }
