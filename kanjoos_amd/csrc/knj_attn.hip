@@ -83,26 +83,92 @@ __device__ __forceinline__ void split_h8(const float4& p, const float4& q, h16x8
 }
 
 
-// SMALL_FIRST: the query/key/value, norm and RoPE loads before the first
-// chunk's, so the query preparation overlaps the chunk's fetch (measured: one
-// or two chunks per workgroup 1-3% faster per step; three, at 32K slots, 2%
-// slower than the chunk first)
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(1))) void glb_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// 32-bit LDS address of a pointer into shared memory
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Four f16 of a transposed LDS read (ds_read_b64_tr_b16).  Within each group
+// of 16 lanes, lane 4q + e receives element e of the 8-byte pieces addressed
+// by lanes q, 4 + q, 8 + q and 12 + q, in that order: a 4 x 16 block of a
+// row-major matrix read one piece per lane arrives as its columns.  Issued as
+// asm: the compiler's wait placement treats the builtin as aliasing every
+// LDS DMA in flight and would wait for the next chunk's DMA before it; the
+// caller waits for the reads itself (lds_wait8) before using the values.
+template <int OFF>
+__device__ __forceinline__ u32x2 lds_tr16(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+// every LDS access of this wave complete; the eight values are tied to the
+// wait so that no use moves above it
+__device__ __forceinline__ void lds_wait8(u32x2* v) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+}
+__device__ __forceinline__ void lds_tie8(u32x2* v) {
+  asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
+}
+
+// s_waitcnt immediates (gfx9 encoding): at most n vector memory operations
+// of this wave outstanding and every LDS access complete; LDS only
+constexpr int vm_lds_imm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4); }
+constexpr int kLdsOnly = vm_lds_imm(63);
+// Workgroup barrier after the wait `imm`.  __syncthreads() is a release fence
+// plus the barrier and the fence waits for every LDS DMA in flight, which
+// would drain the next chunk's fetch at every barrier of a chunk; the asm's
+// memory clobber keeps the compiler from moving memory accesses across it.
+#define KNJ_ATTN_BARRIER(imm)                 \
+  do {                                        \
+    __builtin_amdgcn_s_waitcnt(imm);          \
+    __builtin_amdgcn_sched_barrier(0);        \
+    asm volatile("s_barrier" ::: "memory");   \
+    __builtin_amdgcn_sched_barrier(0);        \
+  } while (0)
+
+// Decode attention of one new token per sequence: workgroup (kv head, split
+// of the KV range, sequence).  The G query heads of the kv head are
+// normalised and rotated in LDS; per 64-slot chunk, the scores on the matrix
+// cores (wave w: slots 16w .. 16w+15 against the heads), an online softmax
+// per head (wave w: heads 2w, 2w+1, lane = slot), and the values on the
+// matrix cores (wave w: dims 32w .. 32w+31).  K/V chunks reach LDS by DMA
+// (39 KB of LDS: four workgroups per CU), row-major with the 16-byte slots of
+// a row XOR-permuted by the row index as in the prompt kernel; one stage, the
+// next chunk's K fetched once the scores are written and its V once the
+// value products are done.  The step's key/value row is written to the cache
+// after the loop (no fetch of this launch reads it); the workgroup holding
+// it writes it into the staged chunk and zeroes the V rows past it (slots
+// past the valid length under a weight of 0).  SMALL_FIRST: the
+// query/key/value, norm and RoPE loads before the first chunk's DMA, so the
+// query preparation overlaps the chunk's fetch (measured: one or two chunks
+// per workgroup 1-3% faster per step; three, at 32K slots, 2% slower than
+// the chunk first)
 template <int D, bool SMALL_FIRST>
 __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
-  constexpr int ROWH = D + 8;            // f16 elements per K/V LDS row (16-byte pad)
+  constexpr int ROWH = D + 8;            // f16 elements per query LDS row (16-byte pad)
   constexpr int EROW = kChunk + 4;       // floats per score row
   constexpr int T = D / 4;               // threads per head for the q pass
-  constexpr int VTS = kChunk + 8;         // f16 elements per transposed V row (one dim)
-  // slot p of dim d sits in 8-slot block (p / 8) ^ ((d / 8) % 8) of the row, so
-  // the staging writes of consecutive dims spread over the banks while the
-  // matrix-core reads still take 8 consecutive slots
-  auto vti = [](int d, int p) { return d * VTS + ((((p >> 3) ^ (d >> 3)) & 7) << 3) + (p & 7); };
+  constexpr int RB = 2 * D, RPB = 256 / RB, NSLOT = RB / 16, NPAIR = RB / 32;
+  constexpr int CB = kChunk * RB;        // bytes of one matrix's chunk
+  constexpr int NI = CB / 1024 / (kBlock / 64);  // 1 KB DMA instructions per wave per matrix
+  static_assert(NI >= 1 && CB % (1024 * (kBlock / 64)) == 0, "head_dim 64 or 128");
+  auto kslot = [](int p, int sl) { return sl ^ ((p / RPB) & (NSLOT - 1)); };
+  auto vslot = [](int p, int sl) { return sl ^ (((p / RPB) & (NPAIR - 1)) << 1); };
+  // (the staged chunks in the dynamic array, the rest in objects of their
+  // own, so that the compiler sees their accesses apart from the DMA's)
   __shared__ __align__(16) _Float16 qh[8 * ROWH];  // normalised, rotated queries: f16 high parts
   __shared__ __align__(16) _Float16 ql[8 * ROWH];  // and remainders
-  __shared__ __align__(16) uint16_t ks[kChunk * ROWH];
-  __shared__ __align__(16) uint16_t vt[D * VTS];    // V transposed: vt[dim][slot]
-  __shared__ float es[8 * EROW];         // scores, then exp(score - running max), per head
-  __shared__ float alpha[16];            // per head: rescale of the running sums this chunk
+  __shared__ __align__(16) float es[8 * EROW];     // scores, then exp(score - running max), per head
+  __shared__ float alpha[16];                      // per head: rescale of the running sums this chunk
+  __shared__ __align__(16) uint8_t ks[CB];          // the chunk's K rows
+  __shared__ __align__(16) uint8_t vs[CB];          // and V rows
   const int kvh = blockIdx.x, split = blockIdx.y, n_split = gridDim.y;
   const int G = a.n_head / a.n_head_kv;
   KNJ_STAMP(0);
@@ -119,30 +185,25 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   const float* rc = a.rope_cos + (uint64_t)z * a.rope_stride;
   const float* rs = a.rope_sin + (uint64_t)z * a.rope_stride;
   const uint64_t hstride = (uint64_t)n_split * (D + 2);
-  // 1) every load that does not depend on the position first: the raw
-  // query/key/value, the norm weights and the RoPE row and the first chunk's
-  // cache slots (16 bytes per load; rows past the valid length are dropped
-  // later), in the order SMALL_FIRST picks
-  constexpr int PER = (kChunk * D * 2) / (16 * kBlock);  // loads per thread per matrix
-  static_assert(PER == 2 || PER == 4, "head_dim 64 or 128");
-  // (named registers rather than an array: an array live across the query
-  // pass below was placed in scratch memory)
-  uint4 k0, k1, k2, k3, v0, v1, v2, v3;
-  auto ld = [&](int p0, int j, uint4& kk, uint4& vv) {
-    const int c16 = tid + kBlock * j;
-    const int p = min(p0 + (c16 * 8) / D, a.n_ctx - 1), off = (c16 * 8) % D;
-    kk = *reinterpret_cast<const uint4*>(kc + (uint64_t)p * D + off);
-    vv = *reinterpret_cast<const uint4*>(vc + (uint64_t)p * D + off);
-  };
-  auto ld_chunk = [&](int p0) {
-    ld(p0, 0, k0, v0);
-    ld(p0, 1, k1, v1);
-    if constexpr (PER > 2) {
-      ld(p0, 2, k2, v2);
-      ld(p0, 3, k3, v3);
+  // wave w's DMA instruction i fills bytes (w NI + i) KB .. +1 KB of the
+  // chunk's K and V (rows past the cache clamp to its last row)
+  const uint8_t* kcb = reinterpret_cast<const uint8_t*>(kc);
+  const uint8_t* vcb = reinterpret_cast<const uint8_t*>(vc);
+  auto dma = [&](int p0, bool k, bool v) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int o0 = (wave * NI + i) * 1024, o = o0 + 16 * lane;
+      const int p = o / RB, sl = (o % RB) / 16;
+      const uint64_t row = (uint64_t)min(p0 + p, a.n_ctx - 1) * RB;
+      if (k) __builtin_amdgcn_global_load_lds((glb_void*)(kcb + row + 16 * kslot(p, sl)), (lds_void*)(ks + o0), 16, 0, 0);
+      if (v) __builtin_amdgcn_global_load_lds((glb_void*)(vcb + row + 16 * vslot(p, sl)), (lds_void*)(vs + o0), 16, 0, 0);
     }
   };
-  if constexpr (!SMALL_FIRST) ld_chunk(c0 * kChunk);
+  // 1) every load that does not depend on the position first: the raw
+  // query/key/value, the norm weights and the RoPE row and the first chunk's
+  // DMA, in the order SMALL_FIRST picks
+  auto dma_first = [&]() { dma(c0 * kChunk, true, true); };
+  if constexpr (!SMALL_FIRST) dma_first();
   const int qhd = min(tid / T, G - 1), qc = tid % T;
   const float4 qraw = *reinterpret_cast<const float4*>(qz + (uint64_t)(kvh * G + qhd) * D + 4 * qc);
   const float4 qnw = *reinterpret_cast<const float4*>(a.q_norm + 4 * qc);
@@ -154,10 +215,10 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   const float4 sn = *reinterpret_cast<const float4*>(rs + ri);
   const int pos = a.pos[z];
   if constexpr (SMALL_FIRST) {
-    // the first chunk's slots after the small loads: the memory counter is in
-    // order, so the query/key preparation below waits only for those
+    // the chunk DMA after the small loads: the memory counter is in order, so
+    // the query/key preparation below waits only for those
     __builtin_amdgcn_sched_barrier(0);
-    ld_chunk(c0 * kChunk);
+    dma_first();
   }
   const int n_kv = pos + 1;
   const int nch = min(cpw, (n_kv - c0 * kChunk + kChunk - 1) / kChunk);  // chunks holding slots
@@ -168,6 +229,7 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
       const int g = i / (D + 2), j = i % (D + 2);
       *(part + g * hstride + j) = (j == 0) ? -INFINITY : 0.0f;
     }
+    __builtin_amdgcn_s_waitcnt(0);  // the fetch lands before the workgroup ends
     return;
   }
   // 2) queries of this kv head: 4 floats per thread, T threads per head
@@ -181,12 +243,13 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
       ql[qhd * ROWH + 4 * qc + i] = (_Float16)(rv[i] - (float)h);
     }
   }
-  // the key of this step (written to its slot below, in the chunk holding it)
-  uint16_t kh[4] = {0, 0, 0, 0}, vh[4] = {0, 0, 0, 0};
+  // the key/value of this step as f16 (cache and staged chunk)
+  uint2 kh2 = make_uint2(0u, 0u), vh2 = make_uint2(0u, 0u);
   if (tid < T) {
     const float4 r = norm_rope4<D>(kraw, tid, knw, a.eps, cs, sn);
-    kh[0] = f2h(r.x); kh[1] = f2h(r.y); kh[2] = f2h(r.z); kh[3] = f2h(r.w);
-    vh[0] = f2h(vraw.x); vh[1] = f2h(vraw.y); vh[2] = f2h(vraw.z); vh[3] = f2h(vraw.w);
+    kh2 = make_uint2((uint32_t)f2h(r.x) | ((uint32_t)f2h(r.y) << 16), (uint32_t)f2h(r.z) | ((uint32_t)f2h(r.w) << 16));
+    vh2 = make_uint2((uint32_t)f2h(vraw.x) | ((uint32_t)f2h(vraw.y) << 16),
+                     (uint32_t)f2h(vraw.z) | ((uint32_t)f2h(vraw.w) << 16));
   }
   const int r = lane & 15, kq = lane >> 4;
   const bool hv = r < G;
@@ -199,80 +262,37 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   for (int j = 0; j < nch; ++j) {
     const int p0 = (c0 + j) * kChunk;
     const int cnt = min(kChunk, n_kv - p0);
-    // 3) the slot written this step goes to the cache now; in LDS it is
-    // written over the staged chunk below
-    const bool here = pos >= p0 && pos < p0 + cnt;  // uniform
-    if (here && tid < T) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        kc[(uint64_t)pos * D + 4 * tid + k] = kh[k];
-        vc[(uint64_t)pos * D + 4 * tid + k] = vh[k];
-      }
-    }
+    // 3) chunk j has landed; the barrier also hands the query rows over on
+    // the first pass
+    KNJ_ATTN_BARRIER(vm_lds_imm(0));
     KNJ_STAMP(2);
-    // cache rows past the valid length become zeros: the value product below
-    // runs over all 64 rows with weight 0 there.  V goes in as (slot p, slot
-    // p + 1) pairs of one dim, 32 bits per write: the lanes staging slots p
-    // (even) and p + 1 hold the same 8 dims D/8 lanes apart and swap half of
-    // them, the even lane then writing dims off .. off+3 and the odd lane dims
-    // off+4 .. off+7 of both slots
-    auto st = [&](int jj, const uint4& kk, const uint4& vv) {
-      const int c16 = tid + kBlock * jj;
-      const int p = (c16 * 8) / D, off = (c16 * 8) % D;
-      const bool dead = p >= cnt;
-      const uint4 k4 = dead ? make_uint4(0u, 0u, 0u, 0u) : kk;
-      const uint4 v4 = dead ? make_uint4(0u, 0u, 0u, 0u) : vv;
-      *reinterpret_cast<uint4*>(ks + p * ROWH + off) = k4;
-      const bool even = (p & 1) == 0;
-      auto swap = [](uint32_t x) {
-        if constexpr (D == 128) return xor16_u32(x);
-        else return dpp_u32<kDppRor8>(x);
-      };
-      const uint32_t r0 = swap(even ? v4.z : v4.x), r1 = swap(even ? v4.w : v4.y);
-      const uint32_t o0 = even ? v4.x : v4.z, o1 = even ? v4.y : v4.w;
-      const uint32_t lo0 = even ? o0 : r0, hi0 = even ? r0 : o0;  // slot p&~1, slot p|1
-      const uint32_t lo1 = even ? o1 : r1, hi1 = even ? r1 : o1;
-      const int d0 = off + (even ? 0 : 4), pe = p & ~1;
-      *reinterpret_cast<uint32_t*>(vt + vti(d0, pe)) = (lo0 & 0xFFFFu) | (hi0 << 16);
-      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 1, pe)) = (lo0 >> 16) | (hi0 & 0xFFFF0000u);
-      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 2, pe)) = (lo1 & 0xFFFFu) | (hi1 << 16);
-      *reinterpret_cast<uint32_t*>(vt + vti(d0 + 3, pe)) = (lo1 >> 16) | (hi1 & 0xFFFF0000u);
-    };
-    st(0, k0, v0);
-    st(1, k1, v1);
-    if constexpr (PER > 2) {
-      st(2, k2, v2);
-      st(3, k3, v3);
-    }
+    const bool here = pos >= p0 && pos < p0 + kChunk;  // uniform
     if (here) {
-      // the staged copy of slot pos (the cache's value before this step) is
-      // replaced once every lane's pair write has landed
-      __syncthreads();
+      // the step's row replaces the fetched one (fetched before this step's
+      // write), and V rows past it become zeros
+      const int lp = pos - p0;
       if (tid < T) {
-        const int lp = pos - p0;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          ks[lp * ROWH + 4 * tid + k] = kh[k];
-          vt[vti(4 * tid + k, lp)] = vh[k];
-        }
+        *reinterpret_cast<uint2*>(ks + lp * RB + 16 * kslot(lp, tid >> 1) + 8 * (tid & 1)) = kh2;
+        *reinterpret_cast<uint2*>(vs + lp * RB + 16 * vslot(lp, tid >> 1) + 8 * (tid & 1)) = vh2;
       }
+      for (int o = (lp + 1) * RB + 16 * tid; o < CB; o += 16 * kBlock)
+        *reinterpret_cast<uint4*>(vs + o) = make_uint4(0u, 0u, 0u, 0u);
+      KNJ_ATTN_BARRIER(kLdsOnly);
     }
-    // the next chunk's slots load while this one is computed
-    if (j + 1 < nch) ld_chunk(p0 + kChunk);
-    __syncthreads();
     KNJ_STAMP(3);
     // 4) scores on the matrix cores: wave w computes S[p][h] for the 16 slots
     // 16w..16w+15 (rows) and the query heads (columns, zero past G).  Lane
-    // (r = l%16, kq = l/16) contributes dims kq*D/4 .. kq*D/4 + D/4 - 1.
+    // (r = l%16, kq = l/16) contributes dims 8kq .. 8kq+7 of each 32.
     {
       // A = K (16 slots x 32 dims per step), B = the queries (hi, then lo)
-      const uint16_t* krow = ks + (16 * wave + r) * ROWH + 8 * kq;
+      const int p = 16 * wave + r;
+      const uint8_t* krow = ks + p * RB;
       const int hq = min(r, G - 1);
       const h16x8 zero8 = {};
       f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
-        const h16x8 ka = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(krow + 32 * c));
+        const h16x8 ka = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(krow + 16 * kslot(p, 4 * c + kq)));
         const h16x8 bh = hv ? *reinterpret_cast<const h16x8*>(qh + hq * ROWH + 32 * c + 8 * kq) : zero8;
         const h16x8 bl = hv ? *reinterpret_cast<const h16x8*>(ql + hq * ROWH + 32 * c + 8 * kq) : zero8;
         sa = mfma16(ka, bh, sa);
@@ -283,7 +303,9 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
         for (int i = 0; i < 4; ++i) es[r * EROW + 16 * wave + 4 * kq + i] = sa[i] * scale2;
       }
     }
-    __syncthreads();
+    KNJ_ATTN_BARRIER(kLdsOnly);
+    // every wave's K reads are done: the next chunk's K
+    if (j + 1 < nch) dma(p0 + kChunk, true, false);
     // 5) online softmax of the chunk: wave w owns heads 2w, 2w+1; lane = slot
     if (h0 < G) {
       const float s0 = lane < cnt ? es[h0 * EROW + lane] : -INFINITY;
@@ -303,16 +325,16 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
         if (h1 < G) alpha[h1] = a1;
       }
     }
-    __syncthreads();
+    KNJ_ATTN_BARRIER(kLdsOnly);
     KNJ_STAMP(4);
     // 6) sum e*v on the matrix cores: O[h][d] over the 64 slots.  Wave w owns
-    // dims 32w .. 32w+31 as two column tiles, even dims and odd dims, so one
-    // 32-bit LDS read feeds both; lane (r, kq) contributes slots kq*16 .. +15.
+    // dims 32w .. 32w+31 as two 16-column tiles; step c's 32 reduction
+    // indices of lane (r, kq) are slots 32c + 4kq + i and 32c + 16 + 4kq + i
+    // (i < 4): A = e (heads x slots, hi then lo), B = V (slots x 16 dims) by
+    // transposed reads of rows 32c (+16) + 4kq + r/4, dims 4(r%4) .. +3 of
+    // the tile, which deliver dim r of the four rows
     if (32 * wave < D) {
-      // A = e (heads x 32 slots per step, hi then lo), B = V (32 slots x 16
-      // dims) from the transposed rows; wave w owns dims 32w .. 32w + 31 as
-      // two 16-column tiles
-      const float* erow = es + min(r, G - 1) * EROW + 8 * kq;
+      const float* erow = es + min(r, G - 1) * EROW + 4 * kq;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = 4 * kq + i;
@@ -320,27 +342,49 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
         oe[i] *= al;
         oo[i] *= al;
       }
+      const int pa = 4 * kq + (r >> 2), sub = 8 * (r & 3);
+      // rows pa + 32c and pa + 32c + 16 share the swizzle of row pa
+      const uint32_t vrow = lds_addr(vs) + pa * RB + (sub & 15);
+      const uint32_t ad0 = vrow + 16 * vslot(pa, (64 * wave + sub) >> 4);
+      const uint32_t ad1 = vrow + 16 * vslot(pa, (64 * wave + 32 + sub) >> 4);
+      u32x2 vv[8];
+      vv[0] = lds_tr16<0>(ad0);
+      vv[1] = lds_tr16<16 * RB>(ad0);
+      vv[2] = lds_tr16<0>(ad1);
+      vv[3] = lds_tr16<16 * RB>(ad1);
+      vv[4] = lds_tr16<32 * RB>(ad0);
+      vv[5] = lds_tr16<48 * RB>(ad0);
+      vv[6] = lds_tr16<32 * RB>(ad1);
+      vv[7] = lds_tr16<48 * RB>(ad1);
+      lds_wait8(vv);
 #pragma unroll
       for (int c = 0; c < kChunk / 32; ++c) {
         const float4 e0 = *reinterpret_cast<const float4*>(erow + 32 * c);
-        const float4 e1 = *reinterpret_cast<const float4*>(erow + 32 * c + 4);
+        const float4 e1 = *reinterpret_cast<const float4*>(erow + 32 * c + 16);
         h16x8 eh, el;
         split_h8(e0, e1, eh, el);
         if (!hv) {
           eh = h16x8{};
           el = h16x8{};
         }
-        const h16x8 v0 = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(vt + vti(32 * wave + r, 32 * c + 8 * kq)));
-        const h16x8 v1 = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(vt + vti(32 * wave + 16 + r, 32 * c + 8 * kq)));
+        const h16x8 v0 = __builtin_bit_cast(h16x8, make_uint4(vv[4 * c].x, vv[4 * c].y, vv[4 * c + 1].x, vv[4 * c + 1].y));
+        const h16x8 v1 = __builtin_bit_cast(h16x8, make_uint4(vv[4 * c + 2].x, vv[4 * c + 2].y, vv[4 * c + 3].x, vv[4 * c + 3].y));
         oe = mfma16(eh, v0, oe);
         oe = mfma16(el, v0, oe);
         oo = mfma16(eh, v1, oo);
         oo = mfma16(el, v1, oo);
       }
     }
-    __syncthreads();  // the next chunk overwrites ks/vs/es
+    // every wave is done with V and es: the next chunk's V
+    KNJ_ATTN_BARRIER(kLdsOnly);
+    if (j + 1 < nch) dma(p0 + kChunk, false, true);
   }
-  // 7) the partial record {max, sum, sum e*v} of each head
+  // 7) the step's row to the cache, by the workgroup that holds it
+  if (pos >= c0 * kChunk && pos < (c0 + nch) * kChunk && tid < T) {
+    *reinterpret_cast<uint2*>(kc + (uint64_t)pos * D + 4 * tid) = kh2;
+    *reinterpret_cast<uint2*>(vc + (uint64_t)pos * D + 4 * tid) = vh2;
+  }
+  // 8) the partial record {max, sum, sum e*v} of each head
   if (h0 < G && lane == 0) {
     *(part + h0 * hstride + 0) = m0;
     *(part + h0 * hstride + 1) = l0;
@@ -563,40 +607,6 @@ __global__ __launch_bounds__(kBlock) void k_prefill_rope_append(PrefillAttnArgs 
   vv.y = (uint32_t)f2h(v.z) | ((uint32_t)f2h(v.w) << 16);
   *reinterpret_cast<uint2*>(a.k_cache + slot) = kk;
   *reinterpret_cast<uint2*>(a.v_cache + slot) = vv;
-}
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(1))) void glb_void;
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-
-typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-
-// 32-bit LDS address of a pointer into shared memory
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-
-// Four f16 of a transposed LDS read (ds_read_b64_tr_b16).  Within each group
-// of 16 lanes, lane 4q + e receives element e of the 8-byte pieces addressed
-// by lanes q, 4 + q, 8 + q and 12 + q, in that order: a 4 x 16 block of a
-// row-major matrix read one piece per lane arrives as its columns.  Issued as
-// asm: the compiler's wait placement treats the builtin as aliasing every
-// LDS DMA in flight and would wait for the next chunk's DMA before it; the
-// caller waits for the reads itself (lds_wait8) before using the values.
-template <int OFF>
-__device__ __forceinline__ u32x2 lds_tr16(uint32_t addr) {
-  u32x2 v;
-  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
-  return v;
-}
-// every LDS access of this wave complete; the eight values are tied to the
-// wait so that no use moves above it
-__device__ __forceinline__ void lds_wait8(u32x2* v) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
-}
-__device__ __forceinline__ void lds_tie8(u32x2* v) {
-  asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
 }
 
 // Prefill, step 2: causal attention of a tile of prompt rows.  Workgroup
@@ -831,11 +841,11 @@ __global__ __launch_bounds__(kBlock) void k_prefill_merge(PrefillAttnArgs a, int
 int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
 
 // splits of one head: one 64-slot chunk per workgroup up to kMaxSplit1
-// chunks at one sequence (the merge folds 8 parts x 40 splits; measured at 32K
-// slots, 256 splits of 2-3 chunks beat 128 of 4-5 by 2% per token, and the
-// 40-split parts keep 2 chunks per workgroup just past 32768 slots), up to
-// kMaxSplit with several sequences (the per-head merge)
-constexpr int kMaxSplit = 256, kMaxSplit1 = 320;
+// chunks at one sequence, several chunks per workgroup beyond (measured at
+// 32,770 slots: 171 splits of 3 chunks, 684 workgroups all resident at four
+// per CU, 2.545 ms/token against 2.60 for 257 splits of 2 and 2.61 for 103 of
+// 5), up to kMaxSplit with several sequences (the per-head merge)
+constexpr int kMaxSplit = 256, kMaxSplit1 = 171;
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   // one 64-slot chunk per workgroup up to kMaxSplit chunks; beyond, several
@@ -860,8 +870,6 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH((k_attn_merge<128, 8, 16>), dim3(a.n_head * 8, z), dim3(kBlock), 0, s, a, n_split);
     else if (z == 1 && !a.split_hi && n_split <= 256)
       KNJ_LAUNCH((k_attn_merge<128, 32, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
-    else if (z == 1 && !a.split_hi)
-      KNJ_LAUNCH((k_attn_merge<128, 40, 32>), dim3(a.n_head * 4, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
@@ -873,8 +881,6 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
       KNJ_LAUNCH((k_attn_merge<64, 16, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else if (z == 1 && !a.split_hi && n_split <= 256)
       KNJ_LAUNCH((k_attn_merge<64, 32, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
-    else if (z == 1 && !a.split_hi)
-      KNJ_LAUNCH((k_attn_merge<64, 40, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else
       KNJ_LAUNCH(k_attn_merge_head<64>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else {
