@@ -145,12 +145,10 @@ constexpr int kLdsOnly = vm_lds_imm(63);
 // value products are done.  The step's key/value row is written to the cache
 // after the loop (no fetch of this launch reads it); the workgroup holding
 // it writes it into the staged chunk and zeroes the V rows past it (slots
-// past the valid length under a weight of 0).  SMALL_FIRST: the
-// query/key/value, norm and RoPE loads before the first chunk's DMA, so the
-// query preparation overlaps the chunk's fetch (measured: one or two chunks
-// per workgroup 1-3% faster per step; three, at 32K slots, 2% slower than
-// the chunk first)
-template <int D, bool SMALL_FIRST>
+// past the valid length under a weight of 0).  The query/key/value, norm and
+// RoPE loads are issued before the first chunk's DMA (measured 1-3% faster
+// per step than the chunk first).
+template <int D>
 __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   constexpr int ROWH = D + 8;            // f16 elements per query LDS row (16-byte pad)
   constexpr int EROW = kChunk + 4;       // floats per score row
@@ -200,10 +198,8 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
     }
   };
   // 1) every load that does not depend on the position first: the raw
-  // query/key/value, the norm weights and the RoPE row and the first chunk's
-  // DMA, in the order SMALL_FIRST picks
-  auto dma_first = [&]() { dma(c0 * kChunk, true, true); };
-  if constexpr (!SMALL_FIRST) dma_first();
+  // query/key/value, the norm weights and the RoPE row, then the first
+  // chunk's DMA
   const int qhd = min(tid / T, G - 1), qc = tid % T;
   const float4 qraw = *reinterpret_cast<const float4*>(qz + (uint64_t)(kvh * G + qhd) * D + 4 * qc);
   const float4 qnw = *reinterpret_cast<const float4*>(a.q_norm + 4 * qc);
@@ -214,12 +210,8 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   const float4 cs = *reinterpret_cast<const float4*>(rc + ri);
   const float4 sn = *reinterpret_cast<const float4*>(rs + ri);
   const int pos = a.pos[z];
-  if constexpr (SMALL_FIRST) {
-    // the chunk DMA after the small loads: the memory counter is in order, so
-    // the query/key preparation below waits only for those
-    __builtin_amdgcn_sched_barrier(0);
-    dma_first();
-  }
+  __builtin_amdgcn_sched_barrier(0);
+  dma(c0 * kChunk, true, true);
   const int n_kv = pos + 1;
   const int nch = min(cpw, (n_kv - c0 * kChunk + kChunk - 1) / kChunk);  // chunks holding slots
   KNJ_STAMP(1);
@@ -860,10 +852,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   if (n_split > max_split) return hipErrorInvalidValue;
   const int z = std::max(1, a.n_seq);
   if (a.head_dim == 128) {
-    if (cpw <= 2)
-      KNJ_LAUNCH((k_attention<128, true>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    else
-      KNJ_LAUNCH((k_attention<128, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
+    KNJ_LAUNCH(k_attention<128>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     // up to 128 splits: 16 dims per workgroup, 16 parts of at most 8 splits
     // (the loads a part holds cost at short contexts)
     if (z == 1 && !a.split_hi && n_split <= 128)
@@ -873,10 +862,7 @@ hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
     else
       KNJ_LAUNCH(k_attn_merge_head<128>, dim3(a.n_head, z), dim3(kBlock), 0, s, a, n_split);
   } else if (a.head_dim == 64) {
-    if (cpw <= 2)
-      KNJ_LAUNCH((k_attention<64, true>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
-    else
-      KNJ_LAUNCH((k_attention<64, false>), dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
+    KNJ_LAUNCH(k_attention<64>, dim3(a.n_head_kv, n_split, z), dim3(kBlock), 0, s, a, cpw);
     if (z == 1 && !a.split_hi && n_split <= 128)
       KNJ_LAUNCH((k_attn_merge<64, 16, 32>), dim3(a.n_head * 2, z), dim3(kBlock), 0, s, a, n_split);
     else if (z == 1 && !a.split_hi && n_split <= 256)
