@@ -113,6 +113,18 @@ __device__ __forceinline__ void lds_wait8(u32x2* v) {
   asm volatile("s_waitcnt lgkmcnt(0)"
                : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
 }
+// LDS DMA of 16 bytes per lane (global_load_lds_dwordx4) by asm: lane l's
+// 16 bytes from g land at LDS address base + 16 l (base wave-uniform).  The
+// compiler's wait placement treats every LDS access after a DMA it knows of
+// as aliasing it and waits for all of them; a kernel using this form waits
+// for its DMA itself (vmcnt; in-order) before the barriers that hand the
+// rows over, and the compiler's own counts only grow stricter by it.  M0 is
+// reserved to the compiler, which sets it right before each of its own uses
+// and keeps no value in it across this asm.
+__device__ __forceinline__ void dma16(const void* g, uint32_t base) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(base) : "memory");
+}
+
 __device__ __forceinline__ void lds_tie8(u32x2* v) {
   asm volatile("" : "+v"(v[0]), "+v"(v[1]), "+v"(v[2]), "+v"(v[3]), "+v"(v[4]), "+v"(v[5]), "+v"(v[6]), "+v"(v[7]));
 }
@@ -142,14 +154,16 @@ constexpr int kLdsOnly = vm_lds_imm(63);
 // (39 KB of LDS: four workgroups per CU), row-major with the 16-byte slots of
 // a row XOR-permuted by the row index as in the prompt kernel; one stage, the
 // next chunk's K fetched once the scores are written and its V once the
-// value products are done.  The step's key/value row is written to the cache
+// value products are done; each barrier waits only for the rows it hands
+// over (K at the chunk's start, V before the value products).  The step's
+// key/value row is written to the cache
 // after the loop (no fetch of this launch reads it); the workgroup holding
 // it writes it into the staged chunk and zeroes the V rows past it (slots
 // past the valid length under a weight of 0).  The query/key/value, norm and
 // RoPE loads are issued before the first chunk's DMA (measured 1-3% faster
 // per step than the chunk first).
 template <int D>
-__global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
+__global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) {  // 4 waves per SIMD: 128 VGPRs
   constexpr int ROWH = D + 8;            // f16 elements per query LDS row (16-byte pad)
   constexpr int EROW = kChunk + 4;       // floats per score row
   constexpr int T = D / 4;               // threads per head for the q pass
@@ -193,8 +207,8 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
       const int o0 = (wave * NI + i) * 1024, o = o0 + 16 * lane;
       const int p = o / RB, sl = (o % RB) / 16;
       const uint64_t row = (uint64_t)min(p0 + p, a.n_ctx - 1) * RB;
-      if (k) __builtin_amdgcn_global_load_lds((glb_void*)(kcb + row + 16 * kslot(p, sl)), (lds_void*)(ks + o0), 16, 0, 0);
-      if (v) __builtin_amdgcn_global_load_lds((glb_void*)(vcb + row + 16 * vslot(p, sl)), (lds_void*)(vs + o0), 16, 0, 0);
+      if (k) dma16(kcb + row + 16 * kslot(p, sl), __builtin_amdgcn_readfirstlane(lds_addr(ks + o0)));
+      if (v) dma16(vcb + row + 16 * vslot(p, sl), __builtin_amdgcn_readfirstlane(lds_addr(vs + o0)));
     }
   };
   // 1) every load that does not depend on the position first: the raw
@@ -211,7 +225,8 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   const float4 sn = *reinterpret_cast<const float4*>(rs + ri);
   const int pos = a.pos[z];
   __builtin_amdgcn_sched_barrier(0);
-  dma(c0 * kChunk, true, true);
+  dma(c0 * kChunk, true, false);  // all of K, then all of V: the counter is in order
+  dma(c0 * kChunk, false, true);
   const int n_kv = pos + 1;
   const int nch = min(cpw, (n_kv - c0 * kChunk + kChunk - 1) / kChunk);  // chunks holding slots
   KNJ_STAMP(1);
@@ -254,21 +269,15 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
   for (int j = 0; j < nch; ++j) {
     const int p0 = (c0 + j) * kChunk;
     const int cnt = min(kChunk, n_kv - p0);
-    // 3) chunk j has landed; the barrier also hands the query rows over on
-    // the first pass
-    KNJ_ATTN_BARRIER(vm_lds_imm(0));
+    // 3) chunk j's K has landed (its V, fetched after it, may still be in
+    // flight); the barrier also hands the query rows over on the first pass
+    KNJ_ATTN_BARRIER(vm_lds_imm(NI));
     KNJ_STAMP(2);
     const bool here = pos >= p0 && pos < p0 + kChunk;  // uniform
+    const int lp = pos - p0;
     if (here) {
-      // the step's row replaces the fetched one (fetched before this step's
-      // write), and V rows past it become zeros
-      const int lp = pos - p0;
-      if (tid < T) {
-        *reinterpret_cast<uint2*>(ks + lp * RB + 16 * kslot(lp, tid >> 1) + 8 * (tid & 1)) = kh2;
-        *reinterpret_cast<uint2*>(vs + lp * RB + 16 * vslot(lp, tid >> 1) + 8 * (tid & 1)) = vh2;
-      }
-      for (int o = (lp + 1) * RB + 16 * tid; o < CB; o += 16 * kBlock)
-        *reinterpret_cast<uint4*>(vs + o) = make_uint4(0u, 0u, 0u, 0u);
+      // the step's key replaces the fetched row (fetched before this step's write)
+      if (tid < T) *reinterpret_cast<uint2*>(ks + lp * RB + 16 * kslot(lp, tid >> 1) + 8 * (tid & 1)) = kh2;
       KNJ_ATTN_BARRIER(kLdsOnly);
     }
     KNJ_STAMP(3);
@@ -317,7 +326,17 @@ __global__ __launch_bounds__(kBlock) void k_attention(AttnArgs a, int cpw) {
         if (h1 < G) alpha[h1] = a1;
       }
     }
-    KNJ_ATTN_BARRIER(kLdsOnly);
+    // chunk j's V has landed (the next chunk's K may stay in flight)
+    if (j + 1 < nch) KNJ_ATTN_BARRIER(vm_lds_imm(NI));
+    else KNJ_ATTN_BARRIER(vm_lds_imm(0));
+    if (here) {
+      // the step's value replaces the fetched row, and the rows past it
+      // become zeros (finite under their weight of 0)
+      if (tid < T) *reinterpret_cast<uint2*>(vs + lp * RB + 16 * vslot(lp, tid >> 1) + 8 * (tid & 1)) = vh2;
+      for (int o = (lp + 1) * RB + 16 * tid; o < CB; o += 16 * kBlock)
+        *reinterpret_cast<uint4*>(vs + o) = make_uint4(0u, 0u, 0u, 0u);
+      KNJ_ATTN_BARRIER(kLdsOnly);
+    }
     KNJ_STAMP(4);
     // 6) sum e*v on the matrix cores: O[h][d] over the 64 slots.  Wave w owns
     // dims 32w .. 32w+31 as two 16-column tiles; step c's 32 reduction
