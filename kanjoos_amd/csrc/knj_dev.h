@@ -290,6 +290,21 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t w1, uint32_t w2, uint32_t
   }
 }
 
+// All eight 6-bit scales and mins of a Q4_K super-block at once, one byte
+// each: s[0] = sc0..3, s[1] = sc4..7, m[0] = m0..3, m[1] = m4..7 (the same
+// values as q4k_scale_min for s = 0..7, byte-parallel).
+struct Q4Scales8 {
+  uint32_t s[2], m[2];
+};
+__device__ __forceinline__ Q4Scales8 q4k_scales8(uint32_t w1, uint32_t w2, uint32_t w3) {
+  Q4Scales8 r;
+  r.s[0] = w1 & 0x3F3F3F3Fu;
+  r.m[0] = w2 & 0x3F3F3F3Fu;
+  r.s[1] = (w3 & 0x0F0F0F0Fu) | ((w1 >> 2) & 0x30303030u);
+  r.m[1] = ((w3 >> 4) & 0x0F0F0F0Fu) | ((w2 >> 2) & 0x30303030u);
+  return r;
+}
+
 // The 64 activations of a slice, in registers, with the two sub-block sums.
 struct XSlice {
   float v[64];
@@ -381,6 +396,10 @@ __device__ __forceinline__ float ub0(uint32_t v) { float r; asm("v_cvt_f32_ubyte
 __device__ __forceinline__ float ub1(uint32_t v) { float r; asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(v)); return r; }
 __device__ __forceinline__ float ub2(uint32_t v) { float r; asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(v)); return r; }
 __device__ __forceinline__ float ub3(uint32_t v) { float r; asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(v)); return r; }
+// byte n (a constant) of a word as f32
+__device__ __forceinline__ float ubn(uint32_t v, int n) {
+  return n == 0 ? ub0(v) : n == 1 ? ub1(v) : n == 2 ? ub2(v) : ub3(v);
+}
 
 // 16 code bytes: low nibbles against xlo (sub-block 2g), high nibbles against
 // xhi (sub-block 2g+1), each summed in element order.

@@ -527,37 +527,37 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
     const WBlock& w1c = w1s[ci];
     const uint4* L = lds + buf * kBuf;
     const half8 am = __builtin_bit_cast(half8, L[2 * kPart + kh * 32 + j]);
-    // the mins of this lane's row and the min-term step; the scales are
-    // decoded per code group below
-    auto mins = [&](const uint4& h) {
-      half8 bm;
-#pragma unroll
-      for (int s2 = 0; s2 < 8; ++s2) {
-        uint32_t sc, mn;
-        q4k_scale_min(h.y, h.z, h.w, s2, sc, mn);
-        bm[s2] = (_Float16)(float)mn;
-      }
+    // the scales and mins of this lane's row, decoded byte-parallel (small
+    // integers: every f16 below is exact, the same values as a per-sub-block
+    // decode), and the min-term step
+    const Q4Scales8 q0 = q4k_scales8(w0c.h.y, w0c.h.z, w0c.h.w);
+    Q4Scales8 q1 = {};
+    if constexpr (GATEUP) q1 = q4k_scales8(w1c.h.y, w1c.h.z, w1c.h.w);
+    auto pk = [](float x, float y) { return __builtin_bit_cast(half2v, __builtin_amdgcn_cvt_pkrtz(x, y)); };
+    auto mins = [&](const Q4Scales8& q) {
+      const half2v m01 = pk(ub0(q.m[0]), ub1(q.m[0])), m23 = pk(ub2(q.m[0]), ub3(q.m[0]));
+      const half2v m45 = pk(ub0(q.m[1]), ub1(q.m[1])), m67 = pk(ub2(q.m[1]), ub3(q.m[1]));
+      const half8 bm = {m01[0], m01[1], m23[0], m23[1], m45[0], m45[1], m67[0], m67[1]};
       return mfma32(am, bm, f32x16{});
     };
-    auto scales = [&](const uint4& h, int g, half2v& sl, half2v& nl, half2v& sh, half2v& nh) {
-      uint32_t s0, s1, mn;
-      q4k_scale_min(h.y, h.z, h.w, 2 * g, s0, mn);
-      q4k_scale_min(h.y, h.z, h.w, 2 * g + 1, s1, mn);
-      const float f0 = (float)s0, f1 = (float)s1;
-      sl = cvt_h2(f0);
-      nl = cvt_h2(-1024.0f * f0);
-      sh = cvt_h2(0.0625f * f1);
-      nh = cvt_h2(-64.0f * f1);
+    auto scales = [&](const Q4Scales8& q, int g, half2v& sl, half2v& nl, half2v& sh, half2v& nh) {
+      const uint32_t sw = q.s[g >> 1];
+      const float f0 = ubn(sw, (2 * g) & 3), f1 = ubn(sw, (2 * g + 1) & 3);
+      sl = pk(f0, f0);
+      nl = sl * half2v{(_Float16)-1024.0f, (_Float16)-1024.0f};
+      const half2v s1 = pk(f1, f1);
+      sh = s1 * half2v{(_Float16)0.0625f, (_Float16)0.0625f};
+      nh = s1 * half2v{(_Float16)-64.0f, (_Float16)-64.0f};
     };
-    const f32x16 cm0 = mins(w0c.h);
+    const f32x16 cm0 = mins(q0);
     f32x16 cm1 = {};
-    if constexpr (GATEUP) cm1 = mins(w1c.h);
+    if constexpr (GATEUP) cm1 = mins(q1);
     f32x16 cqa = {}, cqb = {};  // gate (or even groups), up (or odd groups)
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       half2v sl0, nl0, sh0, nh0, sl1, nl1, sh1, nh1;
-      scales(w0c.h, g, sl0, nl0, sh0, nh0);
-      if constexpr (GATEUP) scales(w1c.h, g, sl1, nl1, sh1, nh1);
+      scales(q0, g, sl0, nl0, sh0, nh0);
+      if constexpr (GATEUP) scales(q1, g, sl1, nl1, sh1, nh1);
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         const int q = 8 * g + 2 * kh + kk;
