@@ -729,13 +729,18 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int 
       }
       sc[s4] = sa;
     }
+    // the causal mask only where the chunk reaches past the tile's first row
+    // (uniform); the exponentials on the hardware's exp2 (results below
+    // 2^-126, which the library routine would keep as denormals, weigh
+    // nothing against a running sum of at least 1)
     float cmax = -INFINITY;
+    const bool masked = p0 + kChunk - 1 > a.pos0 + t0;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int ps = p0 + 16 * s4 + 4 * kq + i;
-        const float v = ps <= qp ? sc[s4][i] * scale2 : -INFINITY;
+        const float v = (!masked || ps <= qp) ? sc[s4][i] * scale2 : -INFINITY;
         sc[s4][i] = v;
         cmax = fmaxf(cmax, v);
       }
@@ -746,13 +751,13 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int 
     // starts after it); the exponents then use 0 so that no -inf - -inf occurs
     const float mnew = fmaxf(mrun, cmax);
     const float mref = mnew == -INFINITY ? 0.0f : mnew;
-    const float alpha = exp2f(mrun - mref);
+    const float alpha = __builtin_amdgcn_exp2f(mrun - mref);
     float esum = 0.0f;
 #pragma unroll
     for (int s4 = 0; s4 < 4; ++s4) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float e = exp2f(sc[s4][i] - mref);  // 2^-inf = 0 past the row's position
+        const float e = __builtin_amdgcn_exp2f(sc[s4][i] - mref);  // 2^-inf = 0 past the row's position
         sc[s4][i] = e;
         esum += e;
       }
@@ -761,10 +766,14 @@ __global__ __launch_bounds__(kBlock) void k_prefill_attn(PrefillAttnArgs a, int 
     esum += xor32_f(esum);
     lrun = lrun * alpha + esum;
     mrun = mnew;
+    // the rescale multiplies by exactly 1 when no column of the wave found a
+    // larger score: skipped then
+    if (__ballot(alpha != 1.0f) != 0) {
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
+      for (int dt = 0; dt < D / 16; ++dt) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
+        for (int i = 0; i < 4; ++i) acc[dt][i] *= alpha;
+      }
     }
     // values: step c covers slots 32c + 4kq + i (i < 4) and 32c + 16 + 4kq + i;
     // lane r's transposed read takes row 32c (+16) + 4kq + r/4, dims
