@@ -862,10 +862,10 @@ int attn_splits(int n_ctx) { return (n_ctx + kChunk - 1) / kChunk; }
 
 // splits of one head: one 64-slot chunk per workgroup up to kMaxSplit1
 // chunks at one sequence, several chunks per workgroup beyond (measured at
-// 32,770 slots: 171 splits of 3 chunks, 684 workgroups all resident at four
-// per CU, 2.545 ms/token against 2.60 for 257 splits of 2 and 2.61 for 103 of
-// 5), up to kMaxSplit with several sequences (the per-head merge)
-constexpr int kMaxSplit = 256, kMaxSplit1 = 171;
+// 32,770 slots, 513 chunks: 103 splits of 5 chunks 2.47 ms/token, 129 of 4
+// and 171 of 3 2.48, 86 of 6 and 73 of 7-8 2.52, 257 of 2 and an even 256-way
+// partition 2.55), up to kMaxSplit with several sequences (the per-head merge)
+constexpr int kMaxSplit = 256, kMaxSplit1 = 103;
 
 hipError_t launch_attention(const AttnArgs& a, hipStream_t s) {
   // one 64-slot chunk per workgroup up to kMaxSplit chunks; beyond, several
