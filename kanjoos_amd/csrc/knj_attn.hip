@@ -151,17 +151,16 @@ constexpr int kLdsOnly = vm_lds_imm(63);
 // cores (wave w: slots 16w .. 16w+15 against the heads), an online softmax
 // per head (wave w: heads 2w, 2w+1, lane = slot), and the values on the
 // matrix cores (wave w: dims 32w .. 32w+31).  K/V chunks reach LDS by DMA
-// (39 KB of LDS: four workgroups per CU), row-major with the 16-byte slots of
-// a row XOR-permuted by the row index as in the prompt kernel; one stage, the
-// next chunk's K fetched once the scores are written and its V once the
-// value products are done; each barrier waits only for the rows it hands
-// over (K at the chunk's start, V before the value products).  The step's
-// key/value row is written to the cache
-// after the loop (no fetch of this launch reads it); the workgroup holding
-// it writes it into the staged chunk and zeroes the V rows past it (slots
-// past the valid length under a weight of 0).  The query/key/value, norm and
-// RoPE loads are issued before the first chunk's DMA (measured 1-3% faster
-// per step than the chunk first).
+// (dma16; 39 KB of LDS: four workgroups per CU), row-major with the 16-byte
+// slots of a row XOR-permuted by the row index as in the prompt kernel; one
+// stage, the next chunk's K fetched once the scores are written and its V
+// once the value products are done; each barrier waits only for the rows it
+// hands over (K at the chunk's start, V before the value products).  The
+// step's key/value row is written to the cache after the loop (no fetch of
+// this launch reads it); the workgroup holding it writes it into the staged
+// chunk and zeroes the V rows past it (slots past the valid length under a
+// weight of 0).  The query/key/value, norm and RoPE loads are issued before
+// the first chunk's DMA (measured 1-3% faster per step than the chunk first).
 template <int D>
 __global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) {  // 4 waves per SIMD: 128 VGPRs
   constexpr int ROWH = D + 8;            // f16 elements per query LDS row (16-byte pad)
@@ -173,8 +172,6 @@ __global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) { 
   static_assert(NI >= 1 && CB % (1024 * (kBlock / 64)) == 0, "head_dim 64 or 128");
   auto kslot = [](int p, int sl) { return sl ^ ((p / RPB) & (NSLOT - 1)); };
   auto vslot = [](int p, int sl) { return sl ^ (((p / RPB) & (NPAIR - 1)) << 1); };
-  // (the staged chunks in the dynamic array, the rest in objects of their
-  // own, so that the compiler sees their accesses apart from the DMA's)
   __shared__ __align__(16) _Float16 qh[8 * ROWH];  // normalised, rotated queries: f16 high parts
   __shared__ __align__(16) _Float16 ql[8 * ROWH];  // and remainders
   __shared__ __align__(16) float es[8 * EROW];     // scores, then exp(score - running max), per head
