@@ -121,6 +121,20 @@ __device__ __forceinline__ void lds_wait8(u32x2* v) {
 // rows over, and the compiler's own counts only grow stricter by it.  M0 is
 // reserved to the compiler, which sets it right before each of its own uses
 // and keeps no value in it across this asm.
+// A 16-byte global load by asm (for loads that precede an asm DMA: the
+// caller waits for them with an explicit count, which the compiler's own
+// count, blind to the DMA, would set too deep), and that wait.
+__device__ __forceinline__ f32x4 ld16_asm(const void* g) {
+  f32x4 v;
+  asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(v) : "v"(g) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void vm_wait7(f32x4& a, f32x4& b, f32x4& c, f32x4& d, f32x4& e, f32x4& f, f32x4& g) {
+  asm volatile("s_waitcnt vmcnt(%7)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e), "+v"(f), "+v"(g) : "i"(N));
+}
+__device__ __forceinline__ float4 as_f4(f32x4 v) { return make_float4(v[0], v[1], v[2], v[3]); }
+
 __device__ __forceinline__ void dma16(const void* g, uint32_t base) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(base) : "memory");
 }
@@ -211,19 +225,26 @@ __global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) { 
   // 1) every load that does not depend on the position first: the raw
   // query/key/value, the norm weights and the RoPE row, then the first
   // chunk's DMA
+  // (asm loads: the wait below leaves the chunk's 2 NI DMA instructions,
+  // issued after them, in flight while the queries are prepared)
   const int qhd = min(tid / T, G - 1), qc = tid % T;
-  const float4 qraw = *reinterpret_cast<const float4*>(qz + (uint64_t)(kvh * G + qhd) * D + 4 * qc);
-  const float4 qnw = *reinterpret_cast<const float4*>(a.q_norm + 4 * qc);
-  const float4 kraw = *reinterpret_cast<const float4*>(kz + (uint64_t)kvh * D + 4 * qc);
-  const float4 vraw = *reinterpret_cast<const float4*>(vz + (uint64_t)kvh * D + 4 * qc);
-  const float4 knw = *reinterpret_cast<const float4*>(a.k_norm + 4 * qc);
   const int ri = (qc < T / 2) ? 4 * qc : 4 * qc - D / 2;  // rotation index of element 4qc
-  const float4 cs = *reinterpret_cast<const float4*>(rc + ri);
-  const float4 sn = *reinterpret_cast<const float4*>(rs + ri);
-  const int pos = a.pos[z];
-  __builtin_amdgcn_sched_barrier(0);
+  f32x4 l_q = ld16_asm(qz + (uint64_t)(kvh * G + qhd) * D + 4 * qc);
+  f32x4 l_qn = ld16_asm(a.q_norm + 4 * qc);
+  f32x4 l_k = ld16_asm(kz + (uint64_t)kvh * D + 4 * qc);
+  f32x4 l_v = ld16_asm(vz + (uint64_t)kvh * D + 4 * qc);
+  f32x4 l_kn = ld16_asm(a.k_norm + 4 * qc);
+  f32x4 l_cs = ld16_asm(rc + ri);
+  f32x4 l_sn = ld16_asm(rs + ri);
   dma(c0 * kChunk, true, false);  // all of K, then all of V: the counter is in order
   dma(c0 * kChunk, false, true);
+  // the position by a scalar load (asm: as a vector load, the compiler's wait
+  // for it would also wait for the DMA issued before it)
+  int pos;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(pos) : "s"(a.pos + z) : "memory");
+  vm_wait7<2 * NI>(l_q, l_qn, l_k, l_v, l_kn, l_cs, l_sn);
+  const float4 qraw = as_f4(l_q), qnw = as_f4(l_qn), kraw = as_f4(l_k), vraw = as_f4(l_v);
+  const float4 knw = as_f4(l_kn), cs = as_f4(l_cs), sn = as_f4(l_sn);
   const int n_kv = pos + 1;
   const int nch = min(cpw, (n_kv - c0 * kChunk + kChunk - 1) / kChunk);  // chunks holding slots
   KNJ_STAMP(1);
