@@ -123,23 +123,23 @@ __global__ __launch_bounds__(kBlock) void k_norm_rows(const float* __restrict__ 
 // perm8 order and as per-32 sums split the same way.  Layouts interleave the
 // pairs so that a wave's 32 pairs read one contiguous run:
 // hi/lo[(q * P + p) * 8 + j] for 8-group q; sums[((b / 8) * P + p) * 8 + b % 8]
-// for 32-sub-block b.  Workgroup = a tile of 32 pairs x 256 elements
-// (blockIdx.x, blockIdx.y): each pair's row segment is read whole (32
-// consecutive threads, 1 KB), the 8-element groups pass through LDS, and each
-// output row [group][pairs] is written as 32 consecutive 16-byte records.
-// n % 256 == 0.
+// for 32-sub-block b.  Workgroup = a tile of 32 pairs x 64 elements
+// (blockIdx.x, blockIdx.y; 64-element tiles give the launch four times the
+// workgroups of 256-element ones, which left it short of work): each pair's
+// row segment is read whole (8 consecutive threads, 256 bytes), the
+// 8-element groups pass through LDS, and each output row [group][pairs] is
+// written as 32 consecutive 16-byte records.  n % 64 == 0.
 __global__ __launch_bounds__(kBlock) void k_split_tile(const float* __restrict__ src,
                                                        const int* __restrict__ row_of, int n,
                                                        int P, _Float16* __restrict__ hi,
                                                        _Float16* __restrict__ lo,
                                                        _Float16* __restrict__ shi,
                                                        _Float16* __restrict__ slo) {
-  __shared__ uint4 th[32][33], tl[32][33];  // [group][pair] (+1 against bank conflicts)
-  __shared__ __align__(16) _Float16 sh_h[32][8], sh_l[32][8];  // [pair][sub-block]
-  const int t = threadIdx.x, p0 = blockIdx.x * 32, c0 = blockIdx.y * 256;
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = t + kBlock * u, pr = i >> 5, g = i & 31;  // 32 consecutive threads: one pair
+  __shared__ uint4 th[8][33], tl[8][33];  // [group][pair] (+1 against bank conflicts)
+  __shared__ __align__(16) _Float16 sh_h[32][2], sh_l[32][2];  // [pair][sub-block]
+  const int t = threadIdx.x, p0 = blockIdx.x * 32, c0 = blockIdx.y * 64;
+  {
+    const int pr = t >> 3, g = t & 7;  // 8 consecutive threads: one pair
     const int p = min(p0 + pr, P - 1);
     const float* s = src + (uint64_t)(row_of ? row_of[p] : p) * n + c0 + 8 * g;
     const float4 a = *reinterpret_cast<const float4*>(s);
@@ -164,9 +164,8 @@ __global__ __launch_bounds__(kBlock) void k_split_tile(const float* __restrict__
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int u = 0; u < 4; ++u) {
-    const int i = t + kBlock * u, g = i >> 5, pr = i & 31;  // 32 consecutive threads: one group
+  {
+    const int g = t >> 5, pr = t & 31;  // 32 consecutive threads: one group
     if (p0 + pr < P) {
       const uint64_t o = ((uint64_t)(c0 / 8 + g) * P + p0 + pr) * 8;
       *reinterpret_cast<uint4*>(hi + o) = th[g][pr];
@@ -176,10 +175,11 @@ __global__ __launch_bounds__(kBlock) void k_split_tile(const float* __restrict__
   if (t < 64) {
     const int pr = t & 31;
     if (p0 + pr < P) {
-      // the 8 sub-blocks of this tile are sub-block group c0 / 256
-      const uint64_t so = ((uint64_t)(c0 / 256) * P + p0 + pr) * 8;
-      *reinterpret_cast<uint4*>((t < 32 ? shi : slo) + so) =
-          *reinterpret_cast<const uint4*>(t < 32 ? sh_h[pr] : sh_l[pr]);
+      // the tile's two sub-blocks b, b + 1 (b even: one 4-byte pair of the record)
+      const int b = c0 / 32;
+      const uint64_t so = ((uint64_t)(b / 8) * P + p0 + pr) * 8 + (b % 8);
+      *reinterpret_cast<uint32_t*>((t < 32 ? shi : slo) + so) =
+          *reinterpret_cast<const uint32_t*>(t < 32 ? sh_h[pr] : sh_l[pr]);
     }
   }
 }
@@ -1484,7 +1484,7 @@ hipError_t launch_moe_batch(const MoeBatchArgs& a, void* scratch, hipStream_t s)
              a.topk_idx, a.topk_w);
   KNJ_LAUNCH(k_bucket, dim3(1), dim3(kBucketThreads), 0, s, a.topk_idx, m, K, E, offsets, pair_tok,
                      pair_of, items, n_items, tile);
-  KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), H / 256), dim3(kBlock), 0, s, xin,
+  KNJ_LAUNCH(k_split_tile, dim3((unsigned)((P + 31) / 32), H / 64), dim3(kBlock), 0, s, xin,
              pair_tok, H, (int)P, xh, xl, sxh, sxl);
   GroupArgs gu{a.gate, a.up, H, F, xh, xl, sxh, sxl, (int)P, offsets, items, n_items, act};
   gu.tile = tile;
@@ -1604,7 +1604,7 @@ hipError_t launch_dense_q4k_ex(const uint8_t* w, int n_in, int n_out, int m, con
     sh = ex.pre[2];
     sl = ex.pre[3];
   } else {
-    KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 256), dim3(kBlock), 0, s, x, nullptr,
+    KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 64), dim3(kBlock), 0, s, x, nullptr,
                n_in, m, const_cast<_Float16*>(xh), const_cast<_Float16*>(xl),
                const_cast<_Float16*>(sh), const_cast<_Float16*>(sl));
   }
@@ -1662,7 +1662,7 @@ hipError_t launch_dense_q6k(const uint8_t* w, int n_in, int n_out, int m, const 
   _Float16* xl = (_Float16*)take(P * n_in * 2);
   _Float16* sh = (_Float16*)take(P * n_in / 16);
   _Float16* sl = (_Float16*)take(P * n_in / 16);
-  KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 256), dim3(kBlock), 0, s, x, nullptr,
+  KNJ_LAUNCH(k_split_tile, dim3((m + 31) / 32, n_in / 64), dim3(kBlock), 0, s, x, nullptr,
              n_in, m, xh, xl, sh, sl);
   GroupArgs g{w, nullptr, n_in, n_out, xh, xl, sh, sl, m, nullptr, nullptr, nullptr, out, nullptr};
   KNJ_LAUNCH(k_group_q6k, dim3((n_out + kRowsWG - 1) / kRowsWG, (m + kTok - 1) / kTok),
