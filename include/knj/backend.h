@@ -99,7 +99,7 @@ struct AttentionPlan {
 // same call with its output sent to scratch_out.
 struct KvWritePlan {
   AttentionPlan attn;
-  float* scratch_out = nullptr;  // [n_head][head_dim]
+  float* scratch_out = nullptr;  // [n_head][head_dim]; null: a device buffer the backend owns
 };
 
 class Backend {

@@ -291,21 +291,24 @@ def moe_router(x, router_w, n_embd, n_expert, k, hx, logits, topk_idx, topk_w, n
 
 def moe_decode_layer(x, router_w, gate, up, down, n_embd, n_ff, n_expert, k, out, logits,
                      topk_idx, topk_w, norm_w=None, eps: float = 1e-6, resid=None,
-                     type_gate_up: int = TYPE_Q4_K, type_down: int = TYPE_Q4_K) -> None:
+                     type_gate_up: int = TYPE_Q4_K, type_down: int = TYPE_Q4_K,
+                     stream=None) -> None:
     check(lib().knj_moe_decode_layer(_p(x), _p(norm_w), eps, _p(router_w), _p(gate), _p(up),
                                      _p(down), type_gate_up, type_down, n_embd, n_ff, n_expert, k,
-                                     _p(resid), _p(out), _p(logits), _p(topk_idx), _p(topk_w), None))
+                                     _p(resid), _p(out), _p(logits), _p(topk_idx), _p(topk_w),
+                                     stream))
 
 
 def moe_decode_layer_noalloc(x, router_w, gate, up, down, n_embd, n_ff, n_expert, k, out, logits,
                              topk_idx, topk_w, norm_w=None, eps: float = 1e-6, resid=None,
-                             type_gate_up: int = TYPE_Q4_K, type_down: int = TYPE_Q4_K) -> None:
+                             type_gate_up: int = TYPE_Q4_K, type_down: int = TYPE_Q4_K,
+                             stream=None) -> None:
     """knj_moe_decode_layer with its scratch in the library's fixed device array
     (no allocation; n_embd + k * n_ff <= 32768)."""
     check(lib().knj_moe_decode_layer_noalloc(_p(x), _p(norm_w), eps, _p(router_w), _p(gate), _p(up),
                                              _p(down), type_gate_up, type_down, n_embd, n_ff,
                                              n_expert, k, _p(resid), _p(out), _p(logits),
-                                             _p(topk_idx), _p(topk_w), None))
+                                             _p(topk_idx), _p(topk_w), stream))
 
 
 def moe_batch_layer(x, router_w, gate, up, down, n_tokens, n_embd, n_ff, n_expert, k, out, logits,

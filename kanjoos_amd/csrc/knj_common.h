@@ -102,6 +102,7 @@ struct ExpertArgs {
   float* hidden_copy;     // optional second destination of out
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
+hipError_t expert_kernel_attributes();
 // t0/t1, when set, are recorded by the kernel dispatch itself at its start and
 // end (hipExtLaunchKernel): the launch's execution time, as a profiler sees it.
 hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t0 = nullptr,

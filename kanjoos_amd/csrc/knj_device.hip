@@ -117,6 +117,7 @@ int knj_device_open(int device) {
   const int rc = knj_check_arch(p.gcnArchName, kBuiltArch, std::getenv("KNJ_BUILD_ARCH"));
   if (rc != KNJ_OK) return rc;
   KNJ_HIP(hipSetDevice(device));
+  KNJ_HIP(expert_kernel_attributes());
   std::lock_guard<std::mutex> g(g_mu);
   if (device < kMaxDevices && !g_fixed_scratch[device]) {
     void* p = nullptr;

@@ -1061,10 +1061,6 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
                         (rb * a.n_embd) % 16 == 0 && (reinterpret_cast<uintptr_t>(a.down) & 15) == 0;
     if (staged) {
       const unsigned lds = (unsigned)(8 * kDownRows * rb);  // 8 waves x 8 rows
-      static const hipError_t attr = hipFuncSetAttribute(
-          (const void*)k_expert_down8_q6<true>, hipFuncAttributeMaxDynamicSharedMemorySize,
-          (int)(8 * kDownRows * 4 * KNJ_Q6K_BLOCK));
-      if (attr != hipSuccess) return attr;
       if (t0 || span_take("k_expert_down8_q6", &t0, &t1))
         hipExtLaunchKernelGGL(k_expert_down8_q6<true>, dim3(grid), dim3(512), lds, s, t0, t1, 0u, a);
       else
@@ -1107,6 +1103,16 @@ hipError_t launch_expert_down(const ExpertArgs& a, hipStream_t s, hipEvent_t t0,
   GQ(8) GQ(16) GQ(32) GQ(64)
 #undef GQ
   return hipErrorInvalidValue;
+}
+
+// Kernel attributes the batch-1 expert launches rely on, set once per device
+// when it is opened (knj_device_open), so no launch path (possibly under graph
+// capture) sets them lazily: the staged Q6_K down's dynamic LDS (8 waves x 8
+// rows of up to n_ff = 1024) exceeds the 64 KiB default.
+hipError_t expert_kernel_attributes() {
+  return hipFuncSetAttribute((const void*)k_expert_down8_q6<true>,
+                             hipFuncAttributeMaxDynamicSharedMemorySize,
+                             (int)(8 * kDownRows * 4 * KNJ_Q6K_BLOCK));
 }
 
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s) {

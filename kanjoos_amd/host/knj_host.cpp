@@ -197,12 +197,39 @@ class Gfx950Backend final : public Backend {
                               p.out, p.stream) == KNJ_OK;
   }
 
+  // The reference's KvWritePlan has no output buffer: without one, the step's
+  // attention output goes to a device buffer this backend owns.  A failed
+  // launch is recorded where knj_last_refusal() reads it (the method returns
+  // nothing, as the reference's does).
   void launch_kv_write(const KvWritePlan& p) override {
-    if (p.scratch_out == nullptr) return;
+    if (p.attn.q == nullptr || !would_instantiate(KnjCap::Wave64)) return;  // an empty plan
     AttentionPlan a = p.attn;
     a.out = p.scratch_out;
-    (void)launch_attention(a);
+    if (a.out == nullptr) {
+      const uint64_t need = (uint64_t)std::max(a.n_head, 1) * (uint64_t)std::max(a.head_dim, 1) * 4;
+      if (need > kv_out_bytes_) {
+        if (kv_out_) knj_free(kv_out_);
+        kv_out_ = nullptr;
+        kv_out_bytes_ = 0;
+        if (knj_malloc(&kv_out_, need) != KNJ_OK) {
+          std::snprintf(g_refusal, sizeof(g_refusal), "launch_kv_write: %s", knj_last_error());
+          return;
+        }
+        kv_out_bytes_ = need;
+      }
+      a.out = static_cast<float*>(kv_out_);
+    }
+    if (!launch_attention(a))
+      std::snprintf(g_refusal, sizeof(g_refusal), "launch_kv_write: %s", knj_last_error());
   }
+
+  ~Gfx950Backend() override {
+    if (kv_out_) knj_free(kv_out_);
+  }
+
+ private:
+  void* kv_out_ = nullptr;
+  uint64_t kv_out_bytes_ = 0;
 };
 
 void copy_arch(char (&dst)[16], const char* src) {

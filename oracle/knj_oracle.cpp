@@ -470,6 +470,30 @@ void synth_model(Pool& pool, const knj_model_config* c, uint64_t seed, uint8_t* 
   synth_tensor(pool, knj_tensor_key(seed, -1, KNJ_T_HEAD, -1), c->type_head, H, V, sd, img + off_head);
 }
 
+// One query head over slots 0..n_slots-1 of its KV head (model.cpp:591-616):
+// scores q.k * scale in slot order, softmax, then out = sum_s a_s * v_s in slot
+// order, K and V read back from the f16 cache.  The scores live in a buffer of
+// the calling thread, so heads (and rows) can run on different threads with the
+// same arithmetic per head.
+void attend_head(const float* qh, const uint16_t* kh0, const uint16_t* vh0, int n_slots, int D,
+                 float attn_scale, float* out) {
+  thread_local std::vector<float> scores;
+  if ((int)scores.size() < n_slots) scores.resize((size_t)n_slots);
+  for (int s = 0; s < n_slots; ++s) {
+    const uint16_t* kh = kh0 + (size_t)s * D;
+    float acc = 0.0f;
+    for (int d = 0; d < D; ++d) acc += qh[d] * knj_f16_to_f32(kh[d]);
+    scores[s] = acc * attn_scale;
+  }
+  softmax(scores.data(), n_slots);
+  std::fill(out, out + D, 0.0f);
+  for (int s = 0; s < n_slots; ++s) {
+    const uint16_t* vh = vh0 + (size_t)s * D;
+    const float a = scores[s];
+    for (int d = 0; d < D; ++d) out[d] += a * knj_f16_to_f32(vh[d]);
+  }
+}
+
 }  // namespace
 
 // ======================================================================= model
@@ -485,7 +509,7 @@ struct knjo_model {
   std::vector<knj_layer_offsets> lo;
   uint64_t off_embd = 0, off_onorm = 0, off_head = 0;
   int pos = 0;
-  std::vector<float> x, xn, q, k, v, ctx, ao, hx, ffn_out, rlog, scores, logits, inv_freq, head_tmp;
+  std::vector<float> x, xn, q, k, v, ctx, ao, hx, ffn_out, rlog, logits, inv_freq, head_tmp;
   std::vector<uint16_t> kv_k, kv_v;
   // optional f16 values to adopt for each newly written slot (see
   // knjo_model_set_kv_source) and the statistics of that adoption
@@ -641,7 +665,6 @@ knjo_model* knjo_model_create(const knj_model_config* cfg, uint64_t seed, const 
     m->hx.assign(H, 0.f);
     m->ffn_out.assign(H, 0.f);
     m->rlog.assign((size_t)c.n_expert, 0.f);
-    m->scores.assign((size_t)c.n_ctx, 0.f);
     m->logits.assign((size_t)c.n_vocab, 0.f);
     m->head_tmp.assign((size_t)c.head_dim, 0.f);
     m->kv_k.assign(knj_kv_elems(&c), 0);
@@ -754,25 +777,11 @@ int knjo_model_forward_steps(knjo_model* m, const int32_t* tokens, int n, float*
         }
         // attention (model.cpp:591-616), K/V read back from the f16 cache
         const int group = c.n_head / c.n_head_kv;
-        for (int h = 0; h < c.n_head; ++h) {
-          const int kvh = h / group;
-          const float* qh = m->q.data() + (size_t)h * D;
-          const size_t hb = ((size_t)il * c.n_head_kv + kvh) * c.n_ctx;
-          for (int s = 0; s <= p; ++s) {
-            const uint16_t* kh = m->kv_k.data() + (hb + s) * D;
-            float acc = 0.0f;
-            for (int d = 0; d < D; ++d) acc += qh[d] * knj_f16_to_f32(kh[d]);
-            m->scores[s] = acc * attn_scale;
-          }
-          softmax(m->scores.data(), p + 1);
-          float* ch = m->ctx.data() + (size_t)h * D;
-          std::fill(ch, ch + D, 0.0f);
-          for (int s = 0; s <= p; ++s) {
-            const uint16_t* vh = m->kv_v.data() + (hb + s) * D;
-            const float a = m->scores[s];
-            for (int d = 0; d < D; ++d) ch[d] += a * knj_f16_to_f32(vh[d]);
-          }
-        }
+        pool.for_each(c.n_head, [&](int h) {
+          const size_t hb = ((size_t)il * c.n_head_kv + h / group) * c.n_ctx;
+          attend_head(m->q.data() + (size_t)h * D, m->kv_k.data() + hb * D, m->kv_v.data() + hb * D,
+                      p + 1, D, attn_scale, m->ctx.data() + (size_t)h * D);
+        });
         // attn-o + residual (model.cpp:620-625)
         matmul(pool, c.type_attn, img + lo.wo, QD, H, m->ctx.data(), 1, QD, m->ao.data(), H, m->col);
         for (int i = 0; i < H; ++i) m->x[i] += m->ao[i];
@@ -884,28 +893,15 @@ int knjo_model_forward(knjo_model* m, const int32_t* tokens, int n, float* logit
           }
         }
       }
-      // causal attention, row t over slots 0..pos+t (model.cpp:591-616)
-      for (int t = 0; t < n; ++t) {
-        const int p = m->pos + t;
-        for (int h = 0; h < c.n_head; ++h) {
-          const float* qh = q.data() + (size_t)t * QD + (size_t)h * D;
-          const size_t hb = ((size_t)il * c.n_head_kv + h / group) * c.n_ctx;
-          for (int s = 0; s <= p; ++s) {
-            const uint16_t* kh = m->kv_k.data() + (hb + s) * D;
-            float acc = 0.0f;
-            for (int d = 0; d < D; ++d) acc += qh[d] * knj_f16_to_f32(kh[d]);
-            m->scores[s] = acc * attn_scale;
-          }
-          softmax(m->scores.data(), p + 1);
-          float* ch = ctx.data() + (size_t)t * QD + (size_t)h * D;
-          std::fill(ch, ch + D, 0.0f);
-          for (int s = 0; s <= p; ++s) {
-            const uint16_t* vh = m->kv_v.data() + (hb + s) * D;
-            const float a = m->scores[s];
-            for (int d = 0; d < D; ++d) ch[d] += a * knj_f16_to_f32(vh[d]);
-          }
-        }
-      }
+      // causal attention, row t over slots 0..pos+t (model.cpp:591-616); the
+      // (row, head) pairs are independent, so they are spread over the pool
+      pool.for_each(n * c.n_head, [&](int task) {
+        const int t = task / c.n_head, h = task - t * c.n_head;
+        const size_t hb = ((size_t)il * c.n_head_kv + h / group) * c.n_ctx;
+        attend_head(q.data() + (size_t)t * QD + (size_t)h * D, m->kv_k.data() + hb * D,
+                    m->kv_v.data() + hb * D, m->pos + t + 1, D, attn_scale,
+                    ctx.data() + (size_t)t * QD + (size_t)h * D);
+      });
       // attn-o + residual (model.cpp:620-625)
       matmul(pool, c.type_attn, img + lo.wo, QD, H, ctx.data(), n, QD, ao.data(), H, m->col);
       for (size_t i = 0; i < N * H; ++i) x[i] += ao[i];
