@@ -43,6 +43,11 @@ namespace dev {
 
 constexpr int kBlock = 256;
 
+// s_waitcnt immediate that waits for this wave's LDS accesses only (gfx9
+// encoding: vmcnt 63, expcnt 7, lgkmcnt 0): a barrier after it hands over LDS
+// writes while vector memory loads stay in flight.
+constexpr int kWaitLdsOnly = 0xC07F;
+
 __device__ __forceinline__ float h2f(uint32_t bits16) {
   return (float)__builtin_bit_cast(_Float16, (unsigned short)(bits16 & 0xFFFFu));
 }

@@ -360,6 +360,187 @@ __global__ __launch_bounds__(kBlock) void k_expert_gateup(ExpertArgs a) {
   KNJ_STAMP(4);
 }
 
+// ------------------------------------------------------------------ gate/up, one routing wave
+// The routed gate/up for n_expert <= 128, n_embd <= 2048, as one workgroup of
+// kGuWaves waves per CU.  Wave 0 routes alone while waves 1-4 load x and form
+// its sum of squares; after one barrier every wave issues its weight loads,
+// and waves 1-4 normalise x into LDS while the weights are in flight.
+//
+// Routing (the same selection as k_expert_gateup, bit for bit): lane l holds
+// experts l and l + 64.  The softmax max is a wave maximum; the denominator is
+// the sum of the two 64-expert halves, each a wave tree, added in order (the
+// workgroup sum of k_expert_gateup).  Candidates: the maxima of the 16 groups
+// of 8 consecutive experts are 16 distinct experts, so the k-th largest of
+// them bounds the k-th largest probability from below and every selected
+// expert is at or above it.  Lane 8g + j compares groups g and 8 + g with
+// groups j and 8 + j (one LDS permute each) and the group's 8 lanes add the
+// counts.  Each candidate then counts the larger candidate keys (probability,
+// then the lower index; model.cpp:442-451) by a scalar walk over the ~10
+// candidates.  A single wave keeps the routing off the other waves' SIMD time;
+// every wave routing for itself measured slower (8.3 vs 8.0 us), this form
+// ~7.0 us against 8.0 for the workgroup-cooperative routing.
+constexpr int kGuWaves = 12;
+
+__global__ __launch_bounds__(64 * kGuWaves) void k_expert_gateup_r(ExpertArgs a) {
+  constexpr int RS = 2;
+  __shared__ float xs[xpad_size(2048)];
+  __shared__ float xsum[64];
+  __shared__ float red[4];
+  __shared__ int sel[16];
+  __shared__ float selp[16];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int H = a.n_embd, E = a.n_expert;
+  const int tx = t - 64;  // waves 1-4 stage x as the 256 threads of k_expert_gateup
+  const bool xw = wave >= 1 && wave <= 4;
+  float4 x4[2], w4[2];
+  if (wave == 0) {
+    const float lg0 = lane < E ? a.logits[lane] : -INFINITY;
+    const float lg1 = lane + 64 < E ? a.logits[lane + 64] : -INFINITY;
+    const float mx = group_max<64>(fmaxf(lg0, lg1));
+    const float ex0 = lane < E ? expf(lg0 - mx) : 0.0f;
+    const float ex1 = lane + 64 < E ? expf(lg1 - mx) : 0.0f;
+    const float sum = group_sum<64>(ex0) + group_sum<64>(ex1);
+    const float p0 = ex0 / sum, p1 = ex1 / sum;
+    const uint32_t pb0 = lane < E ? __float_as_uint(p0) + 1u : 0u;  // 0: no expert
+    const uint32_t pb1 = lane + 64 < E ? __float_as_uint(p1) + 1u : 0u;
+    auto gmax8 = [](uint32_t v) {
+      v = max(v, dpp_u32<kDppXor1>(v));
+      v = max(v, dpp_u32<kDppXor2>(v));
+      return max(v, dpp_u32<kDppHalfMirror>(v));
+    };
+    const uint32_t gm0 = gmax8(pb0), gm1 = gmax8(pb1);  // groups g, 8 + g in lanes 8g..8g+7
+    const int n_group = (E + 7) >> 3;
+    const int g = lane >> 3, j = lane & 7;
+    const uint32_t mj0 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (8 * j), (int)gm0);
+    const uint32_t mj1 = (uint32_t)__builtin_amdgcn_ds_bpermute(4 * (8 * j), (int)gm1);
+    auto beats = [&](uint32_t o, int go, uint32_t me, int gme) {
+      return (go < n_group && (o > me || (o == me && go < gme))) ? 1 : 0;
+    };
+    int ra = beats(mj0, j, gm0, g) + beats(mj1, 8 + j, gm0, g);
+    int rb = beats(mj0, j, gm1, 8 + g) + beats(mj1, 8 + j, gm1, 8 + g);
+    ra += __builtin_amdgcn_update_dpp(ra, ra, kDppXor1, 0xF, 0xF, false);
+    rb += __builtin_amdgcn_update_dpp(rb, rb, kDppXor1, 0xF, 0xF, false);
+    ra += __builtin_amdgcn_update_dpp(ra, ra, kDppXor2, 0xF, 0xF, false);
+    rb += __builtin_amdgcn_update_dpp(rb, rb, kDppXor2, 0xF, 0xF, false);
+    ra += __builtin_amdgcn_update_dpp(ra, ra, kDppHalfMirror, 0xF, 0xF, false);
+    rb += __builtin_amdgcn_update_dpp(rb, rb, kDppHalfMirror, 0xF, 0xF, false);
+    const unsigned long long ta = __ballot(g < n_group && ra == a.k - 1);
+    const unsigned long long tb = __ballot(8 + g < n_group && rb == a.k - 1);
+    uint32_t thr = 0u;  // fewer groups than k: every expert is a candidate
+    if (n_group >= a.k)
+      thr = ta ? (uint32_t)__builtin_amdgcn_readlane((int)gm0, (int)__builtin_ctzll(ta))
+               : (uint32_t)__builtin_amdgcn_readlane((int)gm1, (int)__builtin_ctzll(tb));
+    const bool c0 = lane < E && pb0 >= thr, c1 = lane + 64 < E && pb1 >= thr;
+    unsigned long long m0 = __ballot(c0), m1 = __ballot(c1);
+    int r0 = 0, r1 = 0;
+    while (m0 | m1) {
+      const bool hi = m0 == 0;
+      const int l = (int)__builtin_ctzll(hi ? m1 : m0);
+      const uint32_t pc = (uint32_t)__builtin_amdgcn_readlane((int)(hi ? pb1 : pb0), l);
+      const int ec = l + (hi ? 64 : 0);
+      r0 += (pc > pb0 || (pc == pb0 && ec < lane)) ? 1 : 0;
+      r1 += (pc > pb1 || (pc == pb1 && ec < lane + 64)) ? 1 : 0;
+      if (hi) m1 &= m1 - 1;
+      else m0 &= m0 - 1;
+    }
+    if (c0 && r0 < a.k) {
+      sel[r0] = lane;
+      selp[r0] = p0;
+    }
+    if (c1 && r1 < a.k) {
+      sel[r1] = lane + 64;
+      selp[r1] = p1;
+    }
+  } else if (xw) {
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int i4 = tx + kBlock * jj;
+      x4[jj] = 4 * i4 < H ? *reinterpret_cast<const float4*>(a.hx + 4 * i4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      w4[jj] = (a.norm_w && 4 * i4 < H) ? *reinterpret_cast<const float4*>(a.norm_w + 4 * i4)
+                                         : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
+    float ss = 0.0f;
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+      ss += x4[jj].x * x4[jj].x + x4[jj].y * x4[jj].y + x4[jj].z * x4[jj].z + x4[jj].w * x4[jj].w;
+    ss = group_sum<64>(ss);
+    if (lane == 0) red[wave - 1] = ss;
+  }
+  __syncthreads();
+  // the weights of this wave's RS (slot, row) pairs: lanes [0,32) the gate
+  // row, [32,64) the up row, one 64-weight slice per lane
+  const int half = lane >> 5, sub = lane & 31;
+  const int nslices = H >> 6;
+  const bool active = sub < nslices;
+  const uint64_t rb = (uint64_t)(H >> 8) * KNJ_Q4K_BLOCK;
+  const uint64_t slab = rb * (uint64_t)a.n_ff;
+  const int npairs = a.k * a.n_ff;
+  const int pair0 = (blockIdx.x * kGuWaves + wave) * RS;
+  const int b = sub >> 2, g = sub & 3;
+  const uint8_t* base = half ? a.up : a.gate;
+  Q4Slice q0, q1;
+  auto load_pair = [&](int pr, Q4Slice& q) {
+    const int prc = min(pr, npairs - 1);  // always a valid row; unused results are dropped
+    const int kk = prc / a.n_ff, row = prc - kk * a.n_ff;
+    q = q4k_load(base + (uint64_t)sel[kk] * slab + (uint64_t)row * rb + (uint64_t)(active ? b : 0) * KNJ_Q4K_BLOCK, g);
+  };
+  load_pair(pair0, q0);
+  load_pair(pair0 + 1, q1);
+  __builtin_amdgcn_sched_barrier(0);
+  // x normalised into LDS with its 32-element sub-block sums (as k_expert_gateup)
+  if (xw) {
+    const float sst = ((red[0] + red[1]) + red[2]) + red[3];
+    const float scale = 1.0f / sqrtf(sst / (float)H + a.eps);
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+      const int i4 = tx + kBlock * jj;
+      float4 o = x4[jj];
+      if (a.norm_w) {
+        o.x = x4[jj].x * scale * w4[jj].x;
+        o.y = x4[jj].y * scale * w4[jj].y;
+        o.z = x4[jj].z * scale * w4[jj].z;
+        o.w = x4[jj].w * scale * w4[jj].w;
+      }
+      const float sb = group_sum<8>((o.x + o.y) + (o.z + o.w));
+      if (4 * i4 < H) {
+        *reinterpret_cast<float4*>(xs + xpad(4 * i4)) = o;
+        if ((lane & 7) == 0) xsum[(4 * i4) >> 5] = sb;
+      }
+    }
+  }
+  // barrier on the LDS writes only: the weight loads stay in flight
+  __builtin_amdgcn_s_waitcnt(kWaitLdsOnly);
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_barrier" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  XSlice xv;
+  const int sl = active ? sub : 0;
+  xslice_load_sums(xs, sl, xsum[2 * sl], xsum[2 * sl + 1], xv);
+  float res[RS];
+#pragma unroll
+  for (int st = 0; st < RS; ++st) {
+    const int pr = pair0 + st;
+    float acc = (active && pr < npairs) ? q4k_dot(st == 0 ? q0 : q1, g, xv) : 0.0f;
+    acc = group_sum<32>(acc);
+    const float u = lane_bcast(acc, 32);
+    res[st] = (acc / (1.0f + expf(-acc))) * u;
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int st = 0; st < RS; ++st)
+      if (pair0 + st < npairs) a.act[pair0 + st] = res[st];  // act is [k][n_ff]
+  }
+  if (blockIdx.x == 0 && t < a.k) {
+    // weights renormalised over the kept probabilities, summed in selection
+    // order (model.cpp:452-458)
+    float keep = 0.0f;
+    for (int q = 0; q < a.k; ++q) keep += selp[q];
+    const float inv = keep > 0.0f ? 1.0f / keep : 0.0f;
+    a.topk_idx[t] = sel[t];
+    a.topk_w[t] = selp[t] * inv;
+  }
+}
+
 // Reference-shaped fallback for n_embd > 2048: 32 lanes per row, loop.
 __global__ __launch_bounds__(kBlock) void k_expert_gateup_wide(ExpertArgs a) {
   extern __shared__ float xw[];
@@ -566,14 +747,29 @@ __global__ __launch_bounds__(kBlock) void k_expert_down(ExpertArgs a) {
   KNJ_WG_STAMP(1);
 }
 
+// Rank of slot kk's expert in ascending expert index among the k <= KMAX
+// slots (unused slots hold 0x7FFFFFFF and rank last; ids are distinct).
+template <int KMAX>
+__device__ __forceinline__ int expert_rank(const int (&ids)[KMAX], int kk) {
+  int me = ids[0];
+#pragma unroll
+  for (int q = 1; q < KMAX; ++q) me = kk == q ? ids[q] : me;
+  int rk = 0;
+#pragma unroll
+  for (int q = 0; q < KMAX; ++q) rk += ids[q] < me ? 1 : 0;
+  return rk;
+}
+
 // ------------------------------------------------------------------ down (Q4_K, k <= 8)
 // Workgroup = 8 waves x 8 output rows; wave w takes expert slot w for all 8
 // rows (16-lane row groups, one 64-weight slice per lane, two rows per lane
 // so each staged activation slice serves two rows).  The loads are ordered so
-// no wait covers more than it needs: first the k activation vectors, the
-// routing and the residuals (one round trip), then this wave's expert rows;
-// the activations are staged in LDS while the weights are in flight.  The k
-// products of a row are folded in ascending expert index by one thread per row.
+// no wait covers more than it needs: first the routing (the expert rows'
+// addresses wait on it alone), then the k activation vectors and the
+// residuals, then this wave's expert rows; the activations are staged in LDS
+// while the weights are in flight.  Each wave files its products under its
+// expert's rank in ascending index, and one thread per row adds them in that
+// order (a search of the slot order per row cost ~2 us of the launch).
 constexpr int kDownRows = 8;
 
 __global__ __launch_bounds__(512) void k_expert_down8(ExpertArgs a) {
@@ -590,20 +786,22 @@ __global__ __launch_bounds__(512) void k_expert_down8(ExpertArgs a) {
   __shared__ float acts[KMAX * xpad_size(1024)];
   __shared__ float sums[KMAX * 32];
   __shared__ float dots[KMAX][kDownRows];
+  __shared__ float wsr[KMAX];
   const int fpad = xpad_size(F);
-  // 1) activations (k * n_ff <= 8192 floats: four float4 per thread), routing, residuals
-  float4 v[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int i = 4 * (t + 512 * j);
-    v[j] = *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
-  }
+  // 1) the routing first (the weight addresses wait on it alone), then the
+  // activations (k * n_ff <= 8192 floats: four float4 per thread) and residuals
   int ids[KMAX];
   float wts[KMAX];
 #pragma unroll
   for (int q = 0; q < KMAX; ++q) {
     ids[q] = q < K ? a.topk_idx[q] : 0x7FFFFFFF;
     wts[q] = q < K ? a.topk_w[q] : 0.0f;
+  }
+  float4 v[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int i = 4 * (t + 512 * j);
+    v[j] = *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
   }
   const bool own_row = t < kDownRows && r0 + t < a.n_embd;
   const float resid = (own_row && a.resid) ? a.resid[r0 + t] : 0.0f;
@@ -636,28 +834,21 @@ __global__ __launch_bounds__(512) void k_expert_down8(ExpertArgs a) {
   xslice_load_sums(acts + kk * fpad, sl, sums[sb0], sums[sb0 + 1], xv);
   const float d0 = group_sum<16>(active ? q4k_dot(q0, g, xv) : 0.0f);
   const float d1 = group_sum<16>(active ? q4k_dot(q1, g, xv) : 0.0f);
+  // 5) each wave files its products and weight under its expert's rank in
+  // ascending index (rank = #{slots with a lower expert}; ids are distinct),
+  // so one thread per row folds them in that order with no search
+  const int rk = expert_rank<KMAX>(ids, kk);
   if (sub == 0 && wave < K) {
-    dots[wave][rg] = d0;
-    dots[wave][rg + 4] = d1;
+    dots[rk][rg] = d0;
+    dots[rk][rg + 4] = d1;
   }
+  if (lane == 0 && wave < K) wsr[rk] = wts[kk];
   __syncthreads();
   if (!own_row) return;
-  // 5) ascending expert index: rank[q] = #{slots with a lower expert}
   float o = 0.0f;
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) {
-    float wr = 0.0f, dr = 0.0f;
-#pragma unroll
-    for (int q = 0; q < KMAX; ++q) {
-      int rank = 0;
-#pragma unroll
-      for (int q2 = 0; q2 < KMAX; ++q2) rank += ids[q2] < ids[q] ? 1 : 0;
-      const bool hit = rank == r;
-      wr = hit ? wts[q] : wr;
-      dr = hit ? dots[q][t] : dr;
-    }
-    if (r < K) o = __fadd_rn(o, __fmul_rn(wr, dr));
-  }
+  for (int r = 0; r < KMAX; ++r)
+    if (r < K) o = __fadd_rn(o, __fmul_rn(wsr[r], dots[r][t]));
   const int row = r0 + t;
   const float out = a.resid ? __fadd_rn(resid, o) : o;
   a.out[row] = out;
@@ -714,12 +905,9 @@ __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
   __shared__ float acts[KMAX * 1024];
   __shared__ float s8[KMAX * 1024 / 8];
   __shared__ float dots[KMAX][kDownRows];
-  // (named registers: an array here was placed in scratch memory)
-  auto act4 = [&](int j) {
-    const int i = 4 * (t + 512 * j);
-    return *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
-  };
-  const float4 v0 = act4(0), v1 = act4(1), v2 = act4(2), v3 = act4(3);
+  __shared__ float wsr[KMAX];
+  // the routing first, then the activations (named registers: an array here
+  // was placed in scratch memory)
   int ids[KMAX];
   float wts[KMAX];
 #pragma unroll
@@ -727,6 +915,11 @@ __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
     ids[q] = q < K ? a.topk_idx[q] : 0x7FFFFFFF;
     wts[q] = q < K ? a.topk_w[q] : 0.0f;
   }
+  auto act4 = [&](int j) {
+    const int i = 4 * (t + 512 * j);
+    return *reinterpret_cast<const float4*>(a.act + (i < n ? i : 0));
+  };
+  const float4 v0 = act4(0), v1 = act4(1), v2 = act4(2), v3 = act4(3);
   const bool own_row = t < kDownRows && r0 + t < a.n_embd;
   const float resid = (own_row && a.resid) ? a.resid[r0 + t] : 0.0f;
   int e = ids[0];
@@ -786,28 +979,21 @@ __global__ __launch_bounds__(512) void k_expert_down8_q6(ExpertArgs a) {
     x8[tq][1] = *reinterpret_cast<const float4*>(acts + i + 4);
     sx[tq] = s8[i >> 3];
   }
+  // products and weight filed under the expert's rank in ascending index,
+  // folded in that order by one thread per row (as k_expert_down8)
+  const int rk = expert_rank<KMAX>(ids, kk);
 #pragma unroll
   for (int it = 0; it < kDownRows / 2; ++it) {
     const float acc = group_sum<32>(active ? q6_unit_dot(qu[it], x8, sx) : 0.0f);
-    if (u == 0 && wave < K) dots[wave][2 * it + half] = acc;
+    if (u == 0 && wave < K) dots[rk][2 * it + half] = acc;
   }
+  if (lane == 0 && wave < K) wsr[rk] = wts[kk];
   __syncthreads();
   if (!own_row) return;
   float o_ = 0.0f;
 #pragma unroll
-  for (int r = 0; r < KMAX; ++r) {
-    float wr = 0.0f, dr = 0.0f;
-#pragma unroll
-    for (int q = 0; q < KMAX; ++q) {
-      int rank = 0;
-#pragma unroll
-      for (int q2 = 0; q2 < KMAX; ++q2) rank += ids[q2] < ids[q] ? 1 : 0;
-      const bool hit = rank == r;
-      wr = hit ? wts[q] : wr;
-      dr = hit ? dots[q][t] : dr;
-    }
-    if (r < K) o_ = __fadd_rn(o_, __fmul_rn(wr, dr));
-  }
+  for (int r = 0; r < KMAX; ++r)
+    if (r < K) o_ = __fadd_rn(o_, __fmul_rn(wsr[r], dots[r][t]));
   const int row = r0 + t;
   const float out = a.resid ? __fadd_rn(resid, o_) : o_;
   a.out[row] = out;
@@ -987,11 +1173,11 @@ int pow2_at_least(int v) {
 // a span sink is installed (knj_spans.h)
 template <class F>
 void launch_maybe_timed(F kernel, const char* name, dim3 grid, size_t lds, hipStream_t s,
-                        hipEvent_t t0, hipEvent_t t1, const ExpertArgs& a) {
+                        hipEvent_t t0, hipEvent_t t1, const ExpertArgs& a, int block = kBlock) {
   if (t0 || span_take(name, &t0, &t1))
-    hipExtLaunchKernelGGL(kernel, grid, dim3(kBlock), (uint32_t)lds, s, t0, t1, 0u, a);
+    hipExtLaunchKernelGGL(kernel, grid, dim3(block), (uint32_t)lds, s, t0, t1, 0u, a);
   else
-    hipLaunchKernelGGL(kernel, grid, dim3(kBlock), lds, s, a);
+    hipLaunchKernelGGL(kernel, grid, dim3(block), lds, s, a);
 }
 
 }  // namespace
@@ -1016,6 +1202,11 @@ hipError_t launch_topk(const float* logits, int n_expert, int k, int32_t* idx, f
 
 hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
   const int npairs = a.k * a.n_ff;
+  if (a.logits && a.n_embd <= 2048 && a.n_expert <= 128 && a.k <= 16) {
+    const int grid = (npairs + 2 * kGuWaves - 1) / (2 * kGuWaves);
+    launch_maybe_timed(k_expert_gateup_r, "k_expert_gateup", dim3(grid), 0, s, t0, t1, a, 64 * kGuWaves);
+    return hipGetLastError();
+  }
   if (a.n_embd <= 2048) {
     constexpr int RS = 2;
     const int grid = (npairs + 4 * RS - 1) / (4 * RS);
