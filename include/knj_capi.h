@@ -241,7 +241,9 @@ int knj_model_time_decode(knj_model* m, int iters, float* ms_out);
  * greedy tokens from token 0 at the current position, the step's kernels
  * launched directly (no graph); every layer's gate/up and down launch records
  * HIP start/end events of its own execution (hipExtLaunchKernel) on the
- * model's stream.  Returns the mean
+ * model's stream, and so does the router launch before them (unused: a launch
+ * timed right after one without events reads the earlier launch's drain as
+ * its own).  Returns the mean
  * microseconds per launch of each over n_layer * steps launches; advances the
  * position by `steps`. */
 int knj_model_time_experts(knj_model* m, int steps, float* us_gateup, float* us_down);

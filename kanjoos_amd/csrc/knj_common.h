@@ -78,7 +78,9 @@ struct RouterArgs {
   float* topk_w;          // [k]
   unsigned int* counter;  // zero-initialised ticket, left at zero on exit
 };
-hipError_t launch_router(const RouterArgs& a, hipStream_t s);
+// t0/t1 as for the expert launches below (timing runs only)
+hipError_t launch_router(const RouterArgs& a, hipStream_t s, hipEvent_t t0 = nullptr,
+                         hipEvent_t t1 = nullptr);
 // Softmax + top-k of n_expert logits by one workgroup (the C-ABI router).
 hipError_t launch_topk(const float* logits, int n_expert, int k, int32_t* idx, float* w,
                        hipStream_t s);

@@ -324,8 +324,14 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
   RouterArgs ra{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
                 reinterpret_cast<const float*>(img + lo.router), H, c.n_expert, c.n_expert_used,
                 m->hx, m->router_logits + (uint64_t)il * c.n_expert, nullptr, nullptr, m->counter};
+  // timing runs: the router and each expert launch record start/end events of
+  // their own dispatch.  The router's are not used: an event-timed launch that
+  // follows one without events reads ~1.5 us longer (its start event is taken
+  // while the launch before it still drains), so the gate/up launch is timed
+  // after an event-timed launch as the down launch is.
+  hipEvent_t* ev = m->expert_events ? m->expert_events + 6 * m->expert_slot++ : nullptr;
   span_class("moe-router");
-  KNJ_HIP(launch_router(ra, s));
+  KNJ_HIP(launch_router(ra, s, ev ? ev[4] : nullptr, ev ? ev[5] : nullptr));
   // the gate/up launch routes from the logits (softmax + top-k per wave)
   int32_t* ti = m->topk_idx + (uint64_t)il * c.n_expert_used;
   float* tw = m->topk_w + (uint64_t)il * c.n_expert_used;
@@ -334,8 +340,6 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
                 img + lo.gate, img + lo.up, img + lo.down,
                 c.type_gate_up, c.type_down, H, c.n_ff, c.n_expert, c.n_expert_used, m->act, m->x,
                 m->x, m->hidden + (uint64_t)il * H};
-  // timing runs: each expert launch records its own start/end events
-  hipEvent_t* ev = m->expert_events ? m->expert_events + 4 * m->expert_slot++ : nullptr;
   span_class("moe-gate+up+act");
   KNJ_HIP(launch_expert_gateup(ea, s, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr));
   span_class("moe-down+scatter");
@@ -834,7 +838,7 @@ int knj_model_time_experts(knj_model* m, int steps, float* us_gateup, float* us_
     set_error("context exhausted");
     return KNJ_E_ARG;
   }
-  const int n = 4 * m->c.n_layer * steps;
+  const int n = 6 * m->c.n_layer * steps;
   std::vector<hipEvent_t> ev(n, nullptr);
   for (auto& e : ev) KNJ_HIP(hipEventCreate(&e));
   // greedy decode from token 0, the step's kernels launched directly; every
@@ -851,8 +855,8 @@ int knj_model_time_experts(knj_model* m, int steps, float* us_gateup, float* us_
   double gu = 0.0, dn = 0.0;
   for (int i = 0; i < m->c.n_layer * steps && !rc; ++i) {
     float a = 0.0f, b = 0.0f;
-    hipError_t e = hipEventElapsedTime(&a, ev[4 * i], ev[4 * i + 1]);
-    if (e == hipSuccess) e = hipEventElapsedTime(&b, ev[4 * i + 2], ev[4 * i + 3]);
+    hipError_t e = hipEventElapsedTime(&a, ev[6 * i], ev[6 * i + 1]);
+    if (e == hipSuccess) e = hipEventElapsedTime(&b, ev[6 * i + 2], ev[6 * i + 3]);
     if (e != hipSuccess) rc = hip_fail(e, "hipEventElapsedTime");
     gu += a;
     dn += b;

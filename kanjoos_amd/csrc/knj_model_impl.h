@@ -47,7 +47,7 @@ struct knj_model {
   // prompt pass over several rows at once (KNJ_PROMPT_STEPS=1 feeds prompts
   // one decode step per token instead)
   knj_prefill_bufs pf;
-  hipEvent_t* expert_events = nullptr;  // set by knj_model_time_experts: 4 per layer per step
+  hipEvent_t* expert_events = nullptr;  // set by knj_model_time_experts: 6 per layer per step
   int expert_slot = 0;
   // host<->device bytes copied by this model's calls (the profiler's transfer row)
   mutable uint64_t h2d_bytes = 0, d2h_bytes = 0;

@@ -1183,8 +1183,13 @@ void launch_maybe_timed(F kernel, const char* name, dim3 grid, size_t lds, hipSt
 }  // namespace
 
 
-hipError_t launch_router(const RouterArgs& a, hipStream_t s) {
-  if (a.topk_idx) {
+hipError_t launch_router(const RouterArgs& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+  if (t0) {  // a timing run: dispatch events of its own
+    if (a.topk_idx)
+      hipExtLaunchKernelGGL(k_router, dim3((a.n_expert + 3) / 4), dim3(kBlock), 0u, s, t0, t1, 0u, a);
+    else
+      hipExtLaunchKernelGGL(k_router, dim3(a.n_expert), dim3(64), 0u, s, t0, t1, 0u, a);
+  } else if (a.topk_idx) {
     // four rows (waves) per workgroup; the last workgroup also ranks the experts
     KNJ_LAUNCH(k_router, dim3((a.n_expert + 3) / 4), dim3(kBlock), 0, s, a);
   } else {
