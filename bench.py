@@ -156,10 +156,11 @@ def calib_probe() -> None:
     """Two kernels whose HBM traffic is known exactly: k_gemv_bf16 over a
     2048 x 65536 bf16 matrix (268,435,456 bytes read once; x and y are 8 KiB and
     256 KiB) and k_dequant of 16,777,216 Q4_K weights (9,437,184 bytes read,
-    67,108,864 bytes written).  Then a plain stream of the gate/up launch's
-    byte count: k_gemv_bf16 over 2048 x 3456 bf16 rows (14,155,776 bytes, one
-    gate/up launch's weights), 20 launches over 20 different matrices (283 MB,
-    past the 256 MB memory-side cache), for its duration and counters."""
+    67,108,864 bytes written).  Then the gate/up launch's bytes without its
+    routing: the dense Q4_K GEMV (k_gemv_q4k) over 12,288 rows of 2048 weights
+    (14,155,776 bytes: the 8 experts x 2 x 768 rows one gate/up launch reads),
+    20 launches over 20 different matrices (283 MB, past the 256 MB
+    memory-side cache), for its duration and counters."""
     n_in, n_out = 2048, 65536
     w = K.DeviceBuffer(n_in * n_out * 2)
     w.zero()
@@ -176,14 +177,15 @@ def calib_probe() -> None:
     K.synchronize()
     log("calibration probe: 2 x (bf16 GEMV 256 MiB read, Q4_K dequant 64 MiB write)")
     del w, q, out
-    rows = 3456
-    mat = n_in * rows * 2
+    rows = 12288
+    mat = K.row_bytes(K.TYPE_Q4_K, n_in) * rows
     big = K.DeviceBuffer(20 * mat)
     big.zero()
+    yq = K.DeviceBuffer(4 * rows)
     for i in range(20):
-        K.gemv(K.TYPE_BF16, big.ptr + i * mat, n_in, rows, x, y)
+        K.gemv(K.TYPE_Q4_K, big.ptr + i * mat, n_in, rows, x, yq)
     K.synchronize()
-    log(f"stream probe: 20 x bf16 GEMV over {mat} bytes each (one gate/up launch's bytes)")
+    log(f"dense probe: 20 x Q4_K GEMV over {mat} bytes each (one gate/up launch's bytes)")
 
 
 def host_cpus() -> dict:
