@@ -438,6 +438,8 @@ int pow2_at_least(int v) {
 // The bf16 fast path is instantiated for 512, 1024, 2048 and 4096 inputs only;
 // gemv_grid and launch_gemv both decide through this one predicate, so the
 // number of argmax keys the step reads always matches the launch.
+constexpr int kBf16Rows = 2;  // rows per wave step of the bf16 fast path
+
 bool bf16_fast(int n_in) {
   if (n_in % 512 != 0) return false;
   const int nj = n_in / 512;
@@ -458,9 +460,11 @@ int gemv_grid(int type, int n_in, int n_out) {
     return std::max(1, std::min(kMaxKeys, (n_out + rows_per_block - 1) / rows_per_block));
   }
   if (type == KNJ_TYPE_BF16 && bf16_fast(n_in)) {
-    constexpr int RS = 4;
-    const int waves_needed = (n_out + RS - 1) / RS;
-    return std::max(1, std::min(512, (waves_needed + 3) / 4));
+    // two rows per wave step, up to kMaxKeys workgroups: the 151,936-row
+    // head measured 112.5 us at 512 workgroups of four rows per step, 103.5
+    // at 4096 of two (a graph of back-to-back launches)
+    const int waves_needed = (n_out + kBf16Rows - 1) / kBf16Rows;
+    return std::max(1, std::min(kMaxKeys, (waves_needed + 3) / 4));
   }
   return std::max(1, std::min(kMaxKeys, (n_out + 3) / 4));
 }
@@ -512,7 +516,7 @@ hipError_t launch_gemv(const GemvArgs& a, hipStream_t s) {
   }
   if (a.type == KNJ_TYPE_BF16 && bf16_fast(a.n_in)) {
     const int nj = a.n_in / 512;
-    constexpr int RS = 4;
+    constexpr int RS = kBf16Rows;
     const int grid = gemv_grid(a.type, a.n_in, a.n_out);
 #define GB(J)                                                                                   \
   if (nj == J) {                                                                                \
