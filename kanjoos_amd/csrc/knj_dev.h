@@ -165,9 +165,6 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 __device__ __forceinline__ float ld_acquire_f(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int ld_acquire_i(const int* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Cross-workgroup hand-off inside one launch without a device-wide fence.
 // A device-scope fence writes back the whole L2 and serialises across the
@@ -177,9 +174,6 @@ __device__ __forceinline__ int ld_acquire_i(const int* p) {
 // stores to complete, and take a ticket; the last workgroup reads the values
 // with agent-scope atomic loads.
 __device__ __forceinline__ void publish(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void publish_i(int32_t* p, int32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -350,49 +344,6 @@ __device__ __forceinline__ void xslice_load_sums(const float* xs_pad, int slice,
   }
   x.s0 = s0;
   x.s1 = s1;
-}
-
-// The 64 activations of slice `slice` read straight from global memory into
-// registers, optionally RMS-normalised.  The sum of squares is reduced over the
-// W lanes of the row group, which together hold all of x (n_in <= 64*W); lanes
-// with no slice contribute zero.  No LDS and no workgroup barrier.
-template <int W>
-__device__ __forceinline__ void xslice_global(const float* __restrict__ x,
-                                              const float* __restrict__ nw, float eps, int n,
-                                              int slice, bool active, XSlice& xv) {
-  float ss = 0.0f;
-  const float* p = x + 64 * slice;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const float4 t = active ? *reinterpret_cast<const float4*>(p + 4 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
-    xv.v[4 * k] = t.x;
-    xv.v[4 * k + 1] = t.y;
-    xv.v[4 * k + 2] = t.z;
-    xv.v[4 * k + 3] = t.w;
-  }
-  if (nw) {
-#pragma unroll
-    for (int l = 0; l < 64; ++l) ss += xv.v[l] * xv.v[l];
-    ss = group_sum<W>(ss);
-    const float scale = 1.0f / sqrtf(ss / (float)n + eps);
-    const float* q = nw + 64 * slice;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float4 w = active ? *reinterpret_cast<const float4*>(q + 4 * k) : make_float4(0.f, 0.f, 0.f, 0.f);
-      xv.v[4 * k] = xv.v[4 * k] * scale * w.x;
-      xv.v[4 * k + 1] = xv.v[4 * k + 1] * scale * w.y;
-      xv.v[4 * k + 2] = xv.v[4 * k + 2] * scale * w.z;
-      xv.v[4 * k + 3] = xv.v[4 * k + 3] * scale * w.w;
-    }
-  }
-  float a = 0.0f, b = 0.0f;
-#pragma unroll
-  for (int l = 0; l < 32; ++l) {
-    a += xv.v[l];
-    b += xv.v[32 + l];
-  }
-  xv.s0 = a;
-  xv.s1 = b;
 }
 
 // Byte n of a word as f32: one v_cvt_f32_ubyteN each (the compiler otherwise
