@@ -61,6 +61,15 @@ struct GemvArgs {
 };
 constexpr int kMaxKeys = 4096;
 hipError_t launch_gemv(const GemvArgs& a, hipStream_t s);
+// The attention-output GEMV (Q4_K, y = resid + W x, one row step per wave)
+// with the router's unscaled logits u[e] = R[e] . [resid ; x] in the same
+// launch (k_gemv_q4k_router); R [n_router][n_out + n_in] from
+// launch_router_fold.  router_fold_ok says whether a shape can take it.
+bool router_fold_ok(int type_o, int n_in, int n_out, int n_router);
+hipError_t launch_gemv_router(const GemvArgs& a, const float* R, int n_router, float* u,
+                              hipStream_t s, hipEvent_t t0 = nullptr, hipEvent_t t1 = nullptr);
+hipError_t launch_router_fold(const float* wr, const float* nw, const float* wd, int H, int QD,
+                              int E, float* R, hipStream_t s);
 
 hipError_t launch_dequant(int type, const uint8_t* w, uint64_t n, float* out, hipStream_t s);
 
@@ -102,6 +111,9 @@ struct ExpertArgs {
   const float* resid;     // optional residual added to the output
   float* out;             // [n_embd]
   float* hidden_copy;     // optional second destination of out
+  // logits are W_r' applied to the un-normalised rows (launch_gemv_router):
+  // the routed gate/up scales them by 1 / sqrt(mean(hx^2) + eps) first
+  bool logits_unscaled = false;
 };
 hipError_t launch_experts(const ExpertArgs& a, hipStream_t s);
 hipError_t expert_kernel_attributes();

@@ -17,12 +17,14 @@ namespace {
 
 using namespace dev;
 
+constexpr int kRouterF4 = 8;  // float4 per lane of a router quarter row: n_embd + n_in <= 8192
+
 template <int LPR, int RS>
-__global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__ w, int n_in,
-                                                     int n_out, const float* __restrict__ x,
-                                                     const float* __restrict__ nw, float eps,
-                                                     const float* __restrict__ resid,
-                                                     float* __restrict__ y) {
+__device__ __forceinline__ void gemv_q4k_body(const uint8_t* __restrict__ w, int n_in, int n_out,
+                                              const float* __restrict__ x,
+                                              const float* __restrict__ nw, float eps,
+                                              const float* __restrict__ resid,
+                                              float* __restrict__ y) {
   __shared__ float xs[xpad_size(4096)];
   __shared__ float xsum[128];
   __shared__ float red[8];
@@ -65,6 +67,95 @@ __global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__
     const int row = row0 + st * RPW + rsub;
     if (sub == 0 && row < n_out) y[row] = resid ? rv[st] + res[st] : res[st];
   }
+}
+
+template <int LPR, int RS>
+__global__ __launch_bounds__(kBlock) void k_gemv_q4k(const uint8_t* __restrict__ w, int n_in,
+                                                     int n_out, const float* __restrict__ x,
+                                                     const float* __restrict__ nw, float eps,
+                                                     const float* __restrict__ resid,
+                                                     float* __restrict__ y) {
+  gemv_q4k_body<LPR, RS>(w, n_in, n_out, x, nw, eps, resid, y);
+}
+
+// The attention-output GEMV y = resid + W x (one row step per wave) with the
+// router's logits computed in the same launch, before the normalisation of
+// y.  The router applies W_r to RMSNorm(y) with y = resid + W x
+// (/root/reference/src/model/model.cpp:420-423, 620-628); regrouped,
+//   logit_e = scale * (sum_i R[e][i] resid[i] + sum_j R[e][H + j] x[j]),
+//   R[e][i] = W_r[e][i] nw[i],  R[e][H + j] = sum_i R[e][i] W[i][j],
+// with scale = 1 / sqrt(mean(y^2) + eps), which needs all of y and is applied
+// by the gate/up launch (the ranking does not depend on it, the weights do).
+// Workgroups past the GEMV's take one row e of R each, a quarter row per
+// wave (the 8 KB resid and the x inputs read as they are), and write the
+// unscaled logit u[e]; they do not depend on the GEMV's rows, so the two
+// run side by side.  R is precomputed per layer from the weights
+// (launch_router_fold).
+template <int LPR>
+__global__ __launch_bounds__(kBlock) void k_gemv_q4k_router(const uint8_t* __restrict__ w, int n_in,
+                                                            int n_out, const float* __restrict__ x,
+                                                            const float* __restrict__ resid,
+                                                            float* __restrict__ y,
+                                                            const float* __restrict__ R, int n_router,
+                                                            int n_gemv_blocks, float* __restrict__ u) {
+  if ((int)blockIdx.x < n_gemv_blocks) {
+    gemv_q4k_body<LPR, 1>(w, n_in, n_out, x, nullptr, 0.0f, resid, y);
+    return;
+  }
+  __shared__ float part[4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int e = blockIdx.x - n_gemv_blocks, H = n_out, NR = n_out + n_in, Q = NR >> 2;
+  const float* rr = R + (uint64_t)e * NR;
+  float4 wv[kRouterF4], iv[kRouterF4];
+#pragma unroll
+  for (int j = 0; j < kRouterF4; ++j) {
+    const int i = Q * wave + 4 * lane + 256 * j;
+    if (4 * lane + 256 * j < Q) {
+      wv[j] = *reinterpret_cast<const float4*>(rr + i);
+      iv[j] = i < H ? *reinterpret_cast<const float4*>(resid + i)
+                    : *reinterpret_cast<const float4*>(x + (i - H));
+    }
+  }
+  float acc = 0.0f;
+#pragma unroll
+  for (int j = 0; j < kRouterF4; ++j)
+    if (4 * lane + 256 * j < Q) {
+      acc += wv[j].x * iv[j].x;
+      acc += wv[j].y * iv[j].y;
+      acc += wv[j].z * iv[j].z;
+      acc += wv[j].w * iv[j].w;
+    }
+  acc = group_sum<64>(acc);
+  if (lane == 0) part[wave] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0 && e < n_router) u[e] = ((part[0] + part[1]) + part[2]) + part[3];
+}
+
+// R (see k_gemv_q4k_router) from the router weights W_r [E][H], the norm
+// weight nw [H] and the dequantised attention-output matrix Wd [H][QD]:
+// thread (column j, 8 rows e) accumulates sum_i R[e][i] Wd[i][j] in double
+// and rounds once to f32; the first H columns are the products W_r nw.
+__global__ __launch_bounds__(kBlock) void k_router_fold(const float* __restrict__ wr,
+                                                        const float* __restrict__ nw,
+                                                        const float* __restrict__ wd, int H, int QD,
+                                                        int E, float* __restrict__ R) {
+  const int j = blockIdx.x * kBlock + threadIdx.x, e0 = 8 * blockIdx.y;
+  const int NR = H + QD;
+  if (j < H) {
+    for (int e = e0; e < min(E, e0 + 8); ++e) R[(uint64_t)e * NR + j] = wr[(uint64_t)e * H + j] * nw[j];
+  }
+  if (j >= QD) return;
+  double acc[8] = {};
+  for (int i = 0; i < H; ++i) {
+    const double wdv = (double)wd[(uint64_t)i * QD + j];
+    const float nwi = nw[i];
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      if (e0 + q < E) acc[q] += (double)(wr[(uint64_t)(e0 + q) * H + i] * nwi) * wdv;
+  }
+#pragma unroll
+  for (int q = 0; q < 8; ++q)
+    if (e0 + q < E) R[(uint64_t)(e0 + q) * NR + H + j] = (float)acc[q];
 }
 
 // Q4_K rows wider than 64 slices (n_in > 4096, up to 16384): the activations
@@ -543,6 +634,43 @@ hipError_t launch_step_close(StepState* st, const unsigned long long* keys, int 
                              int32_t* out_tokens, int max_steps, hipStream_t s) {
   KNJ_LAUNCH(k_step_close, dim3(1), dim3(kBlock), 0, s, st, keys, nkeys, out_tokens,
                      max_steps);
+  return hipGetLastError();
+}
+
+bool router_fold_ok(int type_o, int n_in, int n_out, int n_router) {
+  if (type_o != KNJ_TYPE_Q4_K || n_router <= 0) return false;
+  if (n_in % 256 || n_out % 256 || n_in / 64 > 64) return false;  // one row step per wave below
+  const int lpr = pow2_at_least(n_in / 64), rpw = 64 / lpr;
+  const int steps_total = (n_out + rpw - 1) / rpw;
+  return steps_total <= 4 * 1024 && (n_in + n_out) / 4 <= 256 * kRouterF4 && lpr >= 4;
+}
+
+hipError_t launch_gemv_router(const GemvArgs& a, const float* R, int n_router, float* u,
+                              hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
+  if (!router_fold_ok(a.type, a.n_in, a.n_out, n_router) || a.norm_w || !a.resid || a.y == a.resid)
+    return hipErrorInvalidValue;
+  const int lpr = pow2_at_least(a.n_in / 64), rpw = 64 / lpr;
+  const int nob = ((a.n_out + rpw - 1) / rpw + 3) / 4;
+  const dim3 grid(nob + n_router);
+#define GR(L)                                                                                  \
+  if (lpr == L) {                                                                              \
+    if (t0) /* a timing run: dispatch events of its own */                                     \
+      hipExtLaunchKernelGGL(k_gemv_q4k_router<L>, grid, dim3(kBlock), 0u, s, t0, t1, 0u, a.w,  \
+                            a.n_in, a.n_out, a.x, a.resid, a.y, R, n_router, nob, u);          \
+    else                                                                                       \
+      KNJ_LAUNCH(k_gemv_q4k_router<L>, grid, dim3(kBlock), 0, s, a.w, a.n_in, a.n_out, a.x,     \
+                 a.resid, a.y, R, n_router, nob, u);                                           \
+    return hipGetLastError();                                                                  \
+  }
+  GR(4) GR(8) GR(16) GR(32) GR(64)
+#undef GR
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_router_fold(const float* wr, const float* nw, const float* wd, int H, int QD,
+                              int E, float* R, hipStream_t s) {
+  const dim3 grid((std::max(H, QD) + kBlock - 1) / kBlock, (E + 7) / 8);
+  hipLaunchKernelGGL(k_router_fold, grid, dim3(kBlock), 0, s, wr, nw, wd, H, QD, E, R);
   return hipGetLastError();
 }
 

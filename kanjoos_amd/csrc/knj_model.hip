@@ -197,6 +197,7 @@ int setup(knj_model* m) {
   if ((rc = alloc(m, (void**)&m->qkv, (QD + 2 * KVD) * 4))) return rc;
   if ((rc = alloc(m, (void**)&m->ctx, QD * 4))) return rc;
   if ((rc = alloc(m, (void**)&m->hx, H * 4))) return rc;
+  if ((rc = alloc(m, (void**)&m->x2, H * 4))) return rc;
   if ((rc = alloc(m, (void**)&m->act, (uint64_t)c.n_expert_used * c.n_ff * 4))) return rc;
   if ((rc = alloc(m, (void**)&m->logits, (uint64_t)c.n_vocab * 4))) return rc;
   if ((rc = alloc(m, (void**)&m->router_logits, (uint64_t)c.n_layer * c.n_expert * 4))) return rc;
@@ -318,28 +319,39 @@ int enqueue_layer(knj_model* m, int il, hipStream_t s) {
               1.0f / std::sqrt((float)D), m->attn_part, m->ctx};
   span_class("attention");
   KNJ_HIP(launch_attention(at, s));
-  GemvArgs o{c.type_attn, img + lo.wo, QD, H, m->ctx, nullptr, 0.0f, m->x, m->x, nullptr};
-  span_class("attn-o");
-  KNJ_HIP(launch_gemv(o, s));
-  RouterArgs ra{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
-                reinterpret_cast<const float*>(img + lo.router), H, c.n_expert, c.n_expert_used,
-                m->hx, m->router_logits + (uint64_t)il * c.n_expert, nullptr, nullptr, m->counter};
-  // timing runs: the router and each expert launch record start/end events of
-  // their own dispatch.  The router's are not used: an event-timed launch that
+  // timing runs: the launch before the experts (the router, or attn-o with the
+  // router folded in) and each expert launch record start/end events of their
+  // own dispatch.  The first pair is not used: an event-timed launch that
   // follows one without events reads ~1.5 us longer (its start event is taken
   // while the launch before it still drains), so the gate/up launch is timed
   // after an event-timed launch as the down launch is.
   hipEvent_t* ev = m->expert_events ? m->expert_events + 6 * m->expert_slot++ : nullptr;
-  span_class("moe-router");
-  KNJ_HIP(launch_router(ra, s, ev ? ev[4] : nullptr, ev ? ev[5] : nullptr));
+  float* const u = m->router_logits + (uint64_t)il * c.n_expert;
+  // with the router folded in, attn-o writes the residual stream into x2 (its
+  // router rows still read x) and the MoE goes from x2 back to x
+  float* const xm = m->fold_router ? m->x2 : m->x;
+  GemvArgs o{c.type_attn, img + lo.wo, QD, H, m->ctx, nullptr, 0.0f, m->x, xm, nullptr};
+  if (m->fold_router) {
+    span_class("attn-o+moe-router");
+    const float* R = m->router_fold + (uint64_t)il * c.n_expert * (H + QD);
+    KNJ_HIP(launch_gemv_router(o, R, c.n_expert, u, s, ev ? ev[4] : nullptr, ev ? ev[5] : nullptr));
+  } else {
+    span_class("attn-o");
+    KNJ_HIP(launch_gemv(o, s));
+    RouterArgs ra{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
+                  reinterpret_cast<const float*>(img + lo.router), H, c.n_expert, c.n_expert_used,
+                  m->hx, u, nullptr, nullptr, m->counter};
+    span_class("moe-router");
+    KNJ_HIP(launch_router(ra, s, ev ? ev[4] : nullptr, ev ? ev[5] : nullptr));
+  }
   // the gate/up launch routes from the logits (softmax + top-k per wave)
   int32_t* ti = m->topk_idx + (uint64_t)il * c.n_expert_used;
   float* tw = m->topk_w + (uint64_t)il * c.n_expert_used;
-  ExpertArgs ea{m->x, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps,
-                m->router_logits + (uint64_t)il * c.n_expert, ti, tw,
+  ExpertArgs ea{xm, reinterpret_cast<const float*>(img + lo.ffn_norm), c.rms_eps, u, ti, tw,
                 img + lo.gate, img + lo.up, img + lo.down,
-                c.type_gate_up, c.type_down, H, c.n_ff, c.n_expert, c.n_expert_used, m->act, m->x,
+                c.type_gate_up, c.type_down, H, c.n_ff, c.n_expert, c.n_expert_used, m->act, xm,
                 m->x, m->hidden + (uint64_t)il * H};
+  ea.logits_unscaled = m->fold_router;
   span_class("moe-gate+up+act");
   KNJ_HIP(launch_expert_gateup(ea, s, ev ? ev[0] : nullptr, ev ? ev[1] : nullptr));
   span_class("moe-down+scatter");
@@ -406,8 +418,42 @@ int set_state(knj_model* m, int32_t token, int step) {
   return KNJ_OK;
 }
 
+// The router folded into the attention-output launch (k_gemv_q4k_router):
+// per layer R = [W_r * ffn_norm | (W_r * ffn_norm) W_o], from the weights in
+// the image, computed once when the model is created.
+int fold_router(knj_model* m) {
+  const knj_model_config& c = m->c;
+  const int H = c.n_embd, QD = c.n_head * c.head_dim, E = c.n_expert;
+  m->fold_router = router_fold_ok(c.type_attn, QD, H, E) && E <= 128 && H <= 2048 &&
+                   c.n_expert_used <= 16 && !std::getenv("KNJ_NO_ROUTER_FOLD");
+  if (!m->fold_router) return KNJ_OK;
+  const uint64_t NR = (uint64_t)H + QD;
+  int rc = alloc(m, (void**)&m->router_fold, (uint64_t)c.n_layer * E * NR * 4);
+  if (rc) return rc;
+  float* wd = nullptr;
+  KNJ_HIP(hipMalloc(&wd, (uint64_t)H * QD * 4));
+  hipError_t e = hipSuccess;
+  for (int il = 0; il < c.n_layer && e == hipSuccess; ++il) {
+    const knj_layer_offsets& lo = m->lo[il];
+    e = launch_dequant(c.type_attn, m->image + lo.wo, (uint64_t)H * QD, wd, m->stream);
+    if (e == hipSuccess)
+      e = launch_router_fold(reinterpret_cast<const float*>(m->image + lo.router),
+                             reinterpret_cast<const float*>(m->image + lo.ffn_norm), wd, H, QD, E,
+                             m->router_fold + (uint64_t)il * E * NR, m->stream);
+  }
+  if (e == hipSuccess) e = hipStreamSynchronize(m->stream);
+  (void)hipFree(wd);
+  if (e != hipSuccess) return hip_fail(e, "router fold");
+  return KNJ_OK;
+}
+
 int finish_create(knj_model* m, knj_model** out) {
-  int rc = ensure_graph(m);
+  int rc = fold_router(m);
+  if (rc) {
+    knj_model_free(m);
+    return rc;
+  }
+  rc = ensure_graph(m);
   if (rc) {
     knj_model_free(m);
     return rc;

@@ -31,6 +31,11 @@ struct knj_model {
   hipStream_t stream = nullptr;
   // activations
   float *x = nullptr, *qkv = nullptr, *ctx = nullptr, *hx = nullptr, *act = nullptr;
+  // with the router folded into the attention-output launch: that launch's
+  // output (the residual stream between attn-o and the MoE), and per layer
+  // the folded router rows [n_expert][n_embd + n_head * head_dim]
+  float *x2 = nullptr, *router_fold = nullptr;
+  bool fold_router = false;
   float *logits = nullptr, *router_logits = nullptr, *hidden = nullptr, *topk_w = nullptr;
   int32_t* topk_idx = nullptr;
   float *rope_cos = nullptr, *rope_sin = nullptr, *rope_cur = nullptr, *attn_part = nullptr;

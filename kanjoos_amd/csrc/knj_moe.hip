@@ -460,8 +460,23 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_expert_gateup_r(ExpertArgs a)
   const bool xw = wave >= 1 && wave <= 4;
   float4 x4[2], w4[2];
   if (wave == 0) {
-    const float lg0 = lane < E ? a.logits[lane] : -INFINITY;
-    const float lg1 = lane + 64 < E ? a.logits[lane + 64] : -INFINITY;
+    float lg0 = lane < E ? a.logits[lane] : -INFINITY;
+    float lg1 = lane + 64 < E ? a.logits[lane + 64] : -INFINITY;
+    if (a.logits_unscaled) {
+      // the RMSNorm scale of the router's input (model.cpp:240-271), from hx
+      float4 hv[8];  // n_embd <= 2048: all loads issued before the sum
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        hv[j] = 4 * lane + 256 * j < H ? *reinterpret_cast<const float4*>(a.hx + 4 * lane + 256 * j)
+                                       : make_float4(0.f, 0.f, 0.f, 0.f);
+      float ss = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += hv[j].x * hv[j].x + hv[j].y * hv[j].y + hv[j].z * hv[j].z + hv[j].w * hv[j].w;
+      ss = group_sum<64>(ss);
+      const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
+      lg0 *= scale;
+      lg1 *= scale;
+    }
     const float mx = group_max<64>(fmaxf(lg0, lg1));
     const float ex0 = lane < E ? expf(lg0 - mx) : 0.0f;
     const float ex1 = lane + 64 < E ? expf(lg1 - mx) : 0.0f;
@@ -1273,6 +1288,9 @@ hipError_t launch_topk(const float* logits, int n_expert, int k, int32_t* idx, f
 
 hipError_t launch_expert_gateup(const ExpertArgs& a, hipStream_t s, hipEvent_t t0, hipEvent_t t1) {
   const int npairs = a.k * a.n_ff;
+  // unscaled logits: only the one-routing-wave kernel applies the scale
+  if (a.logits_unscaled && !(a.logits && a.n_embd <= 2048 && a.n_expert <= 128 && a.k <= 16))
+    return hipErrorInvalidValue;
   if (a.logits && a.n_embd <= 2048 && a.n_expert <= 128 && a.k <= 16) {
     const int grid = (npairs + 2 * kGuWaves - 1) / (2 * kGuWaves);
     launch_maybe_timed(k_expert_gateup_r, "k_expert_gateup", dim3(grid), 0, s, t0, t1, a, 64 * kGuWaves);
