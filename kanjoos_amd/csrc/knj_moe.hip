@@ -459,31 +459,35 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_expert_gateup_r(ExpertArgs a)
   const int tx = t - 64;  // waves 1-4 stage x as the 256 threads of k_expert_gateup
   const bool xw = wave >= 1 && wave <= 4;
   float4 x4[2], w4[2];
+  // wave 0's logits and selection, kept for the softmax weights of
+  // unscaled logits (workgroup 0, after the first barrier)
+  float lg0 = -INFINITY, lg1 = -INFINITY;
+  int r0 = 0, r1 = 0;
+  bool c0 = false, c1 = false;
   if (wave == 0) {
-    float lg0 = lane < E ? a.logits[lane] : -INFINITY;
-    float lg1 = lane + 64 < E ? a.logits[lane + 64] : -INFINITY;
+    lg0 = lane < E ? a.logits[lane] : -INFINITY;
+    lg1 = lane + 64 < E ? a.logits[lane + 64] : -INFINITY;
+    uint32_t pb0, pb1;  // selection keys, 0: no expert
+    float p0 = 0.0f, p1 = 0.0f;
     if (a.logits_unscaled) {
-      // the RMSNorm scale of the router's input (model.cpp:240-271), from hx
-      float4 hv[8];  // n_embd <= 2048: all loads issued before the sum
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        hv[j] = 4 * lane + 256 * j < H ? *reinterpret_cast<const float4*>(a.hx + 4 * lane + 256 * j)
-                                       : make_float4(0.f, 0.f, 0.f, 0.f);
-      float ss = 0.0f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += hv[j].x * hv[j].x + hv[j].y * hv[j].y + hv[j].z * hv[j].z + hv[j].w * hv[j].w;
-      ss = group_sum<64>(ss);
-      const float scale = 1.0f / sqrtf(ss / (float)H + a.eps);
-      lg0 *= scale;
-      lg1 *= scale;
+      // the softmax of s * logit with s > 0 ranks as the logits do: select on
+      // order-preserving keys of the logits themselves (-0 taken as +0)
+      auto okey = [](float v) {
+        const uint32_t b = __float_as_uint(v + 0.0f);
+        return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+      };
+      pb0 = lane < E ? okey(lg0) + 1u : 0u;
+      pb1 = lane + 64 < E ? okey(lg1) + 1u : 0u;
+    } else {
+      const float mx = group_max<64>(fmaxf(lg0, lg1));
+      const float ex0 = lane < E ? expf(lg0 - mx) : 0.0f;
+      const float ex1 = lane + 64 < E ? expf(lg1 - mx) : 0.0f;
+      const float sum = group_sum<64>(ex0) + group_sum<64>(ex1);
+      p0 = ex0 / sum;
+      p1 = ex1 / sum;
+      pb0 = lane < E ? __float_as_uint(p0) + 1u : 0u;
+      pb1 = lane + 64 < E ? __float_as_uint(p1) + 1u : 0u;
     }
-    const float mx = group_max<64>(fmaxf(lg0, lg1));
-    const float ex0 = lane < E ? expf(lg0 - mx) : 0.0f;
-    const float ex1 = lane + 64 < E ? expf(lg1 - mx) : 0.0f;
-    const float sum = group_sum<64>(ex0) + group_sum<64>(ex1);
-    const float p0 = ex0 / sum, p1 = ex1 / sum;
-    const uint32_t pb0 = lane < E ? __float_as_uint(p0) + 1u : 0u;  // 0: no expert
-    const uint32_t pb1 = lane + 64 < E ? __float_as_uint(p1) + 1u : 0u;
     auto gmax8 = [](uint32_t v) {
       v = max(v, dpp_u32<kDppXor1>(v));
       v = max(v, dpp_u32<kDppXor2>(v));
@@ -511,9 +515,9 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_expert_gateup_r(ExpertArgs a)
     if (n_group >= a.k)
       thr = ta ? (uint32_t)__builtin_amdgcn_readlane((int)gm0, (int)__builtin_ctzll(ta))
                : (uint32_t)__builtin_amdgcn_readlane((int)gm1, (int)__builtin_ctzll(tb));
-    const bool c0 = lane < E && pb0 >= thr, c1 = lane + 64 < E && pb1 >= thr;
+    c0 = lane < E && pb0 >= thr;
+    c1 = lane + 64 < E && pb1 >= thr;
     unsigned long long m0 = __ballot(c0), m1 = __ballot(c1);
-    int r0 = 0, r1 = 0;
     while (m0 | m1) {
       const bool hi = m0 == 0;
       const int l = (int)__builtin_ctzll(hi ? m1 : m0);
@@ -568,6 +572,20 @@ __global__ __launch_bounds__(64 * kGuWaves) void k_expert_gateup_r(ExpertArgs a)
   load_pair(pair0, q0);
   load_pair(pair0 + 1, q1);
   __builtin_amdgcn_sched_barrier(0);
+  if (a.logits_unscaled && blockIdx.x == 0 && wave == 0) {
+    // the routing weights (written by workgroup 0 only): softmax of the
+    // logits times the RMSNorm scale of hx (model.cpp:240-271, 438-441), the
+    // scale from waves 1-4's sum of squares of the same hx
+    const float sst = ((red[0] + red[1]) + red[2]) + red[3];
+    const float scale = 1.0f / sqrtf(sst / (float)H + a.eps);
+    const float l0 = lg0 * scale, l1 = lg1 * scale;
+    const float mx = group_max<64>(fmaxf(l0, l1));
+    const float ex0 = lane < E ? expf(l0 - mx) : 0.0f;
+    const float ex1 = lane + 64 < E ? expf(l1 - mx) : 0.0f;
+    const float sum = group_sum<64>(ex0) + group_sum<64>(ex1);
+    if (c0 && r0 < a.k) selp[r0] = ex0 / sum;
+    if (c1 && r1 < a.k) selp[r1] = ex1 / sum;
+  }
   // x normalised into LDS with its 32-element sub-block sums (as k_expert_gateup)
   if (xw) {
     const float sst = ((red[0] + red[1]) + red[2]) + red[3];
