@@ -16,6 +16,12 @@
                        of one to three tokens for every one of 40 prompt seeds
                        tried (4096-4135, GPU only); the prompt uses seed 4121,
                        the one whose cycle has three distinct tokens.
+  config 5 greedy      the same over config 5's workload: Q6_K expert down and
+                       LM head, a 32768-token cache written by the GPU prompt
+                       pass, 64 free-running greedy steps (measured: one
+                       repeated token, smallest top-1/top-2 margin 5.4% of the
+                       largest logit, logits within 4.9e-6 of the oracle's at
+                       every step).
   prompt pass          the prompt pass itself at full width (2048 hidden, 32/4
                        heads x 128, 128 experts top-8) against the oracle's
                        batched forward (model.cpp:354-364 matmul with m > 1,
@@ -90,6 +96,59 @@ def test_config3_free_running_greedy_64(device):
             toks_o.append(to)
         assert toks_g == toks_o
         progress(f"free-running greedy: {steps} steps identical ({len(set(toks_g))} distinct tokens), "
+                 f"smallest margin {min(r[2] for r in rows):.3g}, largest logit diff "
+                 f"{max(r[3] for r in rows):.3g}")
+    finally:
+        if om is not None:
+            om.close()
+        gm.close()
+
+
+def test_config5_free_running_greedy_64(device):
+    """Config 5's workload free-running: the 48-layer model with Q6_K expert
+    down and LM head, a 32768-slot cache written by the GPU prompt pass (in
+    calls of 4096 ids), then 64 greedy steps on each side with its own cache.
+    Tokens must be identical at every step and the logits within 1e-4
+    relative RMSE of the oracle's."""
+    ctx, steps = 32768, 64
+    cfg = dict(n_ctx=ctx + steps + 8, type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)
+    progress("config 5 free-running greedy: 48-layer Q6_K-down/head model, GPU prompt pass over 32768 ids")
+    gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    om = None
+    try:
+        prompt = np.random.default_rng(32768).integers(0, 151936, ctx).astype(np.int32)
+        lg = None
+        for c0 in range(0, ctx, 4096):
+            lg = gm.forward(prompt[c0:c0 + 4096], want_logits=c0 + 4096 >= ctx)
+            progress(f"config 5 free-running greedy: prompt pass at {gm.pos}")
+        assert gm.pos == ctx
+        img = gm.download_image()
+        om = O.OracleModel(O.make_config(**cfg), seed=SEED, image=img, threads=THREADS)
+        del img
+        k, v = gm.kv_download()
+        ok, ov = om.kv()
+        ok[...] = k
+        ov[...] = v
+        del k, v
+        om.set_pos(ctx)
+        tok = int(np.argmax(lg))
+        toks, rows = [tok], []
+        tg = to = tok
+        for st in range(steps):
+            lg = gm.forward([tg])
+            lw = om.forward([to])
+            tg, to = int(np.argmax(lg)), int(np.argmax(lw))
+            mo, _ = margin(lw)
+            scale = float(np.max(np.abs(lw)))
+            diff = float(np.max(np.abs(lg.astype(np.float64) - lw))) / scale
+            rows.append((st, to, mo / scale, diff))
+            progress(f"config 5 greedy step {st} at pos {gm.pos - 1}: gpu {tg} oracle {to}, oracle margin "
+                     f"{mo / scale:.3g} of the largest logit, max |logit diff| {diff:.3g}, "
+                     f"rel-RMSE {rel_rmse(lg, lw):.3g}")
+            assert tg == to, (st, tg, to, mo / scale, diff)
+            assert rel_rmse(lg, lw) <= 1e-4, (st, rel_rmse(lg, lw))
+            toks.append(tg)
+        progress(f"config 5 free-running greedy: {steps} steps identical ({len(set(toks))} distinct tokens), "
                  f"smallest margin {min(r[2] for r in rows):.3g}, largest logit diff "
                  f"{max(r[3] for r in rows):.3g}")
     finally:
