@@ -22,6 +22,11 @@
                        repeated token, smallest top-1/top-2 margin 5.4% of the
                        largest logit, logits within 4.9e-6 of the oracle's at
                        every step).
+  config 4 greedy      32 sequences whose caches the GPU prompt pass wrote
+                       (2048 ids each) decode 32 lockstep greedy steps; 4 of
+                       them free-running against their own oracle models
+                       (measured: each a repeated token, smallest margin 1.1%
+                       of the largest logit, logits within 1.9e-6).
   prompt pass          the prompt pass itself at full width (2048 hidden, 32/4
                        heads x 128, 128 experts top-8) against the oracle's
                        batched forward (model.cpp:354-364 matmul with m > 1,
@@ -154,6 +159,67 @@ def test_config5_free_running_greedy_64(device):
     finally:
         if om is not None:
             om.close()
+        gm.close()
+
+
+def test_config4_free_running_greedy_32(device):
+    """Config 4's workload free-running: 32 sequences, each cache written by a
+    GPU prompt pass over 2048 ids, then 32 lockstep greedy steps of the batch
+    (every sequence fed its own argmax); 4 of the sequences decode on their
+    own oracle model from the same cache, each side keeping its own cache.
+    Tokens must be identical at every step and the logits within 1e-4
+    relative RMSE of the oracle's."""
+    n_seq, ctx, steps, check = 32, 2048, 32, 4
+    cfg = dict(n_ctx=ctx + steps + 8)
+    progress("config 4 free-running greedy: 48-layer model, 32 prompt passes of 2048 ids")
+    gm = K.Model.synthetic(K.qwen3_30b_a3b(**cfg), seed=SEED)
+    batch = K.Batch(gm, n_seq, ctx + steps + 8)
+    oms = []
+    try:
+        img = gm.download_image()
+        picked = list(range(3, n_seq, n_seq // check))
+        rng = np.random.default_rng(20480)
+        first = np.zeros(n_seq, np.int32)
+        for sq in range(n_seq):
+            gm.reset()
+            lg = gm.forward([int(t) for t in rng.integers(0, 151936, ctx)])
+            first[sq] = int(np.argmax(lg))
+            k, v = gm.kv_download()
+            batch.kv_upload(sq, k, v)
+            if sq in picked:
+                om = O.OracleModel(O.make_config(**cfg), seed=SEED, image=img, threads=THREADS)
+                ok, ov = om.kv()
+                ok[...] = k
+                ov[...] = v
+                om.set_pos(ctx)
+                oms.append(om)
+        del img
+        batch.set_pos(ctx)
+        tg = first.copy()
+        to = [int(first[sq]) for sq in picked]
+        seqs = [[t] for t in to]
+        worst, smallest = 0.0, 1.0
+        for st in range(steps):
+            lg = batch.forward(tg)
+            tg = lg.argmax(axis=1).astype(np.int32)
+            for j, sq in enumerate(picked):
+                lw = oms[j].forward([to[j]])
+                to[j] = int(np.argmax(lw))
+                mo, _ = margin(lw)
+                e = rel_rmse(lg[sq], lw)
+                worst, smallest = max(worst, e), min(smallest, mo / float(np.max(np.abs(lw))))
+                assert int(tg[sq]) == to[j], (st, sq, int(tg[sq]), to[j])
+                assert e <= 1e-4, (st, sq, e)
+                seqs[j].append(to[j])
+            progress(f"config 4 greedy step {st}: sequences {picked} tokens {[int(tg[q]) for q in picked]}, "
+                     f"worst logits rel-RMSE so far {worst:.3g}")
+        progress(f"config 4 free-running greedy: {steps} steps identical on {check} sequences "
+                 f"({[len(set(q)) for q in seqs]} distinct tokens), smallest margin {smallest:.3g}, "
+                 f"largest logits rel-RMSE {worst:.3g}")
+    finally:
+        for om in oms:
+            om.close()
+        batch.close()
         gm.close()
 
 
