@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE's full workloads: the 48-layer Qwen3-30B-A3B-shaped
+"""GPU parity at the benchmark configurations' full workloads: the 48-layer Qwen3-30B-A3B-shaped
 model against the CPU oracle (a restatement of /root/reference/src/model/
 model.cpp:512-672) on the same weights and the same KV cache contents.
 
@@ -13,7 +13,7 @@ model.cpp:512-672) on the same weights and the same KV cache contents.
             written by a GPU prompt pass over 32768 random token ids; two
             decode steps.
 
-The caches come from prompt passes over token ids, as BASELINE's configs
+The caches come from prompt passes over token ids, as the benchmark configurations
 state.  A cache of seeded random f16 values (knj_*_fill_kv, which the
 throughput legs use) makes every attention output a sum of thousands of
 uncorrelated values that nearly cancel; the f32 rounding of the oracle's

@@ -1,4 +1,4 @@
-"""GPU parity over long runs at BASELINE's full widths, against the CPU oracle
+"""GPU parity over long runs at the benchmark configurations' full widths, against the CPU oracle
 (a restatement of /root/reference/src/model/model.cpp:512-672).
 
   free-running greedy  config 3's workload: the 48-layer model, a 4096-token
