@@ -48,6 +48,11 @@ struct knj_model {
   int pos = 0;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  // several decode steps captured back to back (decode loops replay it while
+  // at least that many steps remain)
+  hipGraph_t graph_multi = nullptr;
+  hipGraphExec_t exec_multi = nullptr;
+  int multi = 0;
   bool use_graph = true;  // KNJ_NO_GRAPH=1 launches the step's kernels directly
   // prompt pass over several rows at once (KNJ_PROMPT_STEPS=1 feeds prompts
   // one decode step per token instead)
