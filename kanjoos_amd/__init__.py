@@ -188,7 +188,7 @@ def lib():
 
 def check(rc: int) -> None:
     if rc != KNJ_OK:
-        raise KnjError(rc, lib().knj_last_error().decode())
+        raise KnjError(rc, lib().knj_last_error().decode(errors="replace"))
 
 
 def _ptr(a: np.ndarray):

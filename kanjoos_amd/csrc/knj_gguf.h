@@ -25,6 +25,25 @@
 
 namespace knj {
 
+// A string read from a file, as it may appear in an error message: printable
+// ASCII kept, every other byte as \xNN, at most 64 bytes of it.
+inline std::string gguf_printable(const std::string& v) {
+  static const char* hex = "0123456789abcdef";
+  std::string out;
+  for (size_t i = 0; i < v.size() && i < 64; ++i) {
+    const unsigned char ch = (unsigned char)v[i];
+    if (ch >= 0x20 && ch < 0x7f) {
+      out += (char)ch;
+    } else {
+      out += "\\x";
+      out += hex[ch >> 4];
+      out += hex[ch & 15];
+    }
+  }
+  if (v.size() > 64) out += "...";
+  return out;
+}
+
 struct GgufScalar {
   enum Kind { kInt, kFloat, kString } kind = kInt;
   int64_t i = 0;
@@ -181,7 +200,7 @@ class GgufView {
     for (uint64_t i = 0; i < n_tensors; ++i) {
       GgufTensor& t = tensors_[(size_t)i];
       if (!rd_str(t.name) || !rd(t.n_dims)) return false;
-      if (t.n_dims < 1 || t.n_dims > 4) return fail("tensor '" + t.name + "': bad rank");
+      if (t.n_dims < 1 || t.n_dims > 4) return fail("tensor '" + gguf_printable(t.name) + "': bad rank");
       for (uint32_t d = 0; d < t.n_dims; ++d)
         if (!rd(t.dims[d])) return false;
       if (!rd(t.type) || !rd(t.offset)) return false;
@@ -189,7 +208,7 @@ class GgufView {
       // refused by the binder only if the path needs them
       if (knj_row_bytes((int)t.type, 256) != 0) {
         if (t.dims[0] % knj_block_weights((int)t.type))
-          return fail("tensor '" + t.name + "': row not a whole number of blocks");
+          return fail("tensor '" + gguf_printable(t.name) + "': row not a whole number of blocks");
         t.bytes = knj_row_bytes((int)t.type, t.dims[0]);
         for (uint32_t d = 1; d < t.n_dims; ++d) t.bytes *= t.dims[d];
       }
@@ -201,7 +220,7 @@ class GgufView {
     data_ = (pos_ + (uint64_t)align - 1) / (uint64_t)align * (uint64_t)align;
     for (const GgufTensor& t : tensors_)
       if (data_ > size_ || t.offset > size_ - data_ || t.bytes > size_ - data_ - t.offset)
-        return fail("tensor '" + t.name + "' extends past the end of the file");
+        return fail("tensor '" + gguf_printable(t.name) + "' extends past the end of the file");
     return true;
   }
 

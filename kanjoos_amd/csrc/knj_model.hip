@@ -520,7 +520,7 @@ namespace {
 int gguf_config(const GgufView& g, int n_ctx, knj_model_config* c) {
   const std::string arch = g.meta_string("general.architecture");
   if (arch != "qwen3moe") {
-    set_error("model: architecture is '" + arch + "', this path implements 'qwen3moe'");
+    set_error("model: architecture is '" + gguf_printable(arch) + "', this path implements 'qwen3moe'");
     return KNJ_E_ARG;
   }
   const std::string p = arch + ".";

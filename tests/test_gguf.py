@@ -88,6 +88,38 @@ def test_probe_errors(tmp_path, gguf_path):
     _expect_error(str(p), 160, "bad magic")
 
 
+def test_probe_corrupt_files_fail_cleanly(tmp_path):
+    """Truncations and random byte changes in the header, metadata and tensor
+    table of a small model's GGUF: the probe either accepts the file (a
+    change that leaves it consistent) or refuses it with an error, and never
+    reads out of bounds (a crash would end the test run; the same set ran
+    clean under AddressSanitizer)."""
+    cfg = dict(n_layer=1, n_embd=256, n_head=4, n_head_kv=2, head_dim=64, n_ff=256, n_expert=8,
+               n_expert_used=2, n_vocab=512, n_ctx=64)
+    c, img = zero_image(cfg)
+    base = tmp_path / "base.gguf"
+    write_gguf(base, qwen3moe_meta(cfg), tensors_from_image(c, img))
+    raw = base.read_bytes()
+    head = min(len(raw), 6000)
+    rng = np.random.default_rng(7)
+    p = tmp_path / "bad.gguf"
+    accepted = refused = 0
+    cases = [raw[:int(n)] for n in rng.integers(0, head, 60)]
+    for _ in range(200):
+        b = bytearray(raw)
+        for pos in rng.integers(0, head, int(rng.integers(1, 6))):
+            b[int(pos)] = int(rng.integers(0, 256))
+        cases.append(bytes(b))
+    for data in cases:
+        p.write_bytes(data)
+        try:
+            K.gguf_probe(str(p), 64)
+            accepted += 1
+        except K.KnjError:
+            refused += 1
+    assert refused >= 60 and accepted + refused == len(cases)
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("cfgkw", [dict(), dict(type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)])
 def test_gguf_roundtrip_model(device, tmp_path, cfgkw):
