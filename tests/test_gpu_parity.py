@@ -245,7 +245,10 @@ def step_parity(om, gm, tokens, n_layer, tol=1e-5):
     return worst, lg, lw
 
 
-@pytest.mark.parametrize("cfgkw", [dict(), dict(type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)])
+@pytest.mark.parametrize("cfgkw", [dict(), dict(type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K),
+                                   # 64 experts top-6 over 1024-wide rows: the folded router's
+                                   # rows and the selection at another shape
+                                   dict(n_embd=1024, head_dim=128, n_expert=64, n_expert_used=6)])
 def test_small_model_step_parity(device, cfgkw):
     cfg = small_config(**cfgkw)
     say(f"small model per-step parity {cfg}")
