@@ -468,12 +468,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
   // unrolled form every wave does, the same bytes, so that all waves issue
   // the same number of loads and the compiler's count of outstanding loads
   // stays exact along the straight line
+  // (entry e = 512 w + 64 u + lane: part w / 2, 8-group 16 (w & 1) + 2 u +
+  // lane / 32, pair lane % 32; so the source is a part base the wave shares,
+  // plus a per-lane byte offset that does not change, plus 2 u P 16 bytes)
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const uint8_t* sbase = reinterpret_cast<const uint8_t*>((wv >> 1) ? a.al : a.ah);
+  const uint32_t soff =
+      (uint32_t)(((uint64_t)(16 * (wv & 1) + (lane >> 5)) * P + p0 + min(lane & 31, cnt - 1)) * 16);
   auto stage = [&](int sb, int buf) {
+    const uint8_t* b = sbase + (uint64_t)sb * 32 * P * 16;
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
-      const int e0 = (8 * wave + u) * 64, e = e0 + lane;
-      const int part = e >> 10, r = e & 1023, q = r >> 5, jj = r & 31;
-      const _Float16* src = (part ? a.al : a.ah) + ((uint64_t)(32 * sb + q) * P + p0 + min(jj, cnt - 1)) * 8;
+      const int e0 = (8 * wave + u) * 64;
+      const uint8_t* src = b + (uint64_t)u * 2 * P * 16 + soff;
       __builtin_amdgcn_global_load_lds((glb_void*)src, (lds_void*)(lds + buf * kBuf + e0), 16, 0, 0);
     }
     if (NSBT > 0 || wave == 0) {
@@ -492,8 +499,8 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
   // Weight register sets.  Fixed range (NSBT > 0, fully unrolled): three sets
   // in rotation, the weights of super-block i + 2 loaded while i is computed;
   // a straight line, so no register copies wait for loads and the compiler's
-  // wait counts are exact.  Any range: the weights of i + 1 go to set 1 while
-  // set 0 is computed, then are copied over.
+  // wait counts are exact.  Any range: the weights of i + 1 go to the other
+  // of two sets while one is computed.
   WBlock w0s[3], w1s[3];
   const int n_it = NSBT > 0 ? NSBT : nsb - sbb;
   stage(sbb, 0);
@@ -506,11 +513,9 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
   } else {
     KNJ_BARRIER_VM(0);
   }
-  constexpr int kUnroll = NSBT > 0 ? NSBT : 1;
-#pragma unroll kUnroll
-  for (int i = 0; i < n_it; ++i) {
+  // super-block i on register set ci, the next weights into set ni
+  auto step = [&](int i, int ci, int ni) __attribute__((always_inline)) {
     const int buf = i & 1;
-    const int ci = NSBT > 0 ? i % 3 : 0, ni = NSBT > 0 ? (i + 2) % 3 : 1;
     // every load of a later super-block is issued before this one's
     // arithmetic, the staging first: the memory counter is in order, so
     // the wait for the staging at the end leaves the weights in flight
@@ -594,16 +599,12 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
       const float d1 = h2f(w1c.h.x), m1 = h2f(w1c.h.x >> 16);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        acc0[r] += d0 * cqa[r] - m0 * cm0[r];
-        acc1[r] += d1 * cqb[r] - m1 * cm1[r];
+        acc0[r] = __builtin_fmaf(d0, cqa[r], __builtin_fmaf(-m0, cm0[r], acc0[r]));
+        acc1[r] = __builtin_fmaf(d1, cqb[r], __builtin_fmaf(-m1, cm1[r], acc1[r]));
       }
     } else {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc0[r] += d0 * (cqa[r] + cqb[r]) - m0 * cm0[r];
-    }
-    if constexpr (NSBT == 0) {
-      w0s[0] = w0s[1];
-      if constexpr (GATEUP) w1s[0] = w1s[1];
     }
     // the staging done (at most the weight loads issued after it
     // outstanding) before the barrier that hands the buffer over
@@ -611,6 +612,19 @@ __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(2))) voi
       KNJ_BARRIER_VM(WN);
     else
       KNJ_BARRIER_VM(0);
+  };
+  if constexpr (NSBT > 0) {
+#pragma unroll
+    for (int i = 0; i < NSBT; ++i) step(i, i % 3, (i + 2) % 3);
+  } else {
+    // two register sets in turn, so no set is copied (a copy waits for
+    // its loads)
+    int i = 0;
+    for (; i + 2 <= n_it; i += 2) {
+      step(i, 0, 1);
+      step(i + 1, 1, 0);
+    }
+    if (i < n_it) step(i, 0, 1);
   }
   __builtin_amdgcn_s_waitcnt(0);
   if constexpr (GATEUP) {
