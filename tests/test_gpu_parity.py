@@ -261,24 +261,33 @@ def test_small_model_step_parity(device, cfgkw):
 def test_small_model_step_parity_router_unfolded(device, monkeypatch):
     """The same with KNJ_NO_ROUTER_FOLD=1: the router as a launch of its own
     after the attention output (the path for shapes the folded router does
-    not take), and the folded model's logits against it."""
+    not take), and the folded model beside it, each against its own oracle
+    model step by step (per-layer hidden and logits <= 1e-5, top-k exact).
+    The two GPU models are not held to 1e-5 of each other: each keeps its own
+    f16 cache, and a last-bit difference of a layer's input (the router's two
+    forms round differently) can flip the f16 rounding of a new cache element,
+    which moves that layer's output by up to ~1e-4 (measured: 3.5e-5 at one
+    step when both start the step from the same cache); the oracle adopts
+    each side's f16 values after checking they are roundings of its own."""
     cfg = small_config()
     say(f"small model per-step parity, router unfolded {cfg}")
     om = O.OracleModel(O.make_config(**cfg), seed=SEED)
+    of = O.OracleModel(O.make_config(**cfg), seed=SEED)
     monkeypatch.setenv("KNJ_NO_ROUTER_FOLD", "1")
     gm = K.Model.from_image(K.qwen3_30b_a3b(**cfg), om.image())
     monkeypatch.delenv("KNJ_NO_ROUTER_FOLD")
     gf = K.Model.from_image(K.qwen3_30b_a3b(**cfg), om.image())
     toks = [11, 22, 33, 44, 55, 66, 77, 88]
     try:
-        lf = [gf.forward([t]) for t in toks]
         worst, lg, _ = step_parity(om, gm, toks, cfg["n_layer"])
-        say(f"unfolded: worst per-layer rel-RMSE {worst:.3g}, folded vs unfolded logits "
-            f"{rel_rmse(lf[-1], lg):.3g}")
-        assert rel_rmse(lf[-1], lg) <= 1e-5
+        worst_f, lf, _ = step_parity(of, gf, toks, cfg["n_layer"])
+        say(f"unfolded: worst per-layer rel-RMSE {worst:.3g}; folded {worst_f:.3g}; folded vs "
+            f"unfolded logits after {len(toks)} steps {rel_rmse(lf, lg):.3g}")
     finally:
         gm.close()
         gf.close()
+        om.close()
+        of.close()
 
 
 @pytest.mark.parametrize("cfgkw", [dict(), dict(type_down=K.TYPE_Q6_K, type_head=K.TYPE_Q6_K)])
