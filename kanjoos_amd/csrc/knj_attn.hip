@@ -306,14 +306,15 @@ __global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) { 
       // A = K (16 slots x 32 dims per step), B = the queries (hi, then lo)
       const int p = 16 * wave + r;
       const uint8_t* krow = ks + p * RB;
+      // (columns past G take head G - 1's queries: their scores, in
+      // columns of their own, are never stored)
       const int hq = min(r, G - 1);
-      const h16x8 zero8 = {};
       f32x4 sa = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int c = 0; c < D / 32; ++c) {
         const h16x8 ka = __builtin_bit_cast(h16x8, *reinterpret_cast<const uint4*>(krow + 16 * kslot(p, 4 * c + kq)));
-        const h16x8 bh = hv ? *reinterpret_cast<const h16x8*>(qh + hq * ROWH + 32 * c + 8 * kq) : zero8;
-        const h16x8 bl = hv ? *reinterpret_cast<const h16x8*>(ql + hq * ROWH + 32 * c + 8 * kq) : zero8;
+        const h16x8 bh = *reinterpret_cast<const h16x8*>(qh + hq * ROWH + 32 * c + 8 * kq);
+        const h16x8 bl = *reinterpret_cast<const h16x8*>(ql + hq * ROWH + 32 * c + 8 * kq);
         sa = mfma16(ka, bh, sa);
         sa = mfma16(ka, bl, sa);
       }
@@ -337,8 +338,23 @@ __global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) { 
       l1 = l1 * a1 + group_sum<64>(e1);
       m0 = n0;
       m1 = n1;
-      es[h0 * EROW + lane] = e0;
-      if (h1 < G) es[h1 * EROW + lane] = e1;
+      // the weights replace the scores in the head's row (this wave's reads
+      // of the row are done: one wave's LDS accesses complete in order) as
+      // f16 high parts (halves 0..63) and remainders (64..127), slot
+      // 32 c + 16 u + 4 q + i at half 32 c + 8 q + 4 u + i, so that the
+      // value product's lane (q, row) reads its eight weights of step c
+      // (slots 32 c + 4 q + i and 32 c + 16 + 4 q + i) as one 16-byte piece
+      const int ps = (lane & 32) | ((lane & 12) << 1) | ((lane & 16) >> 2) | (lane & 3);
+      _Float16* w0 = reinterpret_cast<_Float16*>(es + h0 * EROW);
+      const _Float16 e0h = (_Float16)e0;
+      w0[ps] = e0h;
+      w0[64 + ps] = (_Float16)(e0 - (float)e0h);
+      if (h1 < G) {
+        _Float16* w1 = reinterpret_cast<_Float16*>(es + h1 * EROW);
+        const _Float16 e1h = (_Float16)e1;
+        w1[ps] = e1h;
+        w1[64 + ps] = (_Float16)(e1 - (float)e1h);
+      }
       if (lane == 0) {
         alpha[h0] = a0;
         if (h1 < G) alpha[h1] = a1;
@@ -363,7 +379,9 @@ __global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) { 
     // transposed reads of rows 32c (+16) + 4kq + r/4, dims 4(r%4) .. +3 of
     // the tile, which deliver dim r of the four rows
     if (32 * wave < D) {
-      const float* erow = es + min(r, G - 1) * EROW + 4 * kq;
+      // (rows past G read head G - 1's weights: their outputs, in rows of
+      // their own, are never stored)
+      const _Float16* erow = reinterpret_cast<const _Float16*>(es + min(r, G - 1) * EROW) + 8 * kq;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int h = 4 * kq + i;
@@ -388,14 +406,8 @@ __global__ __launch_bounds__(kBlock, 4) void k_attention(AttnArgs a, int cpw) { 
       lds_wait8(vv);
 #pragma unroll
       for (int c = 0; c < kChunk / 32; ++c) {
-        const float4 e0 = *reinterpret_cast<const float4*>(erow + 32 * c);
-        const float4 e1 = *reinterpret_cast<const float4*>(erow + 32 * c + 16);
-        h16x8 eh, el;
-        split_h8(e0, e1, eh, el);
-        if (!hv) {
-          eh = h16x8{};
-          el = h16x8{};
-        }
+        const h16x8 eh = *reinterpret_cast<const h16x8*>(erow + 32 * c);
+        const h16x8 el = *reinterpret_cast<const h16x8*>(erow + 64 + 32 * c);
         const h16x8 v0 = __builtin_bit_cast(h16x8, make_uint4(vv[4 * c].x, vv[4 * c].y, vv[4 * c + 1].x, vv[4 * c + 1].y));
         const h16x8 v1 = __builtin_bit_cast(h16x8, make_uint4(vv[4 * c + 2].x, vv[4 * c + 2].y, vv[4 * c + 3].x, vv[4 * c + 3].y));
         oe = mfma16(eh, v0, oe);
