@@ -65,6 +65,126 @@ def expert_traffic():
         return None
 
 
+def hip_runtime():
+    """The HIP runtime's stream, graph and event calls used by the config-1 leg."""
+    import ctypes as C
+
+    h = C.CDLL("libamdhip64.so")
+    P = C.c_void_p
+    for name, argt in [("hipStreamCreate", [C.POINTER(P)]), ("hipStreamDestroy", [P]),
+                       ("hipStreamBeginCapture", [P, C.c_int]),
+                       ("hipStreamEndCapture", [P, C.POINTER(P)]),
+                       ("hipGraphInstantiate", [C.POINTER(P), P, P, P, C.c_size_t]),
+                       ("hipGraphLaunch", [P, P]), ("hipStreamSynchronize", [P]),
+                       ("hipGraphExecDestroy", [P]), ("hipGraphDestroy", [P]),
+                       ("hipEventCreate", [C.POINTER(P)]), ("hipEventRecord", [P, P]),
+                       ("hipEventSynchronize", [P]), ("hipEventDestroy", [P]),
+                       ("hipEventElapsedTime", [C.POINTER(C.c_float), P, P]),
+                       ("hipMemcpy", [P, P, C.c_size_t, C.c_int])]:
+        getattr(h, name).argtypes = argt
+        getattr(h, name).restype = C.c_int
+    return h
+
+
+def moe_layer_leg(model: K.Model, cfg: K.ModelConfig, reps: int, cpu_threads: int) -> dict:
+    """MoE layer leg (config 1): one token through one MoE layer (RMSNorm of
+    weight 1, router, softmax/top-8, the 8 routed experts' Q4_K gate/up + SwiGLU
+    and down, the weighted sum in ascending expert order, the residual) by the
+    C ABI entry point knj_moe_decode_layer_noalloc.  One call per layer of the
+    model (its router and 128 experts each: 16.3 GB of experts in rotation, so
+    the 256 MB memory-side cache cannot serve a layer's weights again), x ~ N(0,1)
+    per layer, captured in one HIP graph; HIP events around `reps` replays on
+    the graph's stream.  With cpu_threads > 0, the oracle's Model::moe on layer
+    0's weights (copied to the host) is timed beside it on that many threads."""
+    import ctypes as C
+
+    H, F, E, k, L = cfg.n_embd, cfg.n_ff, cfg.n_expert, cfg.n_expert_used, cfg.n_layer
+    base = model.image_device()
+    ptr = lambda off: C.c_void_p(base + off)  # noqa: E731
+    rng = np.random.default_rng(1)
+    xs = [K.DeviceBuffer.from_array(rng.standard_normal(H).astype(np.float32)) for _ in range(L)]
+    ones = K.DeviceBuffer.from_array(np.ones(H, np.float32))
+    out = K.DeviceBuffer(4 * H)
+    logits = K.DeviceBuffer(4 * E)
+    ti = K.DeviceBuffer(4 * k)
+    tw = K.DeviceBuffer(4 * k)
+    los = [model.layer_offsets(il) for il in range(L)]
+    h = hip_runtime()
+    P = C.c_void_p
+    s, graph, exe, e0, e1 = P(), P(), P(), P(), P()
+    assert h.hipStreamCreate(C.byref(s)) == 0
+    try:
+        def layer(il):
+            lo = los[il]
+            K.moe_decode_layer_noalloc(xs[il], ptr(lo.router), ptr(lo.gate), ptr(lo.up), ptr(lo.down),
+                                       H, F, E, k, out, logits, ti, tw, norm_w=ones, eps=1e-6,
+                                       resid=xs[il], stream=s.value)
+        for il in range(L):  # eager pass: set-up outside the capture
+            layer(il)
+        assert h.hipStreamSynchronize(s) == 0
+        assert h.hipStreamBeginCapture(s, 2) == 0  # relaxed capture mode
+        for il in range(L):
+            layer(il)
+        assert h.hipStreamEndCapture(s, C.byref(graph)) == 0
+        assert h.hipGraphInstantiate(C.byref(exe), graph, None, None, 0) == 0
+        for _ in range(2):
+            assert h.hipGraphLaunch(exe, s) == 0
+        assert h.hipEventCreate(C.byref(e0)) == 0 and h.hipEventCreate(C.byref(e1)) == 0
+        assert h.hipEventRecord(e0, s) == 0
+        for _ in range(reps):
+            assert h.hipGraphLaunch(exe, s) == 0
+        assert h.hipEventRecord(e1, s) == 0
+        assert h.hipEventSynchronize(e1) == 0
+        ms = C.c_float()
+        assert h.hipEventElapsedTime(C.byref(ms), e0, e1) == 0
+    finally:
+        for ev in (e0, e1):
+            if ev.value:
+                h.hipEventDestroy(ev)
+        if exe.value:
+            h.hipGraphExecDestroy(exe)
+        if graph.value:
+            h.hipGraphDestroy(graph)
+        h.hipStreamSynchronize(s)
+        h.hipStreamDestroy(s)
+    us = ms.value * 1e3 / (reps * L)
+    # bytes per layer-token: router rows, the 8 experts' gate/up/down rows, x in, out
+    wbytes = 4 * H * E + k * (2 * K.row_bytes(cfg.type_gate_up, H) * F + K.row_bytes(cfg.type_down, F) * H)
+    nbytes = wbytes + 4 * H * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    log(f"config 1: one MoE layer, one token: {us:.2f} us per layer ({gbps:.0f} GB/s, "
+        f"{100 * gbps / HBM_PEAK_GBPS:.1f}% of HBM peak)")
+    cpu = None
+    if cpu_threads > 0:
+        import oracle as O  # the CPU baseline only (the checker's C restatement)
+
+        lo = los[0]
+        def host(off, n):
+            a = np.empty(n, np.uint8)
+            assert h.hipMemcpy(a.ctypes.data, base + off, n, 2) == 0  # device to host
+            return a
+        n_gu = E * F * K.row_bytes(cfg.type_gate_up, H)
+        router = host(lo.router, 4 * H * E).view(np.float32)
+        gate, up = host(lo.gate, n_gu), host(lo.up, n_gu)
+        down = host(lo.down, E * H * K.row_bytes(cfg.type_down, F))
+        x0 = xs[0].download(np.float32)
+        hx = (x0 / np.sqrt(np.mean(x0.astype(np.float64) ** 2) + 1e-6)).astype(np.float32)
+        O.moe(hx, router, gate, up, down, H, F, E, k, threads=cpu_threads)  # warm-up
+        best = float("inf")
+        for _ in range(10):
+            t0 = time.perf_counter()
+            O.moe(hx, router, gate, up, down, H, F, E, k, threads=cpu_threads)
+            best = min(best, time.perf_counter() - t0)
+        cpu = {"us_per_layer": round(best * 1e6, 1), "threads": cpu_threads, "kind": "port",
+               "sample": "best of 10 calls of the oracle's Model::moe, one token, layer 0"}
+        log(f"config 1 on the CPU oracle ({cpu_threads} threads): {best * 1e6:.0f} us per layer")
+    return {"workload": "config 1: one token through one MoE layer (router, softmax/top-8, 8 Q4_K "
+                        "experts' gate/up + SwiGLU + down, residual) by knj_moe_decode_layer_noalloc, "
+                        f"the model's {L} layers in rotation in one HIP graph",
+            "us_per_layer": round(us, 3), "bytes_per_layer": nbytes, "achieved_GBps": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "replays": reps, "cpu": cpu}
+
+
 def moe_batch_leg(model: K.Model, cfg: K.ModelConfig, m: int, iters: int) -> dict:
     """Batched MoE leg (config 2): one MoE layer (the model's layer 0: router, 128 Q4_K
     experts) over m tokens at once, x ~ N(0,1) with ffn_norm, timed with HIP
@@ -323,6 +443,8 @@ def main() -> int:
                     help="also run two streaming kernels of known traffic (a 256 MiB bf16 GEMV "
                          "read, a 256 MiB f32 dequant write) to scale rocprofv3 "
                          "FETCH_SIZE/WRITE_SIZE readings")
+    ap.add_argument("--no-moe-layer", dest="moe_layer", action="store_false",
+                    help="skip the config-1 leg (one MoE layer, one token)")
     ap.add_argument("--prefill-tokens", type=int, default=512,
                     help="tokens of the config-2 batched MoE layer leg (0 skips it)")
     ap.add_argument("--batch-seqs", type=int, default=32,
@@ -407,6 +529,10 @@ def main() -> int:
         share = min(args.cpu_share, len(os.sched_getaffinity(0)))
         cpu = cpu_baseline(model, cfg, sweep_cells(args.cpu_sweep, share), share)
 
+    moe_layer = None
+    if args.moe_layer:
+        share = 0 if args.no_cpu_baseline else min(args.cpu_share, len(os.sched_getaffinity(0)))
+        moe_layer = moe_layer_leg(model, cfg, 20, share)
     moe_batch = moe_batch_leg(model, cfg, args.prefill_tokens, 20) if args.prefill_tokens else None
     batched = None
     if args.batch_seqs and args.batch_ctx + args.batch_steps + 8 <= n_ctx:
@@ -452,6 +578,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "prompt_pass": {"tokens": int(args.ctx), "ms": round(prompt_s * 1e3, 2),
                         "tokens_per_s": round(args.ctx / prompt_s, 1)} if args.ctx else None,
+        "moe_layer": moe_layer,
         "moe_batch": moe_batch,
         "batched_decode": batched,
     }
